@@ -1,0 +1,166 @@
+/* q4nx_hip.h -- C ABI of libq4nx_hip.so, the MI355X (gfx950) decode hot path for
+ * q4nx-tiled weights: dequantisation, the q4 (W4A16 Q4_1) and q8 (W8A16) GEMVs, RMSNorm,
+ * RoPE, SwiGLU, the fused [q,k,v,RoPE] and [gate,up,SwiGLU] groups, GQA flash-decode
+ * attention, and the small decode-step helpers (embedding row, argmax).
+ *
+ * Conventions for every entry point:
+ *   - Device pointers are caller-owned and must stay valid until the stream work ends.
+ *   - Every call is asynchronous on `stream` (a hipStream_t; NULL = the null stream).
+ *   - bf16 values are passed as uint16_t bit patterns.
+ *   - Return 0 (Q4NX_OK) on success, a negative Q4NX_ERR_* on an argument error or launch
+ *     failure; q4nx_last_error() gives the message. Nothing throws across the ABI.
+ *   - Tiled weights are raw q4nx bytes, [n_tile_rows][k_tiles][tile], exactly as stored
+ *     in a .q4nx file (tools/q4nx.py:1-18): q4 tiles are 5120 B, q8 tiles 8704 B.
+ *   - Workspaces (`ws`) are laid out as Q4NX_WS_COUNTER_BYTES of arrival counters
+ *     followed by fp32 partial sums. They must be zero-filled once before their first
+ *     use; every call leaves the counters at zero again, whatever the shapes of the
+ *     calls that share the workspace. Calls that share a workspace must be ordered on
+ *     one stream. Any entry point's ws_bytes query includes the counter region.
+ *
+ * The reference interface each entry point replaces is cited beside it (paths relative
+ * to the reference repository).
+ */
+#ifndef Q4NX_HIP_H
+#define Q4NX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q4NX_ABI_VERSION 1
+
+#define Q4NX_OK 0
+#define Q4NX_ERR_ARG (-1)     /* null or misaligned pointer, bad enum            */
+#define Q4NX_ERR_SHAPE (-2)   /* K % 256, N % 32, Hq % Hkv, head_dim, batch ...  */
+#define Q4NX_ERR_WS (-3)      /* workspace missing or too small                  */
+#define Q4NX_ERR_LAUNCH (-4)  /* the HIP runtime refused the launch              */
+
+#define Q4NX_KIND_Q4 4
+#define Q4NX_KIND_Q8 8
+
+#define Q4NX_MAX_BATCH 8
+
+/* Size of the counter region at the start of every workspace (16384 counters). */
+#define Q4NX_WS_COUNTER_BYTES 65536
+
+int q4nx_abi_version(void);
+/* Message of the last error on this thread ("" if none). */
+const char *q4nx_last_error(void);
+
+/* ---------------------------------------------------------------- dequantisation
+ * Replaces tools/q4nx.py:97-111 (dequant_q4 / dequant_q8, bf16 out) and :127-149
+ * (_q4_tiles / _q8_tiles / _untile, fp32 out), and the on-core unpack
+ * designs/q4nx_unpack/q4nx_unpack.cc:40-92. Bit-exact: w = fp32(code*d + m) (q4) or
+ * code*s (q8), then RNE to bf16 when out_f32 == 0.
+ *   untile == 0: out is [n_tiles][8192] in weight-index order (i = rb*4096 + k*16 + r)
+ *   untile == 1: out is the [N][K] matrix, row = tr*32 + rb*16 + r, col = kt*256 + k */
+int q4nx_dequant_q4(const uint8_t *tiles, void *out, int n_tile_rows, int k_tiles,
+                    int out_f32, int untile, void *stream);
+int q4nx_dequant_q8(const uint8_t *tiles, void *out, int n_tile_rows, int k_tiles,
+                    int out_f32, int untile, void *stream);
+
+/* ---------------------------------------------------------------- GEMV
+ * y[b][n] = residual[b][n] + sum_k W[n][k] * x[b][k], fp32 accumulate, b < batch <= 8.
+ * Replaces the per-core kernels designs/granite_gemv/granite_gemv.h:109-300
+ * (granite_gemv_p{P}b{B}_k{N}(tiles, x, y)) and designs/lm_head/lm_head.h:53-113
+ * (lmhead_q8_k{N}(tiles, x, y)), with the whole tensor in one launch.
+ *   w: tile bytes, 16-byte aligned; x: bf16 [batch][x_stride]; y: fp32 [batch][y_stride];
+ *   residual: fp32 [batch][y_stride] or NULL. K = 256*k_tiles, N = 32*n_tile_rows.
+ *   ws: workspace of at least q4nx_gemv_ws_bytes(...) bytes (may be NULL when that is 0). */
+size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch);
+int q4nx_gemv_q4(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
+                 int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
+                 const float *residual, void *ws, size_t ws_bytes, void *stream);
+int q4nx_gemv_q8(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
+                 int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
+                 const float *residual, void *ws, size_t ws_bytes, void *stream);
+
+/* Tuning knob: tiles of K per workgroup (1..8), 0 = automatic. Process-wide. */
+int q4nx_set_split_tiles(int tiles_per_workgroup);
+
+/* ---------------------------------------------------------------- elementwise
+ * RMSNorm y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, bf16 out (+ optional fp32
+ * pre-rounding copy). Replaces designs/granite_gemv/granite_rmsnorm.h:82-87
+ * (granite_rms_norm(x, w, y, cols)). x is bf16 (x_f32 == 0) or fp32 (x_f32 == 1),
+ * [batch][cols]; cols % 2 == 0. */
+int q4nx_rmsnorm(const void *x, int x_f32, const uint16_t *w, uint16_t *y,
+                 float *y_f32, int cols, int batch, float eps, void *stream);
+
+/* Half-split RoPE (rotate_half) on [batch][n_heads][head_dim] bf16 with the fp32
+ * cos/sin table tab[pos][2][head_dim/2] built by q4nx_rope_table_host. Replaces
+ * designs/granite_gemv/granite_elementwise.h:111-114 (granite_rope(x, cs, y, n_heads));
+ * the per-position cos/sin come from the table instead of the caller. */
+int q4nx_rope(const uint16_t *x, uint16_t *y, float *y_f32, int n_heads, int head_dim,
+              int batch, const int32_t *positions, const float *tab, int max_pos,
+              void *stream);
+
+/* Host-side (no GPU): fp32 cos/sin table of pos * theta^(-2i/head_dim), computed in
+ * float64 and rounded once, layout [max_pos][2][head_dim/2]. */
+int q4nx_rope_table_host(float *tab, int max_pos, int head_dim, double theta);
+
+/* y = bf16(silu(g) * u). g, u bf16 (in_f32 == 0) or fp32 GEMV accumulators narrowed to
+ * bf16 first (in_f32 == 1). Replaces designs/granite_gemv/granite_elementwise.h:115-118
+ * (granite_swiglu) and granite_swiglu_f32.h:132-137 (granite_swiglu_f32). */
+int q4nx_swiglu(const void *g, const void *u, int in_f32, uint16_t *y, float *y_f32,
+                int n, int batch, void *stream);
+
+/* ---------------------------------------------------------------- fused groups
+ * [q, k, v, RoPE] in one launch: q|k|v GEMVs over the same input, the q/k accumulators
+ * narrowed to bf16 and rotated, v narrowed; q goes to q_out [batch][n_q*64], k and v
+ * are written into the caches at positions[b]. Replaces the fused design
+ * designs/granite_gemv/granite_qkv.py:50-128 with its epilogue granite_qkv_rope.h:74-78.
+ * Input: bf16 x [batch][x_stride], or, when norm_w != NULL, the fp32 residual h
+ * [batch][x_stride] normalised in the prologue (RMSNorm with norm_w, eps).
+ * Cache layout: k_cache[b][kv_head][l][64] with strides (kv_b_stride, kv_h_stride) in
+ * elements; l < max_pos. raw_out (optional): fp32 [batch][(n_q+2*n_kv)*64] GEMV outputs
+ * before narrowing. xn_out (optional): bf16 [batch][K] normalised input. */
+size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch);
+int q4nx_qkv_rope(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, int n_q_heads,
+                  int n_kv_heads, int k_tiles, const void *x, int64_t x_stride,
+                  const uint16_t *norm_w, float eps, int batch, const int32_t *positions,
+                  const float *rope_tab, int max_pos, uint16_t *q_out, uint16_t *k_cache,
+                  uint16_t *v_cache, int64_t kv_b_stride, int64_t kv_h_stride,
+                  float *raw_out, uint16_t *xn_out, void *ws, size_t ws_bytes, void *stream);
+
+/* [gate, up, SwiGLU] in one launch: h[b][n] = bf16(silu(bf16(gate.x)) * bf16(up.x)).
+ * Replaces designs/granite_gemv/granite_mlp.py:48-133 with granite_swiglu_f32.h. Input
+ * as q4nx_qkv_rope (bf16 x, or fp32 residual + norm_w). raw_out (optional): fp32
+ * [batch][2*N] gate|up accumulators; xn_out (optional) as above. */
+size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch);
+int q4nx_gate_up_swiglu(const uint8_t *wg, const uint8_t *wu, int n_tile_rows,
+                        int k_tiles, const void *x, int64_t x_stride,
+                        const uint16_t *norm_w, float eps, int batch, uint16_t *h_out,
+                        int64_t h_stride, float *raw_out, uint16_t *xn_out, void *ws,
+                        size_t ws_bytes, void *stream);
+
+/* ---------------------------------------------------------------- attention
+ * GQA flash-decode: one query token per sequence, out[b][h] = softmax(scale * K q) V
+ * over positions [0, lens[b]) of the caches, q head h reading kv head h / (Hq/Hkv).
+ * Split-K over the KV length with an exact (m, l, acc) combine. Replaces
+ * designs/granite_gemv/granite_attention.h:221-237 (granite_attn_block /
+ * granite_attn_finish). head_dim must be 64. q: bf16 [B][Hq][64]; out: bf16 and/or fp32
+ * [B][Hq][64]; caches as in q4nx_qkv_rope. n_split = 0 chooses automatically. */
+size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len);
+int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                    uint16_t *out, float *out_f32, int batch, int n_q_heads,
+                    int n_kv_heads, int head_dim, const int32_t *lens, int max_len,
+                    int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
+                    void *ws, size_t ws_bytes, void *stream);
+
+/* ---------------------------------------------------------------- decode-step helpers
+ * h[b][:] = fp32 row tokens[b] of a q8-tiled [vocab][hidden] matrix (a tied lm_head
+ * used as the embedding table). No reference counterpart: the reference has no token
+ * loop (README.md:295-311). */
+int q4nx_embed_q8(const uint8_t *w, const int32_t *tokens, float *h, int vocab,
+                  int hidden, int batch, void *stream);
+/* idx[b] = argmax_n logits[b][n] (first maximum), max[b] its value (optional). */
+int q4nx_argmax(const float *logits, int n, int batch, int64_t stride, int32_t *idx,
+                float *max_val, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q4NX_HIP_H */

@@ -1,0 +1,239 @@
+// RMSNorm, RoPE, SwiGLU and the decode-step helpers (embedding row, argmax) for gfx950.
+//
+// RMSNorm  designs/granite_gemv/granite_rmsnorm.h:45-87   y = x * rsqrt(mean(x^2)+eps) * w
+// RoPE     designs/granite_gemv/granite_elementwise.h:40-75  half-split rotate_half
+// SwiGLU   designs/granite_gemv/granite_elementwise.h:77-108, granite_swiglu_f32.h:27-58
+// All math is fp32; bf16 outputs are rounded once, RNE, and an optional fp32 copy of the
+// pre-rounding value is written for parity checks.
+
+#include <math.h>
+
+#include "common.h"
+
+namespace q4nx {
+
+// ------------------------------------------------------------------ RMSNorm
+template <bool XF32>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const void* __restrict__ x,
+                                                      const uint16_t* __restrict__ w,
+                                                      uint16_t* __restrict__ y,
+                                                      float* __restrict__ y_f32, int cols,
+                                                      float eps) {
+  __shared__ float part[4];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* xf = XF32 ? (const float*)x + (size_t)b * cols : nullptr;
+  const uint16_t* xb = XF32 ? nullptr : (const uint16_t*)x + (size_t)b * cols;
+  float ss = 0.f;
+  for (int c = tid; c < cols; c += 256) {
+    const float v = XF32 ? xf[c] : bf16_to_f32(xb[c]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float inv = 1.0f / sqrtf(tot / (float)cols + eps);
+  for (int c = tid; c < cols; c += 256) {
+    const float v = XF32 ? xf[c] : bf16_to_f32(xb[c]);
+    const float o = (v * inv) * bf16_to_f32(w[c]);
+    y[(size_t)b * cols + c] = f32_to_bf16(o);
+    if (y_f32) y_f32[(size_t)b * cols + c] = o;
+  }
+}
+
+// ------------------------------------------------------------------ RoPE
+__global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ x,
+                                                   uint16_t* __restrict__ y,
+                                                   float* __restrict__ y_f32, int n_heads,
+                                                   int hd, int batch,
+                                                   const int32_t* __restrict__ pos,
+                                                   const float* __restrict__ tab, int max_pos) {
+  const int half = hd >> 1;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, h, d<half)
+  const int64_t total = (int64_t)batch * n_heads * half;
+  if (i >= total) return;
+  const int d = (int)(i % half);
+  const int64_t bh = i / half;
+  const int b = (int)(bh / n_heads);
+  const int p = pos[b];
+  const int64_t base = bh * hd;
+  const float x0 = bf16_to_f32(x[base + d]);
+  const float x1 = bf16_to_f32(x[base + half + d]);
+  float y0, y1;
+  if (p >= 0 && p < max_pos) {
+    const float c = tab[(int64_t)p * hd + d];
+    const float s = tab[(int64_t)p * hd + half + d];
+    y0 = fmaf(x0, c, -(x1 * s));
+    y1 = fmaf(x1, c, x0 * s);
+  } else {
+    y0 = y1 = __builtin_nanf("");
+  }
+  y[base + d] = f32_to_bf16(y0);
+  y[base + half + d] = f32_to_bf16(y1);
+  if (y_f32) {
+    y_f32[base + d] = y0;
+    y_f32[base + half + d] = y1;
+  }
+}
+
+// ------------------------------------------------------------------ SwiGLU
+template <bool INF32>
+__global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ g,
+                                                     const void* __restrict__ u,
+                                                     uint16_t* __restrict__ y,
+                                                     float* __restrict__ y_f32, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float gv, uv;
+  if (INF32) {  // fp32 accumulators are narrowed to bf16 first (granite_swiglu_f32.h:38-41)
+    gv = bf16_to_f32(f32_to_bf16(((const float*)g)[i]));
+    uv = bf16_to_f32(f32_to_bf16(((const float*)u)[i]));
+  } else {
+    gv = bf16_to_f32(((const uint16_t*)g)[i]);
+    uv = bf16_to_f32(((const uint16_t*)u)[i]);
+  }
+  const float h = (gv / (1.0f + expf(-gv))) * uv;
+  y[i] = f32_to_bf16(h);
+  if (y_f32) y_f32[i] = h;
+}
+
+// ------------------------------------------------------------------ embedding row of a q8 matrix
+__global__ __launch_bounds__(256) void embed_q8_kernel(const uint8_t* __restrict__ w,
+                                                       const int32_t* __restrict__ tokens,
+                                                       float* __restrict__ h, int vocab,
+                                                       int hidden) {
+  const int b = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= hidden) return;
+  const int t = tokens[b];
+  if (t < 0 || t >= vocab) {
+    h[(size_t)b * hidden + c] = __builtin_nanf("");
+    return;
+  }
+  const int k_t = hidden / 256;
+  const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
+  const int kt = c >> 8, k = c & 255, kb = k >> 5;
+  const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
+  const int g = kb * 32 + rb * 16 + r;
+  const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
+  const int code = (int)(int8_t)tile[kMetaBytes + rb * 4096 + k * 16 + r];
+  h[(size_t)b * hidden + c] = (float)code * bf16_to_f32(s);
+}
+
+// ------------------------------------------------------------------ argmax
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  // numpy semantics: the first NaN wins, otherwise the first maximum
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int n,
+                                                      int64_t stride, int32_t* __restrict__ idx,
+                                                      float* __restrict__ max_val) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int b = blockIdx.x;
+  const float* row = x + (size_t)b * stride;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    const float v = row[i];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    idx[b] = bi;
+    if (max_val) max_val[b] = bv;
+  }
+}
+
+}  // namespace q4nx
+
+using namespace q4nx;
+
+extern "C" {
+
+int q4nx_rmsnorm(const void* x, int x_f32, const uint16_t* w, uint16_t* y, float* y_f32,
+                 int cols, int batch, float eps, void* stream) {
+  Q4NX_REQUIRE(x && w && y, Q4NX_ERR_ARG, "q4nx_rmsnorm: x, w and y are required");
+  Q4NX_REQUIRE(cols > 0 && batch > 0, Q4NX_ERR_SHAPE, "q4nx_rmsnorm: cols=%d batch=%d", cols,
+               batch);
+  hipStream_t s = (hipStream_t)stream;
+  if (x_f32)
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(batch), dim3(256), 0, s, x, w, y, y_f32, cols, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(batch), dim3(256), 0, s, x, w, y, y_f32, cols, eps);
+  return check_launch("q4nx_rmsnorm");
+}
+
+int q4nx_rope(const uint16_t* x, uint16_t* y, float* y_f32, int n_heads, int head_dim, int batch,
+              const int32_t* positions, const float* tab, int max_pos, void* stream) {
+  Q4NX_REQUIRE(x && y && positions && tab, Q4NX_ERR_ARG,
+               "q4nx_rope: x, y, positions and table are required");
+  Q4NX_REQUIRE(n_heads > 0 && batch > 0 && head_dim > 0 && head_dim % 2 == 0 && max_pos > 0,
+               Q4NX_ERR_SHAPE, "q4nx_rope: n_heads=%d head_dim=%d batch=%d max_pos=%d", n_heads,
+               head_dim, batch, max_pos);
+  const int64_t total = (int64_t)batch * n_heads * (head_dim / 2);
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, y, y_f32, n_heads, head_dim, batch, positions, tab,
+                     max_pos);
+  return check_launch("q4nx_rope");
+}
+
+int q4nx_swiglu(const void* g, const void* u, int in_f32, uint16_t* y, float* y_f32, int n,
+                int batch, void* stream) {
+  Q4NX_REQUIRE(g && u && y, Q4NX_ERR_ARG, "q4nx_swiglu: g, u and y are required");
+  Q4NX_REQUIRE(n > 0 && batch > 0, Q4NX_ERR_SHAPE, "q4nx_swiglu: n=%d batch=%d", n, batch);
+  const int64_t total = (int64_t)n * batch;
+  dim3 grid((unsigned)((total + 255) / 256));
+  if (in_f32)
+    hipLaunchKernelGGL(swiglu_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, g, u, y, y_f32, total);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, g, u, y, y_f32, total);
+  return check_launch("q4nx_swiglu");
+}
+
+int q4nx_embed_q8(const uint8_t* w, const int32_t* tokens, float* h, int vocab, int hidden,
+                  int batch, void* stream) {
+  Q4NX_REQUIRE(w && tokens && h, Q4NX_ERR_ARG, "q4nx_embed_q8: w, tokens and h are required");
+  Q4NX_REQUIRE(vocab > 0 && vocab % 32 == 0 && hidden > 0 && hidden % 256 == 0 && batch > 0,
+               Q4NX_ERR_SHAPE, "q4nx_embed_q8: vocab=%d hidden=%d batch=%d", vocab, hidden, batch);
+  hipLaunchKernelGGL(embed_q8_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0,
+                     (hipStream_t)stream, w, tokens, h, vocab, hidden);
+  return check_launch("q4nx_embed_q8");
+}
+
+int q4nx_argmax(const float* logits, int n, int batch, int64_t stride, int32_t* idx,
+                float* max_val, void* stream) {
+  Q4NX_REQUIRE(logits && idx, Q4NX_ERR_ARG, "q4nx_argmax: logits and idx are required");
+  Q4NX_REQUIRE(n > 0 && batch > 0 && stride >= n, Q4NX_ERR_SHAPE,
+               "q4nx_argmax: n=%d batch=%d stride=%lld", n, batch, (long long)stride);
+  hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(1024), 0, (hipStream_t)stream, logits, n,
+                     stride, idx, max_val);
+  return check_launch("q4nx_argmax");
+}
+
+}  // extern "C"

@@ -1,0 +1,285 @@
+"""Torch-facing wrappers over the C ABI. PyTorch supplies device memory and the stream;
+all arithmetic runs in libq4nx_hip.so.
+
+Tensor conventions: tile bytes are torch.uint8 (raw q4nx bytes), bf16 values are
+torch.bfloat16 (bit-identical to the uint16 patterns of the C ABI), positions/lengths are
+torch.int32. Every tensor must live on the current CUDA (HIP) device.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from .q4nx import Q4_TILE_BYTES, Q8_TILE_BYTES, Q4NXFormatError
+
+KIND = {"q4": 4, "q8": 8}
+WS_COUNTER_BYTES = 65536   # Q4NX_WS_COUNTER_BYTES
+TILE_BYTES = {"q4": Q4_TILE_BYTES, "q8": Q8_TILE_BYTES}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor, got {t.device}")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+class Workspace:
+    """Zero-filled device scratch shared by the split-K launches on one stream.
+
+    Kernels that use it leave its counters at zero, so it is zeroed only on (re)allocation.
+    """
+
+    def __init__(self, nbytes: int = 0, device=None):
+        self.device = torch.device(device or "cuda")
+        self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+
+    def get(self, nbytes: int) -> tuple[int, int]:
+        if nbytes > self.buf.numel():
+            self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        return self.buf.data_ptr(), self.buf.numel()
+
+
+_default_ws: dict = {}
+
+
+def default_workspace() -> Workspace:
+    d = torch.cuda.current_device()
+    if d not in _default_ws:
+        _default_ws[d] = Workspace(1 << 20, device=f"cuda:{d}")
+    return _default_ws[d]
+
+
+def _tiles(w: torch.Tensor, kind: str, n_tile_rows: int, k_tiles: int, name="w") -> None:
+    _dev(w, name, torch.uint8)
+    want = n_tile_rows * k_tiles * TILE_BYTES[kind]
+    if w.numel() != want:
+        raise Q4NXFormatError(f"{name}: {w.numel()} bytes, expected {want} for "
+                              f"{n_tile_rows}x{k_tiles} {kind} tiles")
+
+
+# ---------------------------------------------------------------- dequantisation
+
+def dequant(tiles: torch.Tensor, kind: str, n_tile_rows: int, k_tiles: int,
+            out_dtype=torch.bfloat16, untile: bool = False) -> torch.Tensor:
+    """Dequantise q4nx tiles on the GPU. out_dtype bfloat16 = `dequant_q4/q8`
+    (tools/q4nx.py:97-111); float32 = `_q4_tiles/_q8_tiles` (:127-143). untile=True returns
+    the [N, K] matrix (`_untile`, :146-149), else [n_tiles, 8192] in weight-index order."""
+    _tiles(tiles, kind, n_tile_rows, k_tiles, "tiles")
+    shape = (n_tile_rows * 32, k_tiles * 256) if untile else (n_tile_rows * k_tiles, 8192)
+    out = torch.empty(shape, dtype=out_dtype, device=tiles.device)
+    f32 = 1 if out_dtype == torch.float32 else 0
+    if not f32 and out_dtype != torch.bfloat16:
+        raise TypeError("out_dtype must be bfloat16 or float32")
+    _lib.call(f"q4nx_dequant_{kind}", _ptr(tiles), _ptr(out), n_tile_rows, k_tiles, f32,
+              int(untile), _stream())
+    return out
+
+
+# ---------------------------------------------------------------- GEMV
+
+def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
+         residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+         ws: Workspace | None = None) -> torch.Tensor:
+    """y = residual + W @ x, fp32. x: bf16 [K] or [B, K] (B <= 8). Returns [N] or [B, N]."""
+    _tiles(tiles, kind, n_tile_rows, k_tiles)
+    _dev(x, "x", torch.bfloat16)
+    squeeze = x.dim() == 1
+    x2 = x.reshape(1, -1) if squeeze else x
+    b, k = x2.shape
+    if k != k_tiles * 256:
+        raise Q4NXFormatError(f"x has K={k}, tiles have K={k_tiles * 256}")
+    n = n_tile_rows * 32
+    if out is None:
+        out = torch.empty((b, n), dtype=torch.float32, device=x.device)
+    _dev(out, "out", torch.float32)
+    if residual is not None:
+        _dev(residual, "residual", torch.float32)
+        if residual.numel() != b * n:
+            raise ValueError("residual must have the shape of the output")
+    ws = ws or default_workspace()
+    wp, wn = ws.get(_lib.lib().q4nx_gemv_ws_bytes(KIND[kind], n_tile_rows, k_tiles, b))
+    _lib.call(f"q4nx_gemv_{kind}", _ptr(tiles), _ptr(x2), _ptr(out), n_tile_rows, k_tiles, b,
+              k, n, _ptr(residual), wp, wn, _stream())
+    return out.reshape(n) if squeeze else out
+
+
+def set_split_tiles(tiles_per_workgroup: int) -> None:
+    """Tuning: K-tiles per workgroup for all GEMVs (0 = automatic)."""
+    _lib.call("q4nx_set_split_tiles", int(tiles_per_workgroup))
+
+
+# ---------------------------------------------------------------- elementwise
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5,
+            want_f32: bool = False):
+    """bf16 RMSNorm of x (bf16 or fp32, [C] or [B, C]); returns y or (y, y_f32)."""
+    _dev(x, "x")
+    _dev(w, "w", torch.bfloat16)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("x must be bfloat16 or float32")
+    cols = x.shape[-1]
+    b = x.numel() // cols
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    yf = torch.empty(x.shape, dtype=torch.float32, device=x.device) if want_f32 else None
+    _lib.call("q4nx_rmsnorm", _ptr(x), int(x.dtype == torch.float32), _ptr(w), _ptr(y),
+              _ptr(yf), cols, b, float(eps), _stream())
+    return (y, yf) if want_f32 else y
+
+
+def rope_table(max_pos: int, head_dim: int = 64, theta: float = 10000.0,
+               device="cuda") -> torch.Tensor:
+    """fp32 [max_pos, 2, head_dim/2] cos/sin table, float64 angles rounded once (host)."""
+    tab = np.empty((max_pos, 2, head_dim // 2), np.float32)
+    _lib.call("q4nx_rope_table_host", tab.ctypes.data, max_pos, head_dim, float(theta))
+    return torch.from_numpy(tab).to(device)
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, table: torch.Tensor, want_f32: bool = False):
+    """Half-split RoPE on bf16 x [B, H, D] with per-sequence positions [B]."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(positions, "positions", torch.int32)
+    _dev(table, "table", torch.float32)
+    b, h, d = x.shape
+    if positions.numel() != b:
+        raise ValueError("one position per sequence")
+    y = torch.empty_like(x)
+    yf = torch.empty(x.shape, dtype=torch.float32, device=x.device) if want_f32 else None
+    _lib.call("q4nx_rope", _ptr(x), _ptr(y), _ptr(yf), h, d, b, _ptr(positions), _ptr(table),
+              table.shape[0], _stream())
+    return (y, yf) if want_f32 else y
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor, want_f32: bool = False):
+    """bf16(silu(g) * u); fp32 g/u are narrowed to bf16 first."""
+    _dev(g, "g")
+    _dev(u, "u")
+    if g.shape != u.shape or g.dtype != u.dtype:
+        raise ValueError("g and u must match")
+    n = g.shape[-1]
+    b = g.numel() // n
+    y = torch.empty(g.shape, dtype=torch.bfloat16, device=g.device)
+    yf = torch.empty(g.shape, dtype=torch.float32, device=g.device) if want_f32 else None
+    _lib.call("q4nx_swiglu", _ptr(g), _ptr(u), int(g.dtype == torch.float32), _ptr(y), _ptr(yf),
+              n, b, _stream())
+    return (y, yf) if want_f32 else y
+
+
+# ---------------------------------------------------------------- fused groups
+
+def qkv_rope(wq, wk, wv, n_q_heads: int, n_kv_heads: int, k_tiles: int, x: torch.Tensor,
+             positions: torch.Tensor, table: torch.Tensor, k_cache: torch.Tensor,
+             v_cache: torch.Tensor, q_out: torch.Tensor | None = None,
+             norm_w: torch.Tensor | None = None, eps: float = 1e-5, raw_out=None, xn_out=None,
+             ws: Workspace | None = None) -> torch.Tensor:
+    """[q,k,v,RoPE] in one launch. x: bf16 [B, K], or fp32 residual [B, K] with norm_w.
+    Caches: bf16 [B, Hkv, Lmax, 64]. Returns q_out bf16 [B, Hq*64]."""
+    for t, n, kk in ((wq, "wq", n_q_heads), (wk, "wk", n_kv_heads), (wv, "wv", n_kv_heads)):
+        _tiles(t, "q4", kk * 2, k_tiles, n)
+    _dev(x, "x", torch.float32 if norm_w is not None else torch.bfloat16)
+    b = x.shape[0]
+    _dev(positions, "positions", torch.int32)
+    _dev(k_cache, "k_cache", torch.bfloat16)
+    _dev(v_cache, "v_cache", torch.bfloat16)
+    if k_cache.shape != v_cache.shape or k_cache.shape[0] < b or k_cache.shape[1] != n_kv_heads \
+            or k_cache.shape[3] != 64:
+        raise ValueError("caches must be [B, Hkv, Lmax, 64]")
+    if q_out is None:
+        q_out = torch.empty((b, n_q_heads * 64), dtype=torch.bfloat16, device=x.device)
+    if norm_w is not None:
+        _dev(norm_w, "norm_w", torch.bfloat16)
+    ws = ws or default_workspace()
+    wp, wn = ws.get(_lib.lib().q4nx_qkv_rope_ws_bytes(n_q_heads, n_kv_heads, k_tiles, b))
+    lmax = k_cache.shape[2]
+    _lib.call("q4nx_qkv_rope", _ptr(wq), _ptr(wk), _ptr(wv), n_q_heads, n_kv_heads, k_tiles,
+              _ptr(x), x.shape[1], _ptr(norm_w), float(eps), b, _ptr(positions), _ptr(table),
+              table.shape[0] if table.shape[0] < lmax else lmax, _ptr(q_out), _ptr(k_cache),
+              _ptr(v_cache), k_cache.stride(0), k_cache.stride(1), _ptr(raw_out), _ptr(xn_out),
+              wp, wn, _stream())
+    return q_out
+
+
+def gate_up_swiglu(wg, wu, n_tile_rows: int, k_tiles: int, x: torch.Tensor,
+                   h_out: torch.Tensor | None = None, norm_w: torch.Tensor | None = None,
+                   eps: float = 1e-5, raw_out=None, xn_out=None,
+                   ws: Workspace | None = None) -> torch.Tensor:
+    """[gate, up, SwiGLU] in one launch; returns bf16 h [B, N]."""
+    _tiles(wg, "q4", n_tile_rows, k_tiles, "wg")
+    _tiles(wu, "q4", n_tile_rows, k_tiles, "wu")
+    _dev(x, "x", torch.float32 if norm_w is not None else torch.bfloat16)
+    b = x.shape[0]
+    n = n_tile_rows * 32
+    if h_out is None:
+        h_out = torch.empty((b, n), dtype=torch.bfloat16, device=x.device)
+    ws = ws or default_workspace()
+    wp, wn = ws.get(_lib.lib().q4nx_gate_up_ws_bytes(n_tile_rows, k_tiles, b))
+    _lib.call("q4nx_gate_up_swiglu", _ptr(wg), _ptr(wu), n_tile_rows, k_tiles, _ptr(x),
+              x.shape[1], _ptr(norm_w), float(eps), b, _ptr(h_out), h_out.stride(0),
+              _ptr(raw_out), _ptr(xn_out), wp, wn, _stream())
+    return h_out
+
+
+# ---------------------------------------------------------------- attention
+
+def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+               lens: torch.Tensor, scale: float = 0.125, max_len: int | None = None,
+               n_split: int = 0, out: torch.Tensor | None = None, want_f32: bool = False,
+               ws: Workspace | None = None):
+    """GQA flash-decode. q: bf16 [B, Hq, 64]; caches bf16 [B, Hkv, Lmax, 64]; lens int32 [B].
+    Returns bf16 [B, Hq, 64] (and the fp32 copy when want_f32)."""
+    _dev(q, "q", torch.bfloat16)
+    _dev(lens, "lens", torch.int32)
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.stride(3) != 1 or t.stride(2) != 64:
+            raise ValueError(f"{n} must be a bf16 device tensor [B, Hkv, Lmax, 64] with "
+                             f"contiguous rows")
+    b, hq, d = q.shape
+    hkv, lmax = k_cache.shape[1], k_cache.shape[2]
+    max_len = lmax if max_len is None else min(max_len, lmax)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+    of = torch.empty((b, hq, d), dtype=torch.float32, device=q.device) if want_f32 else None
+    ws = ws or default_workspace()
+    need = _lib.lib().q4nx_gqa_decode_ws_bytes(b, hq, hkv, max_len)
+    if n_split:
+        need = max(need, WS_COUNTER_BYTES + b * hkv * n_split * (hq // hkv) * 66 * 4)
+    wp, wn = ws.get(need)
+    _lib.call("q4nx_gqa_decode", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(of), b,
+              hq, hkv, d, _ptr(lens), max_len, k_cache.stride(0), k_cache.stride(1),
+              float(scale), int(n_split), wp, wn, _stream())
+    return (out, of) if want_f32 else out
+
+
+# ---------------------------------------------------------------- decode helpers
+
+def embed_q8(tiles: torch.Tensor, tokens: torch.Tensor, vocab: int, hidden: int,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    _tiles(tiles, "q8", vocab // 32, hidden // 256, "tiles")
+    _dev(tokens, "tokens", torch.int32)
+    b = tokens.numel()
+    if out is None:
+        out = torch.empty((b, hidden), dtype=torch.float32, device=tiles.device)
+    _lib.call("q4nx_embed_q8", _ptr(tiles), _ptr(tokens), _ptr(out), vocab, hidden, b, _stream())
+    return out
+
+
+def argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(logits, "logits", torch.float32)
+    l2 = logits.reshape(-1, logits.shape[-1])
+    b, n = l2.shape
+    if out is None:
+        out = torch.empty(b, dtype=torch.int32, device=logits.device)
+    _lib.call("q4nx_argmax", _ptr(l2), n, b, n, _ptr(out), None, _stream())
+    return out

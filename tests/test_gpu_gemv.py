@@ -1,0 +1,151 @@
+"""GPU parity of dequantisation and the q4/q8 GEMV against the oracle.
+
+Bars: dequant bit-exact; GEMV max|Δ|/max|ref| < 1e-5 against the float64 oracle with
+cosine > 0.9999999 (the reference's own GEMV gate, designs/granite_gemv/granite_gemv.py:335);
+one-hot activations reproduce a dequantised column exactly (README.md:188-190).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from llmnputest_amd import ops, synth
+from oracle import q4nx_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+COS = 0.9999999
+
+
+def _tiles(kind, n, k, seed):
+    rng = np.random.default_rng(seed)
+    t = synth.q4_tiles(rng, n, k) if kind == "q4" else synth.q8_tiles(rng, n, k)
+    return t.reshape(-1, t.shape[-1]), rng
+
+
+def _dev_u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(dev)
+
+
+def _dev_bf16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("untile", [False, True])
+def test_dequant_bitexact(dev, kind, untile):
+    n, k = 96, 768
+    raw, _ = _tiles(kind, n, k, 1)
+    w = _dev_u8(raw, dev)
+    n_t, k_t = n // 32, k // 256
+    got16 = _bits(ops.dequant(w, kind, n_t, k_t, torch.bfloat16, untile))
+    got32 = ops.dequant(w, kind, n_t, k_t, torch.float32, untile).cpu().numpy()
+    f32 = qo.q4_tiles_f32(raw) if kind == "q4" else qo.q8_tiles_f32(raw)
+    if untile:
+        f32 = qo.untile(f32, n_t, k_t)
+    assert np.array_equal(got32.view(np.uint32), f32.view(np.uint32))
+    assert np.array_equal(got16, qo.bf16_round(f32))
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+def test_onehot_exact(dev, kind):
+    n, k = 64, 1024
+    raw, _ = _tiles(kind, n, k, 2)
+    w = _dev_u8(raw, dev)
+    wm = qo.dequant_matrix(raw, kind, n // 32, k // 256)
+    for kk in (0, 1, 31, 32, 255, 256, 511, 777, 1023):
+        x = np.zeros(k, np.float32)
+        x[kk] = 1.0
+        y = ops.gemv(w, kind, _dev_bf16(qo.bf16_round(x), dev), n // 32, k // 256).cpu().numpy()
+        assert np.array_equal(y.view(np.uint32), wm[:, kk].view(np.uint32)), kk
+
+
+@pytest.mark.parametrize("kind,n,k", [
+    ("q4", 8192, 2560),   # gate/up
+    ("q4", 2560, 8192),   # down
+    ("q4", 2560, 2560),   # q/o
+    ("q4", 512, 2560),    # k/v
+    ("q8", 4096, 1024),
+    ("q8", 2048, 2560),
+])
+def test_gemv_parity(dev, kind, n, k):
+    raw, rng = _tiles(kind, n, k, 3)
+    x = synth.random_bf16(rng, k)
+    y = ops.gemv(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    rel, cos = qo.metrics(y, ref)
+    assert rel < REL and cos > COS, (rel, cos)
+
+
+def test_gemv_q8_lm_head_full(dev):
+    """Config: y[248320] = W[248320, 1024] @ x, q8 tiles."""
+    n, k = 248320, 1024
+    raw, rng = _tiles("q8", n, k, 4)
+    x = synth.random_bf16(rng, k)
+    y = ops.gemv(_dev_u8(raw, dev), "q8", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, "q8", x, n // 32, k // 256, acc=np.float64, chunk=1024)
+    rel, cos = qo.metrics(y, ref)
+    assert rel < REL and cos > COS, (rel, cos)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("batch", [2, 3, 5, 8])
+def test_gemv_batch(dev, kind, batch):
+    n, k = 1024, 2560
+    raw, rng = _tiles(kind, n, k, 5)
+    x = synth.random_bf16(rng, (batch, k))
+    y = ops.gemv(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    for b in range(batch):
+        rel, cos = qo.metrics(y[b], ref[b])
+        assert rel < REL and cos > COS, (b, rel, cos)
+
+
+@pytest.mark.parametrize("tiles_per_wg", [1, 2, 3, 5, 7, 8])
+def test_gemv_split_variants(dev, tiles_per_wg):
+    n, k = 512, 8192
+    raw, rng = _tiles("q4", n, k, 6)
+    x = synth.random_bf16(rng, k)
+    w, xd = _dev_u8(raw, dev), _dev_bf16(x, dev)
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    ops.set_split_tiles(tiles_per_wg)
+    try:
+        y1 = ops.gemv(w, "q4", xd, n // 32, k // 256).cpu().numpy()
+        y2 = ops.gemv(w, "q4", xd, n // 32, k // 256).cpu().numpy()
+    finally:
+        ops.set_split_tiles(0)
+    rel, cos = qo.metrics(y1, ref)
+    assert rel < REL and cos > COS, (rel, cos)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))  # deterministic
+
+
+def test_gemv_residual_and_ones(dev):
+    n, k = 2560, 2560
+    raw, rng = _tiles("q4", n, k, 7)
+    w = _dev_u8(raw, dev)
+    res = rng.standard_normal(n).astype(np.float32)
+    x = qo.bf16_round(np.ones(k, np.float32))
+    y = ops.gemv(w, "q4", _dev_bf16(x, dev), n // 32, k // 256,
+                 residual=torch.from_numpy(res).to(dev).reshape(1, n)).cpu().numpy()
+    rowsum = qo.dequant_matrix(raw, "q4", n // 32, k // 256).astype(np.float64).sum(1)
+    rel, cos = qo.metrics(y - res, rowsum)
+    assert rel < REL and cos > COS
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 1e4, 1e30])
+def test_gemv_activation_range(dev, scale):
+    """The per-workgroup power-of-two fp16 scaling keeps any bf16 range exact."""
+    n, k = 256, 2560
+    raw, rng = _tiles("q4", n, k, 8)
+    xf = rng.standard_normal(k).astype(np.float32) * np.float32(scale)
+    xf[::97] *= np.float32(1e-6)   # a spread of magnitudes inside one vector
+    x = qo.bf16_round(xf)
+    y = ops.gemv(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    rel, cos = qo.metrics(y, ref)
+    assert rel < REL and cos > COS, (rel, cos)

@@ -1,0 +1,264 @@
+"""GPU parity of RMSNorm, RoPE, SwiGLU, the fused groups and GQA decode attention.
+
+fp32 outputs (the pre-rounding values) are held to max|Δ|/max|ref| < 1e-5 against the
+float64 oracle with cosine >= 0.9999; bf16 outputs are compared with the oracle rounded
+the same way and may differ only by rare 1-ulp flips where the fp32 value sits on a
+rounding boundary (see `assert_bf16_close`).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from llmnputest_amd import ops, synth
+from oracle import decode_oracle as do
+from oracle import q4nx_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+COS = 0.9999
+
+
+def bf16_dev(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def assert_close(got, ref, rel=REL, cos=COS):
+    r, c = qo.metrics(got, ref)
+    assert r < rel and c >= cos, (r, c)
+
+
+def assert_bf16_close(got_bits, ref_f64, max_frac=1e-3):
+    """bf16 outputs equal the oracle's RNE rounding except for rare 1-ulp boundary flips."""
+    want = qo.bf16_round(np.asarray(ref_f64, np.float64).astype(np.float32))
+    g = np.asarray(got_bits, np.uint16).ravel().astype(np.int32)
+    w = want.ravel().astype(np.int32)
+    diff = np.abs(g - w)
+    assert diff.max() <= 1, int(diff.max())
+    assert (diff > 0).mean() <= max_frac, float((diff > 0).mean())
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+@pytest.mark.parametrize("xdtype", ["bf16", "f32"])
+def test_rmsnorm(dev, xdtype):
+    rng = np.random.default_rng(10)
+    b, c = 3, 2560
+    w = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(c).astype(np.float32))
+    if xdtype == "bf16":
+        xb = synth.random_bf16(rng, (b, c))
+        x_host = qo.bf16_to_f32(xb)
+        x_dev = bf16_dev(xb, dev)
+    else:
+        x_host = (rng.standard_normal((b, c)) * 30).astype(np.float32)
+        x_dev = torch.from_numpy(x_host).to(dev)
+    y, yf = ops.rmsnorm(x_dev, bf16_dev(w, dev), 1e-5, want_f32=True)
+    ref = do.rmsnorm(x_host, w, 1e-5)
+    assert_close(yf.cpu().numpy(), ref)
+    assert_bf16_close(bits(y), ref)
+    # the weight is non-uniform, so dropping it would fail (granite_rmsnorm.py:132-134)
+    unit = do.rmsnorm(x_host, synth.f32_to_bf16_bits(np.ones(c, np.float32)), 1e-5)
+    assert qo.metrics(yf.cpu().numpy(), unit)[0] > 0.05
+
+
+# ------------------------------------------------------------------ RoPE
+
+def test_rope(dev):
+    rng = np.random.default_rng(11)
+    b, h = 8, 40
+    x = synth.random_bf16(rng, (b, h, 64))
+    pos = rng.integers(0, 4096, b).astype(np.int32)
+    tab_np = do.rope_table(4096, 64, 10000.0)
+    tab = ops.rope_table(4096, 64, 10000.0)
+    assert np.allclose(tab.cpu().numpy(), tab_np, rtol=0, atol=1e-7)
+    y, yf = ops.rope(bf16_dev(x, dev), torch.from_numpy(pos).to(dev), tab, want_f32=True)
+    ref = np.stack([do.rope(qo.bf16_to_f32(x[i]), pos[i], tab_np) for i in range(b)])
+    assert_close(yf.cpu().numpy(), ref)
+    assert_bf16_close(bits(y), ref)
+    alt = np.stack([do.rope_interleaved(qo.bf16_to_f32(x[i]), pos[i], tab_np) for i in range(b)])
+    assert qo.metrics(yf.cpu().numpy(), alt)[0] > 0.1     # granite_elementwise.py:153-162
+    y0 = ops.rope(bf16_dev(x, dev), torch.zeros(b, dtype=torch.int32, device=dev), tab)
+    assert np.array_equal(bits(y0), x)                    # position 0 is the identity
+
+
+# ------------------------------------------------------------------ SwiGLU
+
+@pytest.mark.parametrize("in_f32", [False, True])
+def test_swiglu(dev, in_f32):
+    rng = np.random.default_rng(12)
+    b, n = 2, 8192
+    if in_f32:
+        g = (rng.standard_normal((b, n)) * 3).astype(np.float32)
+        u = (rng.standard_normal((b, n)) * 3).astype(np.float32)
+        gd, ud = torch.from_numpy(g).to(dev), torch.from_numpy(u).to(dev)
+        ref = do.swiglu_from_raw(g, u)
+    else:
+        gb, ub = synth.random_bf16(rng, (b, n), 3.0), synth.random_bf16(rng, (b, n), 3.0)
+        gd, ud = bf16_dev(gb, dev), bf16_dev(ub, dev)
+        ref = do.swiglu(qo.bf16_to_f32(gb), qo.bf16_to_f32(ub))
+    y, yf = ops.swiglu(gd, ud, want_f32=True)
+    assert_close(yf.cpu().numpy(), ref)
+    assert_bf16_close(bits(y), ref)
+    assert (yf.cpu().numpy() != 0).sum() == (ref != 0).sum()   # whole vector processed
+
+
+# ------------------------------------------------------------------ fused [q,k,v,RoPE]
+
+@pytest.mark.parametrize("batch,norm", [(1, False), (1, True), (3, True)])
+def test_qkv_rope(dev, batch, norm):
+    rng = np.random.default_rng(13)
+    hq, hkv, hid, lmax = 40, 8, 2560, 512
+    kt = hid // 256
+    wq = synth.q4_tiles(rng, hq * 64, hid).reshape(-1, 5120)
+    wk = synth.q4_tiles(rng, hkv * 64, hid).reshape(-1, 5120)
+    wv = synth.q4_tiles(rng, hkv * 64, hid).reshape(-1, 5120)
+    pos = rng.integers(0, lmax, batch).astype(np.int32)
+    tab_np = do.rope_table(lmax, 64, 10000.0)
+    tab = ops.rope_table(lmax, 64, 10000.0)
+    kc = torch.zeros((batch, hkv, lmax, 64), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    nraw = (hq + 2 * hkv) * 64
+    raw = torch.empty((batch, nraw), dtype=torch.float32, device=dev)
+    xn = torch.empty((batch, hid), dtype=torch.bfloat16, device=dev)
+    nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+    if norm:
+        h = (rng.standard_normal((batch, hid)) * 20).astype(np.float32)
+        x_dev = torch.from_numpy(h).to(dev)
+        norm_dev = bf16_dev(nw, dev)
+    else:
+        xb = synth.random_bf16(rng, (batch, hid))
+        x_dev = bf16_dev(xb, dev)
+        norm_dev = None
+    d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
+    q = ops.qkv_rope(d(wq), d(wk), d(wv), hq, hkv, kt, x_dev, torch.from_numpy(pos).to(dev), tab,
+                     kc, vc, norm_w=norm_dev, raw_out=raw, xn_out=xn if norm else None)
+    torch.cuda.synchronize()
+    if norm:
+        ref_xn = do.rmsnorm(h, nw, 1e-5)
+        assert_bf16_close(bits(xn), ref_xn, max_frac=2e-3)
+        x_used = bits(xn)            # teacher-force the GEMV on the kernel's own input
+    else:
+        x_used = xb
+    raw_np = raw.cpu().numpy()
+    ref_q = qo.gemv(wq, "q4", x_used, hq * 2, kt, acc=np.float64).reshape(batch, -1)
+    ref_k = qo.gemv(wk, "q4", x_used, hkv * 2, kt, acc=np.float64).reshape(batch, -1)
+    ref_v = qo.gemv(wv, "q4", x_used, hkv * 2, kt, acc=np.float64).reshape(batch, -1)
+    assert_close(raw_np, np.concatenate([ref_q, ref_k, ref_v], axis=1))
+    # epilogue on the kernel's own accumulators: narrow, rotate q and k, narrow v
+    qr, kr, vr = do.qkv_rope_from_raw(raw_np[:, :hq * 64], raw_np[:, hq * 64:(hq + hkv) * 64],
+                                      raw_np[:, (hq + hkv) * 64:], pos, tab_np)
+    assert_bf16_close(bits(q).reshape(batch, hq, 64), qr)
+    kcn, vcn = bits(kc), bits(vc)
+    for b in range(batch):
+        assert_bf16_close(kcn[b, :, pos[b]], kr[b])
+        assert np.array_equal(vcn[b, :, pos[b]], qo.bf16_round(vr[b].astype(np.float32)))
+        mask = np.ones(lmax, bool)
+        mask[pos[b]] = False
+        assert not kcn[b][:, mask].any() and not vcn[b][:, mask].any()   # nothing else written
+
+
+# ------------------------------------------------------------------ fused [gate,up,SwiGLU]
+
+@pytest.mark.parametrize("batch,norm", [(1, False), (2, True)])
+def test_gate_up_swiglu(dev, batch, norm):
+    rng = np.random.default_rng(14)
+    hid, inter = 2560, 8192
+    kt = hid // 256
+    wg = synth.q4_tiles(rng, inter, hid).reshape(-1, 5120)
+    wu = synth.q4_tiles(rng, inter, hid).reshape(-1, 5120)
+    raw = torch.empty((batch, 2 * inter), dtype=torch.float32, device=dev)
+    xn = torch.empty((batch, hid), dtype=torch.bfloat16, device=dev)
+    if norm:
+        h = (rng.standard_normal((batch, hid)) * 20).astype(np.float32)
+        nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+        x_dev, norm_dev = torch.from_numpy(h).to(dev), bf16_dev(nw, dev)
+    else:
+        xb = synth.random_bf16(rng, (batch, hid))
+        x_dev, norm_dev = bf16_dev(xb, dev), None
+    d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
+    hout = ops.gate_up_swiglu(d(wg), d(wu), inter // 32, kt, x_dev, norm_w=norm_dev,
+                              raw_out=raw, xn_out=xn if norm else None)
+    torch.cuda.synchronize()
+    if norm:
+        assert_bf16_close(bits(xn), do.rmsnorm(h, nw, 1e-5), max_frac=2e-3)
+        x_used = bits(xn)
+    else:
+        x_used = xb
+    raw_np = raw.cpu().numpy()
+    ref_g = qo.gemv(wg, "q4", x_used, inter // 32, kt, acc=np.float64).reshape(batch, -1)
+    ref_u = qo.gemv(wu, "q4", x_used, inter // 32, kt, acc=np.float64).reshape(batch, -1)
+    assert_close(raw_np, np.concatenate([ref_g, ref_u], axis=1))
+    ref_h = do.swiglu_from_raw(raw_np[:, :inter], raw_np[:, inter:])
+    assert_bf16_close(bits(hout), ref_h)
+
+
+# ------------------------------------------------------------------ attention
+
+@pytest.mark.parametrize("batch,L,ragged", [
+    (1, 1, False), (1, 32, False), (1, 100, False), (1, 512, False), (1, 4096, False),
+    (8, 512, True), (8, 4096, False), (1, 32768, False),
+])
+def test_gqa_decode(dev, batch, L, ragged):
+    rng = np.random.default_rng(15 + L)
+    hq, hkv = 40, 8
+    q = synth.random_bf16(rng, (batch, hq, 64))
+    k = synth.random_bf16(rng, (batch, hkv, L, 64))
+    v = synth.random_bf16(rng, (batch, hkv, L, 64))
+    lens = (rng.integers(1, L + 1, batch) if ragged else np.full(batch, L)).astype(np.int32)
+    out, of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
+                             torch.from_numpy(lens).to(dev), 0.125, want_f32=True)
+    ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v), lens, 0.125)
+    assert_close(of.cpu().numpy(), ref)
+    assert_bf16_close(bits(out), ref)
+    if L == 1:
+        expect = np.repeat(qo.bf16_to_f32(v)[:, :, 0], hq // hkv, axis=1)
+        assert np.array_equal(of.cpu().numpy(), expect)     # one position: out = V[0]
+
+
+def test_gqa_decode_uniform_softmax(dev):
+    """Constant K gives a uniform softmax, so out = mean(V) (a closed form)."""
+    rng = np.random.default_rng(16)
+    L = 1000
+    q = synth.random_bf16(rng, (1, 40, 64))
+    k = np.tile(synth.random_bf16(rng, (1, 8, 1, 64)), (1, 1, L, 1))
+    v = synth.random_bf16(rng, (1, 8, L, 64))
+    of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
+                        torch.full((1,), L, dtype=torch.int32, device=dev), 0.125,
+                        want_f32=True)[1]
+    expect = np.repeat(qo.bf16_to_f32(v).astype(np.float64).mean(axis=2), 5, axis=1)
+    assert_close(of.cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("n_split", [1, 2, 7, 33])
+def test_gqa_decode_splits(dev, n_split):
+    rng = np.random.default_rng(17)
+    L = 2100
+    q = synth.random_bf16(rng, (2, 40, 64))
+    k = synth.random_bf16(rng, (2, 8, L, 64))
+    v = synth.random_bf16(rng, (2, 8, L, 64))
+    lens = np.array([L, 777], np.int32)
+    of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
+                        torch.from_numpy(lens).to(dev), 0.125, n_split=n_split, want_f32=True)[1]
+    ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v), lens, 0.125)
+    assert_close(of.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------------ helpers
+
+def test_embed_and_argmax(dev):
+    rng = np.random.default_rng(18)
+    vocab, hid = 1024, 512
+    w = synth.q8_tiles(rng, vocab, hid).reshape(-1, 8704)
+    toks = np.array([0, 31, 32, 1023], np.int32)
+    h = ops.embed_q8(torch.from_numpy(w.reshape(-1)).to(dev), torch.from_numpy(toks).to(dev),
+                     vocab, hid).cpu().numpy()
+    assert np.array_equal(h, do.embed_rows(w, toks, vocab, hid))
+    logits = rng.standard_normal((3, 100352)).astype(np.float32)
+    logits[1, 5000] = logits[1, 7000] = 99.0         # first maximum wins
+    idx = ops.argmax(torch.from_numpy(logits).to(dev)).cpu().numpy()
+    assert idx.tolist() == np.argmax(logits, axis=1).tolist()
