@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Benchmark of the q4nx decode hot path on one MI355X.
+
+Headline (one JSON line): q4 W4A16 GEMV throughput at granite-3B projection shapes,
+batch 1 -- gate/up 2560->8192 and down 8192->2560 -- in GB/s of algorithmic bytes
+(packed weights + activation in + fp32 output), with the HBM roofline fraction of the GEMV
+kernel and the reference's own CPU GEMV timed on this host beside it. When the decode
+engine is available the same line also carries granite-3B-shaped decode tokens/s.
+
+A step is one pass over ROT distinct layers' gate, up and down weights (ROT * 39.3 MB,
+well above the 256 MB Infinity Cache, so the bytes come from HBM), captured once in a HIP
+graph and replayed: 3 * ROT GEMV launches per step, inputs resident in HBM.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from llmnputest_amd import ops  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+HIDDEN, INTER = 2560, 8192
+Q4_TILE = 5120
+
+
+def q4_bytes(n: int, k: int) -> int:
+    return (n // 32) * (k // 256) * Q4_TILE
+
+
+def algo_bytes(n: int, k: int) -> int:
+    """Packed weights + bf16 activation in + fp32 output."""
+    return q4_bytes(n, k) + 2 * k + 4 * n
+
+
+def random_q4_tiles(n: int, k: int, gen: torch.Generator, dev) -> torch.Tensor:
+    """Device-generated q4 tiles: uniform nibbles, d = bf16(|N|*0.02), m = bf16(-8d)."""
+    t = (n // 32) * (k // 256)
+    w = torch.randint(0, 256, (t, Q4_TILE), dtype=torch.uint8, device=dev, generator=gen)
+    d = (torch.randn((t, 256), device=dev, generator=gen).abs() * 0.02).to(torch.bfloat16)
+    m = (d.float() * -8.0).to(torch.bfloat16)
+    w[:, 0:512] = d.view(torch.uint8).reshape(t, 512)
+    w[:, 512:1024] = m.view(torch.uint8).reshape(t, 512)
+    return w.reshape(-1)
+
+
+def gemv_bench(steps: int, warmup: int, rot: int, dev) -> dict:
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    layers = [(random_q4_tiles(INTER, HIDDEN, gen, dev), random_q4_tiles(INTER, HIDDEN, gen, dev),
+               random_q4_tiles(HIDDEN, INTER, gen, dev)) for _ in range(rot)]
+    x = torch.randn(HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
+    h = torch.randn(INTER, device=dev, generator=gen).to(torch.bfloat16)
+    y_gu = torch.empty(INTER, dtype=torch.float32, device=dev)
+    y_d = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    ws = ops.Workspace(8 << 20, device=dev)
+
+    def run(which: str):
+        for g, u, d in layers:
+            if which in ("all", "gate_up"):
+                ops.gemv(g, "q4", x, INTER // 32, HIDDEN // 256, out=y_gu, ws=ws)
+                ops.gemv(u, "q4", x, INTER // 32, HIDDEN // 256, out=y_gu, ws=ws)
+            if which in ("all", "down"):
+                ops.gemv(d, "q4", h, HIDDEN // 32, INTER // 256, out=y_d, ws=ws)
+
+    def timed(which: str, n_steps: int) -> float:
+        run(which)                              # eager warm-up (no allocation later)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run(which)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n_steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / n_steps   # seconds per step
+
+    b_gu, b_d = algo_bytes(INTER, HIDDEN), algo_bytes(HIDDEN, INTER)
+    t_all = timed("all", steps)
+    t_gu = timed("gate_up", steps)
+    t_d = timed("down", steps)
+    step_bytes = rot * (2 * b_gu + b_d)
+    return {
+        "t_step": t_all,
+        "launches_per_step": 3 * rot,
+        "step_bytes": step_bytes,
+        "gbs": step_bytes / t_all / 1e9,
+        "us_per_launch": t_all / (3 * rot) * 1e6,
+        "gate_up_gbs": 2 * rot * b_gu / t_gu / 1e9,
+        "gate_up_us": t_gu / (2 * rot) * 1e6,
+        "down_gbs": rot * b_d / t_d / 1e9,
+        "down_us": t_d / rot * 1e6,
+        "bytes_gate_up": b_gu,
+        "bytes_down": b_d,
+    }
+
+
+def cpu_baseline(sample_iters: int) -> dict | None:
+    """The reference's own CPU GEMV (designs/granite_gemv/cpu_baseline.cpp, built from its
+    source into oracle/_ref/) on the same shapes, all host cores; else the C port."""
+    try:
+        from oracle import cpu_oracle
+        from llmnputest_amd import synth
+    except Exception as e:  # pragma: no cover
+        print(f"cpu baseline unavailable: {e}", file=sys.stderr)
+        return None
+    threads = cpu_oracle.host_threads()
+    rng = np.random.default_rng(7)
+    gate = synth.q4_tiles(rng, INTER, HIDDEN).reshape(-1)
+    down = synth.q4_tiles(rng, HIDDEN, INTER).reshape(-1)
+    b_gu, b_d = algo_bytes(INTER, HIDDEN), algo_bytes(HIDDEN, INTER)
+    t0 = time.time()
+    if cpu_oracle.REF_BASELINE.exists():
+        rg = cpu_oracle.run_ref_baseline(gate, INTER // 32, HIDDEN // 256, threads, sample_iters)
+        rd = cpu_oracle.run_ref_baseline(down, HIDDEN // 32, INTER // 256, threads, sample_iters)
+        t_layer = (2 * rg["gemv_ms"] + rd["gemv_ms"]) / 1e3
+        kind = "reference"
+        sample = (f"cpu_baseline.cpp (reference source, AVX2) on gate 8192x2560 and down "
+                  f"2560x8192 q4 tiles, {sample_iters} iterations each; per layer = 2*gate + down")
+    else:
+        x = synth.random_bf16(rng, HIDDEN)
+        xd = synth.random_bf16(rng, INTER)
+        s = time.perf_counter()
+        for _ in range(sample_iters):
+            cpu_oracle.gemv(gate, "q4", x, INTER // 32, HIDDEN // 256, threads)
+        tg = (time.perf_counter() - s) / sample_iters
+        s = time.perf_counter()
+        for _ in range(sample_iters):
+            cpu_oracle.gemv(down, "q4", xd, HIDDEN // 32, INTER // 256, threads)
+        td = (time.perf_counter() - s) / sample_iters
+        t_layer = 2 * tg + td
+        kind = "port"
+        sample = f"oracle/cpu_oracle.c fp64 GEMV, {sample_iters} iterations per shape"
+    return {"value": round((2 * b_gu + b_d) / t_layer / 1e9, 2), "unit": "GB/s",
+            "cores": threads, "kind": kind, "sample": sample,
+            "wall_s": round(time.time() - t0, 1)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--rot", type=int, default=16, help="distinct layers rotated per step")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-iters", type=int, default=400)
+    a = ap.parse_args()
+
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build runs the decode hot path on a single "
+              "MI355X and has no multi-GPU path (see DESIGN.md for how it would shard).",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    r = gemv_bench(a.steps, a.warmup, a.rot, dev)
+    cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
+    gbs = r["gbs"]
+    line = {
+        "metric": "q4 GEMV HBM GB/s (% of peak) + decode tok/s, granite-3B shape, batch 1",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(r["t_step"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded device RNG, q4nx tiles)",
+        "config": {
+            "workload": "q4 W4A16 GEMV batch 1, granite-3B projections gate/up 2560->8192 and "
+                        "down 8192->2560",
+            "layers_rotated": a.rot,
+            "bytes_per_step": r["step_bytes"],
+            "launches_per_step": r["launches_per_step"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "per_shape": {
+            "gate_up_2560x8192": {"GB/s": round(r["gate_up_gbs"], 1), "us": round(r["gate_up_us"], 3)},
+            "down_8192x2560": {"GB/s": round(r["down_gbs"], 1), "us": round(r["down_us"], 3)},
+            "us_per_launch": round(r["us_per_launch"], 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

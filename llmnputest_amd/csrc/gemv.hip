@@ -5,31 +5,31 @@
 // plus the fused epilogues of granite_qkv_rope.h:30-71 and granite_swiglu_f32.h:27-51.
 //
 // Work decomposition
-//   A workgroup owns one (group, member, K-split): `nt` consecutive K-tiles of one
-//   tile-row. A group is the set of tile-rows an epilogue needs together: one tile-row
-//   for a plain GEMV, the two tile-rows of one attention head for [q,k,v,RoPE] (RoPE
-//   pairs dim i with i+32), or the same tile-row of gate and up for SwiGLU. Splits of a
-//   group write fp32 partials to the workspace and the last workgroup to arrive (atomic
-//   counter) sums them in split order and runs the epilogue, so results are
-//   bit-reproducible run to run.
+//   One workgroup owns one output *group*: the tile-rows an epilogue needs together --
+//   one tile-row for a plain GEMV, the two tile-rows of an attention head for
+//   [q,k,v,RoPE] (RoPE pairs dim i with i+32), or the same tile-row of gate and up for
+//   SwiGLU. Each wave of the workgroup owns TPW consecutive K-tiles of one tile-row,
+//   so a workgroup covers the whole K of its group and no cross-workgroup reduction
+//   (and no workspace) is needed. Waves combine through LDS once, in a fixed order,
+//   so results are bit-reproducible.
 //
-// Data path
-//   The workgroup's tile bytes are contiguous; they go global -> LDS with
-//   global_load_lds_dwordx4 (1 KB per wave instruction, fully coalesced). Two lanes own
-//   one (row-block, 32-K group) "unit" of a tile, 16 K each, so the per-group scale and
-//   minimum are applied once per 256 (q4) weights per lane and there is no cross-lane
-//   traffic until the end.
+// Data path (decode is HBM-bound: every byte is read once, straight into registers)
+//   Four lanes own one (row-block, 32-K group) "unit" of a tile: lane l reads the 64
+//   (q4) or 128 (q8) contiguous bytes at unit l/4, quarter l%4, i.e. 8 K x 16 rows. All
+//   of a wave's tile loads are issued before any arithmetic; each tile is consumed as
+//   soon as its registers arrive. The 4-lane partial sums are reduced with two xor
+//   shuffles, then the per-group scale and minimum are applied to the lane's 4 rows.
 //
 // Arithmetic (exact inputs, fp32 accumulate)
-//   x is converted to fp16 with one power-of-two scale per workgroup chosen from
-//   max|x| over its K range (bf16 values convert exactly in fp16's normal range). A
-//   4-bit code c placed in the low bits of an fp16 is the subnormal c * 2^-24, exactly;
-//   v_dot2_f32_f16 then multiplies it by two x values with no rounding of the products.
-//   For one byte b = lo | hi<<4 of two rows at one k, a v_perm_b32 builds
-//   [b(k0), 0, b(k1), 0] = (lo + 16 hi) * 2^-24 for two k, and the same dword masked
-//   with 0x000F000F gives lo alone: two dot2 per 4 weights recover both rows' sums
+//   x is converted to fp16 with one power-of-two scale per wave, chosen from max|x| over
+//   the wave's K range (bf16 values convert exactly in fp16's normal range). A 4-bit code
+//   c placed in the low bits of an fp16 is the subnormal c * 2^-24, exactly, and
+//   v_dot2_f32_f16 multiplies two of them by two x values with exact products. For a
+//   byte b = lo | hi<<4 holding two rows at one k, a v_perm_b32 builds
+//   [b(k0), 0, b(k1), 0] = (lo + 16 hi) * 2^-24 for two k, and the same dword masked with
+//   0x000F000F gives lo alone: two dot2 per 4 weights recover both rows' sums
 //   (hi = (full - lo) / 16). q8 codes are biased by 128 (xor 0x80) into 1..255 and the
-//   bias is removed with 128 * sum(x).  The Q4_1 minimum factors out of the K sum
+//   bias is removed with 128 * sum(x). The Q4_1 minimum factors out of the K sum
 //   (granite_gemv.h:19-29): y_r += d_r * sum(c x) + m_r * sum(x) per 32-K group.
 
 #include "common.h"
@@ -42,10 +42,9 @@ struct GemvArgs {
   const uint8_t* w[3];
   int n_tr[3];
   int op;
-  int G;          // tile-rows per group (1 or 2)
-  int n_groups;
+  int G;             // tile-rows per group (1 or 2)
   int grp_q, grp_k;  // QKV: groups [0,grp_q) are q heads, [grp_q,grp_q+grp_k) k heads, rest v
-  int k_t, nt, n_split, batch;
+  int k_t, batch;
   // input: bf16 x, or fp32 residual h normalised with norm_w in the prologue
   const uint16_t* x;
   const float* hres;
@@ -70,50 +69,49 @@ struct GemvArgs {
   // gate/up
   uint16_t* h_out;
   int64_t h_stride;
-  // split-K
-  float* partial;
-  unsigned* counters;
 };
 
-template <int KIND>
-struct TileTraits;
-template <>
-struct TileTraits<4> {
-  static constexpr int kBytes = kQ4TileBytes;
-};
-template <>
-struct TileTraits<8> {
-  static constexpr int kBytes = kQ8TileBytes;
-};
-
-constexpr int kLanesPerTile = 32;  // 16 units x 2 lanes
-constexpr int kMaxNt = 8;
-
-__host__ __device__ inline int lds_w_bytes(int kind, int nt) {
-  return nt * (kind == 4 ? kQ4TileBytes : kQ8TileBytes);
-}
+constexpr int kMaxWaves = 16;
 
 // v_perm selector for result bytes [s1.b_i, 0, s0.b_i, 0]
 __device__ __forceinline__ constexpr uint32_t sel_byte(int i) {
   return 0x0c040c00u + (uint32_t)i * 0x00010001u;
 }
 
-template <int KIND, int B>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  constexpr int TB = TileTraits<KIND>::kBytes;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+// 16 values summed over lane bits 1 and 0 (xor 2, then xor 1); lane q keeps 4q..4q+3.
+__device__ __forceinline__ void transpose_reduce4(const float (&v)[16], float (&o)[4], int lane) {
+  float t8[8];
+  const bool up1 = (lane & 2) != 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float keep = up1 ? v[i + 8] : v[i];
+    const float send = up1 ? v[i] : v[i + 8];
+    t8[i] = keep + __shfl_xor(send, 2);
+  }
+  const bool up0 = (lane & 1) != 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float keep = up0 ? t8[i + 4] : t8[i];
+    const float send = up0 ? t8[i] : t8[i + 4];
+    o[i] = keep + __shfl_xor(send, 1);
+  }
+}
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int nwaves = blockDim.x >> 6;
+template <int KIND, int B, int TPW>
+__global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
+  constexpr int TB = KIND == 4 ? kQ4TileBytes : kQ8TileBytes;
+  constexpr int NCH = KIND == 4 ? 4 : 8;              // 16-byte chunks per lane per tile
+  constexpr int CODE_OFF = KIND == 4 ? 1024 : 512;    // start of the codes in a tile
+  __shared__ float sred[kMaxWaves][B][32];
+  __shared__ float sgrp[B][64];
+  __shared__ float snorm[kMaxWaves][B];
 
-  // ---- which (group, member, split) this workgroup owns
-  const int blk = blockIdx.x;
-  const int split = blk % a.n_split;
-  const int gm = blk / a.n_split;
-  const int member = gm % a.G;
-  const int group = gm / a.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int W = blockDim.x >> 6;
+  const int WM = W / a.G;             // waves per member tile-row
+  const int member = wave / WM, chunk = wave % WM;
+  const int group = blockIdx.x;
+
   int seg, tr;
   if (a.op == OP_PLAIN) {
     seg = 0;
@@ -135,344 +133,245 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     tr = 2 * hg + member;
   }
-  const int kt0 = split * a.nt;
-  const int ntiles = min(a.nt, a.k_t - kt0);
   const int K = a.k_t * kTileK;
-  const int k_lo = kt0 * kTileK;           // first K of this workgroup
-  const int nk = ntiles * kTileK;          // K values of this workgroup
+  const int kt0 = chunk * TPW;
+  const int ntw = max(0, min(TPW, a.k_t - kt0));    // tiles this wave really owns
 
-  // ---- LDS carve-up
-  uint8_t* sw = smem;                                                  // tiles
-  uint32_t* sx = (uint32_t*)(smem + lds_w_bytes(KIND, a.nt));          // [B][nt*128] fp16 pairs
-  float* sred = (float*)(sx + B * a.nt * (kTileK / 2));                // [nwaves][B][32]
-  float* sgrp = sred + 8 * B * 32;                                     // [B][64]
-  float* sscal = sgrp + B * 64;                                        // [8][B] scratch
-  int* sflag = (int*)(sscal + 8 * B);
+  // lane roles: q = lane bits 0-1 (8-K quarter), kb = bits 2-4, rb = bit 5
+  const int q = lane & 3, kb = (lane >> 2) & 7, rb = lane >> 5;
+  const int kx = kb * kGroup + q * 8;                // first K of this lane inside a tile
+  const bool norm = a.norm_w != nullptr;
 
-  // ---- 1. weights: global -> LDS, all issued up front
-  {
-    const uint8_t* src = a.w[seg] + ((size_t)tr * a.k_t + kt0) * TB;
-    const int n_chunks = ntiles * TB / 16;
-    const int n_inst = (n_chunks + 63) / 64;
-    for (int i = wave; i < n_inst; i += nwaves) {
-      const int c = i * 64 + lane;
-      if (c < n_chunks) {
-        __builtin_amdgcn_global_load_lds(
-            (const void*)(src + (size_t)c * 16),
-            (__attribute__((address_space(3))) void*)(sw + i * 1024), 16, 0, 0);
+  // ---- 1. activations first (so their wait does not include the weight stream)
+  uint4 xr[B][TPW];       // 8 bf16 per lane per tile
+  float hx[B][TPW][8];    // fp32 residual values (RMSNorm prologue only)
+  uint4 nw[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int kt = min(kt0 + t, a.k_t - 1);
+    const int k = kt * kTileK + kx;
+    nw[t] = make_uint4(0, 0, 0, 0);
+    if (norm) nw[t] = *(const uint4*)(a.norm_w + k);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      xr[b][t] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hx[b][t][i] = 0.f;
+      if (b < a.batch) {
+        if (norm) {
+          const float4 h0 = *(const float4*)(a.hres + b * a.x_stride + k);
+          const float4 h1 = *(const float4*)(a.hres + b * a.x_stride + k + 4);
+          hx[b][t][0] = h0.x; hx[b][t][1] = h0.y; hx[b][t][2] = h0.z; hx[b][t][3] = h0.w;
+          hx[b][t][4] = h1.x; hx[b][t][5] = h1.y; hx[b][t][6] = h1.z; hx[b][t][7] = h1.w;
+        } else {
+          xr[b][t] = *(const uint4*)(a.x + b * a.x_stride + k);
+        }
       }
     }
   }
 
-  // ---- 2. activation prologue: [RMSNorm] -> bf16 -> fp16 with a power-of-two scale
-  int xs_exp[B];  // true x = x' * 2^xs_exp
+  // ---- 2. weights and per-group metadata of every tile of this wave
+  uint4 wq[TPW][NCH];
+  uint2 md[TPW], mm[TPW];
   {
-    float inv_rms[B];
-    if (a.norm_w != nullptr) {
-      float ss[B];
+    const uint8_t* rowp = a.w[seg] + (size_t)tr * a.k_t * TB;
+    const int g = kb * 32 + rb * 16 + q * 4;          // meta index of this lane's 4 rows
 #pragma unroll
-      for (int b = 0; b < B; ++b) ss[b] = 0.f;
-      for (int k = tid * 2; k < K; k += blockDim.x * 2) {
+    for (int t = 0; t < TPW; ++t) {
+      const uint8_t* tile = rowp + (size_t)min(kt0 + t, a.k_t - 1) * TB;
+      const uint4* src = (const uint4*)(tile + CODE_OFF + lane * (NCH * 16));
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
-          if (b < a.batch) {
-            float2 v = *(const float2*)(a.hres + b * a.x_stride + k);
-            ss[b] = fmaf(v.x, v.x, ss[b]);
-            ss[b] = fmaf(v.y, v.y, ss[b]);
-          }
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        float s = wave_sum(ss[b]);
-        if (lane == 0) sscal[wave * B + b] = s;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        float s = 0.f;
-        for (int w = 0; w < nwaves; ++w) s += sscal[w * B + b];
-        inv_rms[b] = 1.0f / sqrtf(s / (float)K + a.eps);
-      }
-      __syncthreads();
+      for (int c = 0; c < NCH; ++c) wq[t][c] = src[c];
+      md[t] = *(const uint2*)(tile + 2 * g);
+      mm[t] = make_uint2(0, 0);
+      if (KIND == 4) mm[t] = *(const uint2*)(tile + kMetaBytes + 2 * g);
     }
+  }
 
-    // bf16 values of this workgroup's K range, two per thread-iteration
-    float mx[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) mx[b] = 0.f;
-    const int npairs = nk / 2;
-    // threads >= 32 * nt, pairs <= 128 * nt: at most 4 pairs per thread
-    constexpr int kPairsPerThread = 4;
-    uint32_t xv[B][kPairsPerThread];
-#pragma unroll
-    for (int np = 0; np < kPairsPerThread; ++np) {
-      const int p = tid + np * blockDim.x;
-#pragma unroll
-      for (int b = 0; b < B; ++b) xv[b][np] = 0u;
-      if (p >= npairs) continue;
-      const int k = k_lo + 2 * p;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        uint32_t bits = 0;
-        if (b < a.batch) {
-          if (a.norm_w != nullptr) {
-            float2 v = *(const float2*)(a.hres + b * a.x_stride + k);
-            uint32_t wbits = *(const uint32_t*)(a.norm_w + k);
-            uint16_t lo = f32_to_bf16((v.x * inv_rms[b]) * bf16lo(wbits));
-            uint16_t hi = f32_to_bf16((v.y * inv_rms[b]) * bf16hi(wbits));
-            bits = (uint32_t)lo | ((uint32_t)hi << 16);
-            if (a.xn_out != nullptr && group == 0 && member == 0)
-              *(uint32_t*)(a.xn_out + b * a.x_stride + k) = bits;
-          } else {
-            bits = *(const uint32_t*)(a.x + b * a.x_stride + k);
-          }
-        }
-        xv[b][np] = bits;
-        mx[b] = fmaxf(mx[b], fmaxf(fabsf(bf16lo(bits)), fabsf(bf16hi(bits))));
-      }
-    }
+  // ---- 3. RMSNorm prologue: sum of squares over K from member-0 waves, row-block-0 lanes
+  if (norm) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      float m = wave_max(mx[b]);
-      if (lane == 0) sscal[wave * B + b] = m;
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+        if (t < ntw && rb == 0 && member == 0) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s = fmaf(hx[b][t][i], hx[b][t][i], s);
+        }
+      s = wave_sum(s);
+      if (lane == 0) snorm[wave][b] = s;
     }
     __syncthreads();
-    float to_half[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      float m = 0.f;
-      for (int w = 0; w < nwaves; ++w) m = fmaxf(m, sscal[w * B + b]);
-      int e = 0;
-      if (m > 0.f && m <= 3.0e38f) {
-        (void)frexpf(m, &e);   // m < 2^e
-        e -= 15;               // scaled max < 2^15
-        e = e < -120 ? -120 : e;
-      }
-      to_half[b] = ldexpf(1.0f, -e);
-      xs_exp[b] = e;
-    }
+      float s = 0.f;
+      for (int w = 0; w < WM; ++w) s += snorm[w][b];
+      const float inv = 1.0f / sqrtf(s / (float)K + a.eps);
 #pragma unroll
-    for (int np = 0; np < kPairsPerThread; ++np) {
-      const int p = tid + np * blockDim.x;
-      if (p >= npairs) continue;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        uint32_t bits = xv[b][np];
-        half2_t h;
-        h.x = (_Float16)(bf16lo(bits) * to_half[b]);
-        h.y = (_Float16)(bf16hi(bits) * to_half[b]);
-        sx[b * (a.nt * kTileK / 2) + p] = h2_bits(h);
-      }
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  // ---- 3. per-lane half-unit dot products
-  const int j = tid >> 5;              // tile within the workgroup
-  const int u = (tid >> 1) & 15;       // unit: rb*8 + kb (memory order)
-  const int hh = tid & 1;              // which 16 K of the unit
-  const int rb = u >> 3, kb = u & 7;
-  const bool active = j < ntiles;
-  const int jj = active ? j : 0;
-  const uint8_t* tile = sw + jj * TB;
-  const int pk0 = (jj * kTileK + kb * kGroup + hh * 16) >> 1;  // first x pair
-  constexpr uint32_t kOne2 = 0x3C003C00u;                        // fp16 (1, 1)
-
-  float acc[B][16];
-  if (KIND == 4) {
-    float lo[B][8], full[B][8], X[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      X[b] = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) lo[b][i] = full[b][i] = 0.f;
-    }
-    const uint8_t* nib = tile + 1024 + rb * 2048 + kb * 256 + hh * 128;
-    const int rot = tid >> 1;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int c = (s + rot) & 7;
-      const uint4 q = *(const uint4*)(nib + c * 16);
-      uint32_t xp[B];
-#pragma unroll
-      for (int b = 0; b < B; ++b) xp[b] = sx[b * (a.nt * kTileK / 2) + pk0 + c];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t T0 = perm(q.z, q.x, sel_byte(i));
-        const uint32_t T1 = perm(q.w, q.y, sel_byte(i));
-        const uint32_t L0 = T0 & 0x000F000Fu, L1 = T1 & 0x000F000Fu;
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-          full[b][i] = dot2(T0, xp[b], full[b][i]);
-          lo[b][i] = dot2(L0, xp[b], lo[b][i]);
-          full[b][4 + i] = dot2(T1, xp[b], full[b][4 + i]);
-          lo[b][4 + i] = dot2(L1, xp[b], lo[b][4 + i]);
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < B; ++b) X[b] = dot2(xp[b], kOne2, X[b]);
-    }
-    // scale and minimum of this unit: d[g], m[g], g = kb*32 + rb*16 + r
-    const int g0 = kb * 32 + rb * 16;
-    const uint4 d0 = *(const uint4*)(tile + 2 * g0);
-    const uint4 d1 = *(const uint4*)(tile + 2 * g0 + 16);
-    const uint4 m0 = *(const uint4*)(tile + kMetaBytes + 2 * g0);
-    const uint4 m1 = *(const uint4*)(tile + kMetaBytes + 2 * g0 + 16);
-    const uint32_t dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    const uint32_t mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float se = lo[b][i] * 16777216.0f;             // 2^24
-        const float so = (full[b][i] - lo[b][i]) * 1048576.0f;  // 2^20
-        float ve = fmaf(bf16lo(dd[i]), se, bf16lo(mm[i]) * X[b]);
-        float vo = fmaf(bf16hi(dd[i]), so, bf16hi(mm[i]) * X[b]);
-        acc[b][2 * i] = active ? ve : 0.f;
-        acc[b][2 * i + 1] = active ? vo : 0.f;
-      }
-    }
-  } else {
-    float sacc[B][16], X[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      X[b] = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
-    }
-    const uint8_t* cod = tile + kMetaBytes + u * 512 + hh * 256;
-    const int rot = tid >> 1;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int p = (s + rot) & 7;
-      const uint4 A = *(const uint4*)(cod + p * 32);
-      const uint4 Bv = *(const uint4*)(cod + p * 32 + 16);
-      uint32_t xp[B];
-#pragma unroll
-      for (int b = 0; b < B; ++b) xp[b] = sx[b * (a.nt * kTileK / 2) + pk0 + p];
-      const uint32_t av[4] = {A.x ^ 0x80808080u, A.y ^ 0x80808080u, A.z ^ 0x80808080u,
-                              A.w ^ 0x80808080u};
-      const uint32_t bv[4] = {Bv.x ^ 0x80808080u, Bv.y ^ 0x80808080u, Bv.z ^ 0x80808080u,
-                              Bv.w ^ 0x80808080u};
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
+      for (int t = 0; t < TPW; ++t) {
+        const uint32_t wv[4] = {nw[t].x, nw[t].y, nw[t].z, nw[t].w};
+        uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t T = perm(bv[qd], av[qd], sel_byte(i));
-#pragma unroll
-          for (int b = 0; b < B; ++b) sacc[b][4 * qd + i] = dot2(T, xp[b], sacc[b][4 * qd + i]);
+          const uint16_t lo = f32_to_bf16((hx[b][t][2 * i] * inv) * bf16lo(wv[i]));
+          const uint16_t hi = f32_to_bf16((hx[b][t][2 * i + 1] * inv) * bf16hi(wv[i]));
+          o[i] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-      }
-#pragma unroll
-      for (int b = 0; b < B; ++b) X[b] = dot2(xp[b], kOne2, X[b]);
-    }
-    const int g0 = kb * 32 + rb * 16;
-    const uint4 s0 = *(const uint4*)(tile + 2 * g0);
-    const uint4 s1 = *(const uint4*)(tile + 2 * g0 + 16);
-    const uint32_t sd[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const float bias = 128.0f * X[b];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float ve = fmaf(sacc[b][2 * i], 16777216.0f, -bias);
-        const float vo = fmaf(sacc[b][2 * i + 1], 16777216.0f, -bias);
-        acc[b][2 * i] = active ? bf16lo(sd[i]) * ve : 0.f;
-        acc[b][2 * i + 1] = active ? bf16hi(sd[i]) * vo : 0.f;
+        xr[b][t] = b < a.batch ? make_uint4(o[0], o[1], o[2], o[3]) : make_uint4(0, 0, 0, 0);
+        if (a.xn_out != nullptr && group == 0 && member == 0 && rb == 0 && t < ntw &&
+            b < a.batch)
+          *(uint4*)(a.xn_out + b * a.x_stride + (kt0 + t) * kTileK + kx) = xr[b][t];
       }
     }
   }
 
-  // ---- 4. reduce: lanes with the same row-block, then waves, then splits
-  // transpose-reduce over lane bits 0..3 (h, kb): afterwards lane holds row (lane & 15)
+  // ---- 4. fp16 conversion with one power-of-two scale per wave and batch row
+  uint32_t xp[B][TPW][4];
+  int xexp[B];
 #pragma unroll
   for (int b = 0; b < B; ++b) {
-    float v8[8];
-    {
-      const bool up = (lane & 8) != 0;
+    float m = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float keep = up ? acc[b][i + 8] : acc[b][i];
-        const float send = up ? acc[b][i] : acc[b][i + 8];
-        v8[i] = keep + __shfl_xor(send, 8);
+    for (int t = 0; t < TPW; ++t) {
+      if (t < ntw) {
+        const uint32_t v[4] = {xr[b][t].x, xr[b][t].y, xr[b][t].z, xr[b][t].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf16lo(v[i])), fabsf(bf16hi(v[i]))));
       }
     }
-    float v4[4];
-    {
-      const bool up = (lane & 4) != 0;
+    m = wave_max(m);
+    int e = 0;
+    if (m > 0.f && m <= 3.0e38f) {
+      (void)frexpf(m, &e);  // m < 2^e
+      e -= 15;              // scaled max < 2^15 < fp16 max
+      e = e < -120 ? -120 : e;
+    }
+    xexp[b] = e;
+    const float s = ldexpf(1.0f, -e);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const uint32_t v[4] = {xr[b][t].x, xr[b][t].y, xr[b][t].z, xr[b][t].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float keep = up ? v8[i + 4] : v8[i];
-        const float send = up ? v8[i] : v8[i + 4];
-        v4[i] = keep + __shfl_xor(send, 4);
+        half2_t h;
+        h.x = (_Float16)(bf16lo(v[i]) * s);
+        h.y = (_Float16)(bf16hi(v[i]) * s);
+        xp[b][t][i] = h2_bits(h);
       }
     }
-    float v2[2];
-    {
-      const bool up = (lane & 2) != 0;
+  }
+
+  // ---- 5. tiles, in arrival order
+  constexpr uint32_t kOne2 = 0x3C003C00u;  // fp16 (1, 1)
+  float acc[B][4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const float keep = up ? v4[i + 2] : v4[i];
-        const float send = up ? v4[i] : v4[i + 2];
-        v2[i] = keep + __shfl_xor(send, 2);
+  for (int b = 0; b < B; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[b][i] = 0.f;
+
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    if (t >= ntw) continue;
+    if (KIND == 4) {
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        // pv[2i] = lo of row pair i (even row), pv[2i+1] = lo + 16*hi (both rows)
+        float pv[16], X = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pv[i] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint4 w = wq[t][c];
+          const uint32_t xpc = xp[b][t][c];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t T0 = perm(w.z, w.x, sel_byte(i));   // row pair i   (rows 0..7)
+            const uint32_t T1 = perm(w.w, w.y, sel_byte(i));   // row pair 4+i (rows 8..15)
+            pv[2 * i + 1] = dot2(T0, xpc, pv[2 * i + 1]);
+            pv[2 * i] = dot2(T0 & 0x000F000Fu, xpc, pv[2 * i]);
+            pv[2 * (4 + i) + 1] = dot2(T1, xpc, pv[2 * (4 + i) + 1]);
+            pv[2 * (4 + i)] = dot2(T1 & 0x000F000Fu, xpc, pv[2 * (4 + i)]);
+          }
+          X = dot2(xpc, kOne2, X);
+        }
+        float r4[4];   // lo(2q), full(2q), lo(2q+1), full(2q+1): rows 4q .. 4q+3
+        transpose_reduce4(pv, r4, lane);
+        X += __shfl_xor(X, 1);
+        X += __shfl_xor(X, 2);
+        const float se0 = r4[0] * 16777216.0f, so0 = (r4[1] - r4[0]) * 1048576.0f;
+        const float se1 = r4[2] * 16777216.0f, so1 = (r4[3] - r4[2]) * 1048576.0f;
+        acc[b][0] += fmaf(bf16lo(md[t].x), se0, bf16lo(mm[t].x) * X);
+        acc[b][1] += fmaf(bf16hi(md[t].x), so0, bf16hi(mm[t].x) * X);
+        acc[b][2] += fmaf(bf16lo(md[t].y), se1, bf16lo(mm[t].y) * X);
+        acc[b][3] += fmaf(bf16hi(md[t].y), so1, bf16hi(mm[t].y) * X);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        float v[16], X = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint4 A = wq[t][2 * p], Bv = wq[t][2 * p + 1];
+          const uint32_t av[4] = {A.x ^ 0x80808080u, A.y ^ 0x80808080u, A.z ^ 0x80808080u,
+                                  A.w ^ 0x80808080u};
+          const uint32_t bv[4] = {Bv.x ^ 0x80808080u, Bv.y ^ 0x80808080u, Bv.z ^ 0x80808080u,
+                                  Bv.w ^ 0x80808080u};
+          const uint32_t xpc = xp[b][t][p];
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              v[4 * qd + i] = dot2(perm(bv[qd], av[qd], sel_byte(i)), xpc, v[4 * qd + i]);
+          X = dot2(xpc, kOne2, X);
+        }
+        float r4[4];
+        transpose_reduce4(v, r4, lane);
+        X += __shfl_xor(X, 1);
+        X += __shfl_xor(X, 2);
+        const float bias = 128.0f * X;
+        acc[b][0] += bf16lo(md[t].x) * fmaf(r4[0], 16777216.0f, -bias);
+        acc[b][1] += bf16hi(md[t].x) * fmaf(r4[1], 16777216.0f, -bias);
+        acc[b][2] += bf16lo(md[t].y) * fmaf(r4[2], 16777216.0f, -bias);
+        acc[b][3] += bf16hi(md[t].y) * fmaf(r4[3], 16777216.0f, -bias);
       }
     }
-    float v1;
-    {
-      const bool up = (lane & 1) != 0;
-      const float keep = up ? v2[1] : v2[0];
-      const float send = up ? v2[0] : v2[1];
-      v1 = keep + __shfl_xor(send, 1);
+  }
+
+  // ---- 6. sum over the 8 groups of K (lane bits 2..4), undo the activation scale
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const float sc = ldexpf(1.0f, xexp[b]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = acc[b][i];
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      if ((lane & 28) == 0) sred[wave][b][rb * 16 + q * 4 + i] = v * sc;
     }
-    v1 += __shfl_xor(v1, 32);
-    if (lane < 32) sred[(wave * B + b) * 32 + lane] = v1;  // lane&31 = rb*16 + r
   }
   __syncthreads();
 
-  const bool direct = (a.G == 1 && a.n_split == 1);
-  // a workgroup can be a single wave, so every (b, row) loop strides by blockDim
-  for (int e = tid; e < B * 32; e += blockDim.x) {
-    const int b = e >> 5, r = e & 31;
+  // ---- 7. waves of one member tile-row, in order
+  for (int e = tid; e < a.G * B * 32; e += blockDim.x) {
+    const int m = e / (B * 32), rest = e % (B * 32);
+    const int b = rest >> 5, r = rest & 31;
     float s = 0.f;
-    for (int w = 0; w < nwaves; ++w) s += sred[(w * B + b) * 32 + r];
-    s *= ldexpf(1.0f, xs_exp[b]);
-    if (direct) {
-      sgrp[b * 64 + r] = s;
-    } else {
-      a.partial[(((size_t)group * a.G + member) * a.n_split + split) * (B * 32) + e] = s;
-    }
-  }
-  if (!direct) {
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = atomicAdd(&a.counters[group], 1u);
-      sflag[0] = (prev == (unsigned)(a.G * a.n_split - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (sflag[0] == 0) return;
-    __threadfence();
-    for (int e = tid; e < a.G * B * 32; e += blockDim.x) {
-      const int m = e / (B * 32), rest = e % (B * 32);
-      const int b = rest >> 5, r = rest & 31;
-      const float* p = a.partial + (((size_t)group * a.G + m) * a.n_split) * (B * 32) + rest;
-      float s = 0.f;
-      for (int sp = 0; sp < a.n_split; ++sp) s += p[sp * (B * 32)];
-      sgrp[b * 64 + m * 32 + r] = s;
-    }
-    if (tid == 0) a.counters[group] = 0u;
+    for (int c = 0; c < WM; ++c) s += sred[m * WM + c][b][r];
+    sgrp[b][m * 32 + r] = s;
   }
   __syncthreads();
 
-  // ---- 5. epilogue on the whole group
+  // ---- 8. epilogue on the whole group
   if (a.op == OP_PLAIN) {
     for (int e = tid; e < B * 32; e += blockDim.x) {
       const int b = e >> 5, r = e & 31;
       if (b < a.batch) {
         const int64_t n = (int64_t)tr * 32 + r;
-        float v = sgrp[b * 64 + r];
+        float v = sgrp[b][r];
         if (a.residual != nullptr) v += a.residual[b * a.y_stride + n];
         a.y[b * a.y_stride + n] = v;
       }
@@ -482,7 +381,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       const int b = e >> 5, r = e & 31;
       if (b < a.batch) {
         const int64_t n = (int64_t)group * 32 + r;
-        const float gr = sgrp[b * 64 + r], ur = sgrp[b * 64 + 32 + r];
+        const float gr = sgrp[b][r], ur = sgrp[b][32 + r];
         const float g = bf16_to_f32(f32_to_bf16(gr));
         const float uu = bf16_to_f32(f32_to_bf16(ur));
         const float h = (g / (1.0f + expf(-g))) * uu;
@@ -506,11 +405,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
           hg = group - a.grp_q - a.grp_k;
           seg_off = (a.n_q_heads + a.n_kv_heads) * 64;
         }
-        const float r0 = sgrp[b * 64 + d], r1 = sgrp[b * 64 + 32 + d];
+        const float r0 = sgrp[b][d], r1 = sgrp[b][32 + d];
         if (a.raw_out != nullptr) {
-          const int64_t W = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
-          a.raw_out[b * W + seg_off + hg * 64 + d] = r0;
-          a.raw_out[b * W + seg_off + hg * 64 + 32 + d] = r1;
+          const int64_t Wd = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
+          a.raw_out[b * Wd + seg_off + hg * 64 + d] = r0;
+          a.raw_out[b * Wd + seg_off + hg * 64 + 32 + d] = r1;
         }
         const float x0 = bf16_to_f32(f32_to_bf16(r0));
         const float x1 = bf16_to_f32(f32_to_bf16(r1));
@@ -540,80 +439,54 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
 // ------------------------------------------------------------------ host side
 
-static int g_split_tiles = 0;
-
-constexpr size_t kMaxLds = 65536;
+static int g_tiles_per_wave = 0;
 
 static int round_batch(int batch) { return batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : 8; }
 
-static size_t lds_bytes(int kind, int nt, int B) {
-  return (size_t)lds_w_bytes(kind, nt) + (size_t)B * nt * kTileK * 2 + 8 * B * 32 * 4 +
-         B * 64 * 4 + 8 * B * 4 + 16;
+// K-tiles per wave: the fewest that fit the group's K into the workgroup's wave budget
+// (16 waves for batch <= 2, 8 above); 1, 2 or 4.
+static int plan_tpw(int G, int k_t, int batch) {
+  const int max_waves = round_batch(batch) <= 2 ? kMaxWaves : kMaxWaves / 2;
+  int tpw = g_tiles_per_wave > 0 ? g_tiles_per_wave : (G * k_t + max_waves - 1) / max_waves;
+  tpw = tpw <= 1 ? 1 : tpw <= 2 ? 2 : tpw <= 4 ? 4 : 0;
+  if (tpw && G * ((k_t + tpw - 1) / tpw) > max_waves) tpw = 0;
+  return tpw;  // 0: K too long for one workgroup
 }
 
-// K-tiles per workgroup. Automatic: the largest divisor of k_t (<= 8) giving >= 512
-// workgroups, else >= 256, else 1; then capped so the LDS carve-up fits in 64 KB.
-static int choose_nt(int kind, int total_rows_in_groups, int k_t, int batch) {
-  const int B = round_batch(batch);
-  int nt = 0;
-  if (g_split_tiles > 0) {
-    nt = g_split_tiles < k_t ? g_split_tiles : k_t;
-  } else {
-    for (int target : {512, 256}) {
-      for (int c = (k_t < kMaxNt ? k_t : kMaxNt); c >= 1 && nt == 0; --c) {
-        if (k_t % c) continue;
-        if ((long)total_rows_in_groups * (k_t / c) >= target) nt = c;
-      }
-      if (nt) break;
-    }
-    if (nt == 0) nt = 1;
-  }
-  if (nt > kMaxNt) nt = kMaxNt;
-  while (nt > 1 && lds_bytes(kind, nt, B) > kMaxLds) --nt;
-  return nt;
-}
-
-static size_t ws_bytes_for(int n_groups, int G, int n_split, int B) {
-  if (G == 1 && n_split == 1) return 0;
-  return (size_t)Q4NX_WS_COUNTER_BYTES + (size_t)n_groups * G * n_split * B * 32 * 4;
+template <int KIND, int B, int TPW>
+static void launch_t(const GemvArgs& a, int blocks, int threads, hipStream_t s) {
+  hipLaunchKernelGGL((gemv_kernel<KIND, B, TPW>), dim3(blocks), dim3(threads), 0, s, a);
 }
 
 template <int KIND, int B>
-static void launch_t(const GemvArgs& a, int blocks, int threads, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_kernel<KIND, B>), dim3(blocks), dim3(threads), lds, s, a);
+static void launch_b(const GemvArgs& a, int tpw, int blocks, int threads, hipStream_t s) {
+  switch (tpw) {
+    case 1: launch_t<KIND, B, 1>(a, blocks, threads, s); break;
+    case 2: launch_t<KIND, B, 2>(a, blocks, threads, s); break;
+    default: launch_t<KIND, B, 4>(a, blocks, threads, s); break;
+  }
 }
 
-static int launch(int kind, GemvArgs& a, void* ws, size_t ws_bytes, hipStream_t s,
-                  const char* what) {
+static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char* what) {
   const int B = round_batch(a.batch);
-  a.n_split = (a.k_t + a.nt - 1) / a.nt;
-  const size_t need = ws_bytes_for(a.n_groups, a.G, a.n_split, B);
-  Q4NX_REQUIRE(need == 0 || (ws != nullptr && ws_bytes >= need), Q4NX_ERR_WS,
-               "%s: workspace of %zu bytes needed, %zu given", what, need, ws_bytes);
-  Q4NX_REQUIRE(ws == nullptr || Q4NX_ALIGNED(ws, 256), Q4NX_ERR_ARG,
-               "%s: workspace must be 256-byte aligned", what);
-  if (need) {
-    Q4NX_REQUIRE((size_t)a.n_groups * 4 <= (size_t)Q4NX_WS_COUNTER_BYTES, Q4NX_ERR_SHAPE,
-                 "%s: %d output groups exceed the workspace counter region", what, a.n_groups);
-    a.counters = (unsigned*)ws;
-    a.partial = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
-  }
-  const int blocks = a.n_groups * a.G * a.n_split;
-  const int threads = ((a.nt * kLanesPerTile + 63) / 64) * 64;
-  const size_t lds = lds_bytes(kind, a.nt, B);
+  const int tpw = plan_tpw(a.G, a.k_t, a.batch);
+  Q4NX_REQUIRE(tpw > 0, Q4NX_ERR_SHAPE, "%s: K=%d is longer than one workgroup covers", what,
+               a.k_t * 256);
+  const int wm = (a.k_t + tpw - 1) / tpw;
+  const int threads = a.G * wm * 64;
   if (kind == 4) {
     switch (B) {
-      case 1: launch_t<4, 1>(a, blocks, threads, lds, s); break;
-      case 2: launch_t<4, 2>(a, blocks, threads, lds, s); break;
-      case 4: launch_t<4, 4>(a, blocks, threads, lds, s); break;
-      default: launch_t<4, 8>(a, blocks, threads, lds, s); break;
+      case 1: launch_b<4, 1>(a, tpw, n_groups, threads, s); break;
+      case 2: launch_b<4, 2>(a, tpw, n_groups, threads, s); break;
+      case 4: launch_b<4, 4>(a, tpw, n_groups, threads, s); break;
+      default: launch_b<4, 8>(a, tpw, n_groups, threads, s); break;
     }
   } else {
     switch (B) {
-      case 1: launch_t<8, 1>(a, blocks, threads, lds, s); break;
-      case 2: launch_t<8, 2>(a, blocks, threads, lds, s); break;
-      case 4: launch_t<8, 4>(a, blocks, threads, lds, s); break;
-      default: launch_t<8, 8>(a, blocks, threads, lds, s); break;
+      case 1: launch_b<8, 1>(a, tpw, n_groups, threads, s); break;
+      case 2: launch_b<8, 2>(a, tpw, n_groups, threads, s); break;
+      case 4: launch_b<8, 4>(a, tpw, n_groups, threads, s); break;
+      default: launch_b<8, 8>(a, tpw, n_groups, threads, s); break;
     }
   }
   return check_launch(what);
@@ -630,17 +503,24 @@ static int check_common(const void* w, int n_tile_rows, int k_tiles, int batch, 
   return Q4NX_OK;
 }
 
+static int check_x(const void* x, int64_t x_stride, int k_tiles, const char* what) {
+  Q4NX_REQUIRE(x != nullptr && Q4NX_ALIGNED(x, 16), Q4NX_ERR_ARG,
+               "%s: x must be a non-null 16-byte aligned device pointer", what);
+  Q4NX_REQUIRE(x_stride >= (int64_t)k_tiles * 256 && x_stride % 8 == 0, Q4NX_ERR_SHAPE,
+               "%s: x_stride=%lld must be a multiple of 8 and >= K=%d", what,
+               (long long)x_stride, k_tiles * 256);
+  return Q4NX_OK;
+}
+
 static int gemv_plain(int kind, const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows,
                       int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
-                      const float* residual, void* ws, size_t ws_bytes, void* stream,
-                      const char* what) {
+                      const float* residual, void* stream, const char* what) {
   int rc = check_common(w, n_tile_rows, k_tiles, batch, what);
   if (rc) return rc;
-  Q4NX_REQUIRE(x != nullptr && Q4NX_ALIGNED(x, 4) && y != nullptr && Q4NX_ALIGNED(y, 4),
-               Q4NX_ERR_ARG, "%s: x and y must be non-null 4-byte aligned device pointers", what);
-  Q4NX_REQUIRE(x_stride >= (int64_t)k_tiles * 256 && x_stride % 2 == 0, Q4NX_ERR_SHAPE,
-               "%s: x_stride=%lld must be even and >= K=%d", what, (long long)x_stride,
-               k_tiles * 256);
+  rc = check_x(x, x_stride, k_tiles, what);
+  if (rc) return rc;
+  Q4NX_REQUIRE(y != nullptr && Q4NX_ALIGNED(y, 4), Q4NX_ERR_ARG,
+               "%s: y must be a non-null 4-byte aligned device pointer", what);
   Q4NX_REQUIRE(y_stride >= (int64_t)n_tile_rows * 32, Q4NX_ERR_SHAPE,
                "%s: y_stride=%lld < N=%d", what, (long long)y_stride, n_tile_rows * 32);
   GemvArgs a{};
@@ -648,16 +528,14 @@ static int gemv_plain(int kind, const uint8_t* w, const uint16_t* x, float* y, i
   a.n_tr[0] = n_tile_rows;
   a.op = OP_PLAIN;
   a.G = 1;
-  a.n_groups = n_tile_rows;
   a.k_t = k_tiles;
-  a.nt = choose_nt(kind, n_tile_rows, k_tiles, batch);
   a.batch = batch;
   a.x = x;
   a.x_stride = x_stride;
   a.y = y;
   a.y_stride = y_stride;
   a.residual = residual;
-  return launch(kind, a, ws, ws_bytes, (hipStream_t)stream, what);
+  return launch(kind, a, n_tile_rows, (hipStream_t)stream, what);
 }
 
 }  // namespace q4nx
@@ -667,37 +545,38 @@ using namespace q4nx;
 extern "C" {
 
 int q4nx_set_split_tiles(int tiles) {
-  Q4NX_REQUIRE(tiles >= 0 && tiles <= kMaxNt, Q4NX_ERR_ARG, "split tiles %d outside 0..%d",
-               tiles, kMaxNt);
-  g_split_tiles = tiles;
+  Q4NX_REQUIRE(tiles == 0 || tiles == 1 || tiles == 2 || tiles == 4, Q4NX_ERR_ARG,
+               "tiles per wave must be 0 (automatic), 1, 2 or 4, got %d", tiles);
+  g_tiles_per_wave = tiles;
   return Q4NX_OK;
 }
 
+// The GEMVs reduce inside one workgroup and need no workspace; the queries stay so a
+// caller written against the workspace convention keeps working.
 size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch) {
-  if (n_tile_rows <= 0 || k_tiles <= 0 || batch < 1) return 0;
-  const int nt = choose_nt(kind, n_tile_rows, k_tiles, batch);
-  return ws_bytes_for(n_tile_rows, 1, (k_tiles + nt - 1) / nt, round_batch(batch));
+  (void)kind; (void)n_tile_rows; (void)k_tiles; (void)batch;
+  return 0;
 }
 
 int q4nx_gemv_q4(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
-  return gemv_plain(4, w, x, y, n_tile_rows, k_tiles, batch, x_stride, y_stride, residual, ws,
-                    ws_bytes, stream, "q4nx_gemv_q4");
+  (void)ws; (void)ws_bytes;
+  return gemv_plain(4, w, x, y, n_tile_rows, k_tiles, batch, x_stride, y_stride, residual,
+                    stream, "q4nx_gemv_q4");
 }
 
 int q4nx_gemv_q8(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
-  return gemv_plain(8, w, x, y, n_tile_rows, k_tiles, batch, x_stride, y_stride, residual, ws,
-                    ws_bytes, stream, "q4nx_gemv_q8");
+  (void)ws; (void)ws_bytes;
+  return gemv_plain(8, w, x, y, n_tile_rows, k_tiles, batch, x_stride, y_stride, residual,
+                    stream, "q4nx_gemv_q8");
 }
 
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {
-  if (n_q_heads <= 0 || n_kv_heads <= 0 || k_tiles <= 0 || batch < 1) return 0;
-  const int groups = n_q_heads + 2 * n_kv_heads;
-  const int nt = choose_nt(4, groups * 2, k_tiles, batch);
-  return ws_bytes_for(groups, 2, (k_tiles + nt - 1) / nt, round_batch(batch));
+  (void)n_q_heads; (void)n_kv_heads; (void)k_tiles; (void)batch;
+  return 0;
 }
 
 int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n_q_heads,
@@ -706,6 +585,7 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
                   const float* rope_tab, int max_pos, uint16_t* q_out, uint16_t* k_cache,
                   uint16_t* v_cache, int64_t kv_b_stride, int64_t kv_h_stride, float* raw_out,
                   uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
+  (void)ws; (void)ws_bytes;
   const char* what = "q4nx_qkv_rope";
   for (const void* p : {(const void*)wq, (const void*)wk, (const void*)wv}) {
     int rc = check_common(p, 2, k_tiles, batch, what);
@@ -714,10 +594,12 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
   Q4NX_REQUIRE(n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0, Q4NX_ERR_SHAPE,
                "%s: n_q_heads=%d must be a positive multiple of n_kv_heads=%d", what, n_q_heads,
                n_kv_heads);
-  Q4NX_REQUIRE(x != nullptr && Q4NX_ALIGNED(x, 8), Q4NX_ERR_ARG, "%s: x must be 8-byte aligned",
-               what);
-  Q4NX_REQUIRE(x_stride >= (int64_t)k_tiles * 256 && x_stride % 2 == 0, Q4NX_ERR_SHAPE,
-               "%s: bad x_stride", what);
+  int rc = check_x(x, x_stride, k_tiles, what);
+  if (rc) return rc;
+  Q4NX_REQUIRE(norm_w == nullptr || Q4NX_ALIGNED(norm_w, 16), Q4NX_ERR_ARG,
+               "%s: norm_w must be 16-byte aligned", what);
+  Q4NX_REQUIRE(xn_out == nullptr || Q4NX_ALIGNED(xn_out, 16), Q4NX_ERR_ARG,
+               "%s: xn_out must be 16-byte aligned", what);
   Q4NX_REQUIRE(positions && rope_tab && q_out && k_cache && v_cache, Q4NX_ERR_ARG,
                "%s: positions, rope table, q_out and caches are required", what);
   Q4NX_REQUIRE(max_pos > 0 && kv_h_stride >= (int64_t)max_pos * 64 &&
@@ -734,9 +616,7 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
   a.G = 2;
   a.grp_q = n_q_heads;
   a.grp_k = n_kv_heads;
-  a.n_groups = n_q_heads + 2 * n_kv_heads;
   a.k_t = k_tiles;
-  a.nt = choose_nt(4, a.n_groups * 2, k_tiles, batch);
   a.batch = batch;
   if (norm_w) {
     a.hres = (const float*)x;
@@ -758,28 +638,31 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
   a.n_q_heads = n_q_heads;
   a.n_kv_heads = n_kv_heads;
   a.raw_out = raw_out;
-  return launch(4, a, ws, ws_bytes, (hipStream_t)stream, what);
+  return launch(4, a, n_q_heads + 2 * n_kv_heads, (hipStream_t)stream, what);
 }
 
 size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch) {
-  if (n_tile_rows <= 0 || k_tiles <= 0 || batch < 1) return 0;
-  const int nt = choose_nt(4, n_tile_rows * 2, k_tiles, batch);
-  return ws_bytes_for(n_tile_rows, 2, (k_tiles + nt - 1) / nt, round_batch(batch));
+  (void)n_tile_rows; (void)k_tiles; (void)batch;
+  return 0;
 }
 
 int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, int k_tiles,
                         const void* x, int64_t x_stride, const uint16_t* norm_w, float eps,
                         int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
                         uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
+  (void)ws; (void)ws_bytes;
   const char* what = "q4nx_gate_up_swiglu";
   for (const void* p : {(const void*)wg, (const void*)wu}) {
     int rc = check_common(p, n_tile_rows, k_tiles, batch, what);
     if (rc) return rc;
   }
-  Q4NX_REQUIRE(x != nullptr && Q4NX_ALIGNED(x, 8) && h_out != nullptr, Q4NX_ERR_ARG,
-               "%s: x (8-byte aligned) and h_out are required", what);
-  Q4NX_REQUIRE(x_stride >= (int64_t)k_tiles * 256 && x_stride % 2 == 0, Q4NX_ERR_SHAPE,
-               "%s: bad x_stride", what);
+  int rc = check_x(x, x_stride, k_tiles, what);
+  if (rc) return rc;
+  Q4NX_REQUIRE(norm_w == nullptr || Q4NX_ALIGNED(norm_w, 16), Q4NX_ERR_ARG,
+               "%s: norm_w must be 16-byte aligned", what);
+  Q4NX_REQUIRE(xn_out == nullptr || Q4NX_ALIGNED(xn_out, 16), Q4NX_ERR_ARG,
+               "%s: xn_out must be 16-byte aligned", what);
+  Q4NX_REQUIRE(h_out != nullptr, Q4NX_ERR_ARG, "%s: h_out is required", what);
   Q4NX_REQUIRE(h_stride >= (int64_t)n_tile_rows * 32, Q4NX_ERR_SHAPE, "%s: bad h_stride", what);
   GemvArgs a{};
   a.w[0] = wg;
@@ -788,9 +671,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
   a.n_tr[1] = n_tile_rows;
   a.op = OP_GATEUP;
   a.G = 2;
-  a.n_groups = n_tile_rows;
   a.k_t = k_tiles;
-  a.nt = choose_nt(4, n_tile_rows * 2, k_tiles, batch);
   a.batch = batch;
   if (norm_w) {
     a.hres = (const float*)x;
@@ -804,7 +685,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
   a.h_out = h_out;
   a.h_stride = h_stride;
   a.raw_out = raw_out;
-  return launch(4, a, ws, ws_bytes, (hipStream_t)stream, what);
+  return launch(4, a, n_tile_rows, (hipStream_t)stream, what);
 }
 
 }  // extern "C"
