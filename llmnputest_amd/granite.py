@@ -1,0 +1,284 @@
+"""A granite-3B-shaped decode step on one MI355X, built from the q4nx HIP ops.
+
+The reference validates every op of granite-4.2-3B on the NPU but strings none of them
+into a forward pass (README.md:295-311); this module is that token loop. Per layer the
+step issues five launches, grouped the way designs/granite_gemv/granite_layer.py:54-59
+groups the projections by shared input:
+
+    [RMSNorm, q, k, v, RoPE, KV append]   q4nx_qkv_rope (norm fused as the prologue)
+    [GQA flash-decode attention]          q4nx_gqa_decode
+    [o, residual add]                     q4nx_gemv_q4 (residual epilogue, in place)
+    [RMSNorm, gate, up, SwiGLU]           q4nx_gate_up_swiglu (norm fused)
+    [down, residual add]                  q4nx_gemv_q4
+
+then the final RMSNorm, the tied q8 lm_head GEMV and a device-side argmax. A whole step
+is captured once in a HIP graph and replayed; the greedy loop never leaves the device.
+
+Conventions (the reference fixes none of them): fp32 residual stream, pre-norm
+Llama/Granite order, final RMSNorm, tied q8 lm_head whose dequantised row t is the
+embedding of token t, KV cache bf16 [B][Hkv][L][64] per layer.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import ops
+from .q4nx import Q4_TILE_BYTES, Q8_TILE_BYTES, Q4NX, check_stored_shape, projection_shape
+
+
+@dataclass(frozen=True)
+class GraniteConfig:
+    """granite-4.2-3B shapes (README.md:160-161; designs/granite_gemv/granite_gemv.py:6-9)."""
+    hidden: int = 2560
+    inter: int = 8192
+    n_layers: int = 40
+    n_q: int = 40
+    n_kv: int = 8
+    head_dim: int = 64
+    vocab: int = 100352
+    eps: float = 1e-5
+    theta: float = 10000.0
+    scale: float = 0.125        # head_dim ** -0.5 (designs/granite_gemv/granite_attention.h:28-34)
+
+    @property
+    def q_dim(self) -> int:
+        return self.n_q * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv * self.head_dim
+
+    def layer_bytes(self) -> int:
+        """q4 tile bytes of one layer's seven projections."""
+        h, i, q, kv = self.hidden, self.inter, self.q_dim, self.kv_dim
+        elems = q * h + 2 * kv * h + h * q + 3 * h * i
+        return elems // 2 + elems // 32 * 4     # 4 bits per weight + bf16 d, m per 32
+
+    def lm_head_bytes(self) -> int:
+        return (self.vocab // 32) * (self.hidden // 256) * Q8_TILE_BYTES
+
+
+@dataclass
+class GraniteWeights:
+    """Device tensors: raw q4nx tiles (uint8) per projection, bf16 norm weights."""
+    cfg: GraniteConfig
+    layers: list = field(default_factory=list)   # dicts: q k v o gate up down norm_in norm_post
+    norm_final: torch.Tensor | None = None
+    lm_head: torch.Tensor | None = None           # q8 tiles, [vocab, hidden]
+
+    # ------------------------------------------------------------ synthetic
+    @staticmethod
+    def synthetic(cfg: GraniteConfig, seed: int = 0, device="cuda") -> "GraniteWeights":
+        """Random-init weights of the granite architecture in q4nx tiles, generated on the
+        device from a seeded generator (Q4_1 with d = bf16(|N|*0.02), m = -8d; q8 lm_head
+        with s = bf16(|N|*0.01); norm weights bf16(1 + 0.1 N))."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        w = GraniteWeights(cfg)
+        h, i = cfg.hidden, cfg.inter
+        for _ in range(cfg.n_layers):
+            w.layers.append({
+                "q": random_q4_tiles(cfg.q_dim, h, g, device),
+                "k": random_q4_tiles(cfg.kv_dim, h, g, device),
+                "v": random_q4_tiles(cfg.kv_dim, h, g, device),
+                "o": random_q4_tiles(h, cfg.q_dim, g, device),
+                "gate": random_q4_tiles(i, h, g, device),
+                "up": random_q4_tiles(i, h, g, device),
+                "down": random_q4_tiles(h, i, g, device),
+                "norm_in": random_norm(h, g, device),
+                "norm_post": random_norm(h, g, device),
+            })
+        w.norm_final = random_norm(h, g, device)
+        w.lm_head = random_q8_tiles(cfg.vocab, h, g, device)
+        return w
+
+    # ------------------------------------------------------------ real files
+    @staticmethod
+    def from_q4nx(path, cfg: GraniteConfig, device="cuda") -> "GraniteWeights":
+        """Load a granite `.q4nx` file: raw tiles straight to the device, (N, K) from the
+        config and checked against the stored shape (granite_gemv.py:90-102, 282-288)."""
+        f = Q4NX(path)
+        hf_cfg = {"hidden_size": cfg.hidden, "intermediate_size": cfg.inter,
+                  "num_attention_heads": cfg.n_q, "num_key_value_heads": cfg.n_kv,
+                  "head_dim": cfg.head_dim, "vocab_size": cfg.vocab}
+
+        def tiles(name, want_kind):
+            n, k = projection_shape(name, hf_cfg)
+            check_stored_shape(f.header[name]["shape"], n, k)
+            kind, b = f.tiles(name)
+            if kind != want_kind:
+                raise ValueError(f"{name}: stored as {kind}, this decoder expects {want_kind}")
+            return torch.from_numpy(np.ascontiguousarray(b).reshape(-1)).to(device)
+
+        def norm(name):
+            return torch.from_numpy(f.plain(name).astype(np.uint16).view(np.int16).copy()).to(device).view(torch.bfloat16)
+
+        w = GraniteWeights(cfg)
+        for li in range(cfg.n_layers):
+            p = f"model.layers.{li}."
+            w.layers.append({
+                "q": tiles(p + "self_attn.q_proj.weight", "q4"),
+                "k": tiles(p + "self_attn.k_proj.weight", "q4"),
+                "v": tiles(p + "self_attn.v_proj.weight", "q4"),
+                "o": tiles(p + "self_attn.o_proj.weight", "q4"),
+                "gate": tiles(p + "mlp.gate_proj.weight", "q4"),
+                "up": tiles(p + "mlp.up_proj.weight", "q4"),
+                "down": tiles(p + "mlp.down_proj.weight", "q4"),
+                "norm_in": norm(p + "input_layernorm.weight"),
+                "norm_post": norm(p + "post_attention_layernorm.weight"),
+            })
+        w.norm_final = norm("model.norm.weight")
+        w.lm_head = tiles("lm_head.weight", "q8")
+        return w
+
+
+def random_q4_tiles(n: int, k: int, gen: torch.Generator, device) -> torch.Tensor:
+    """q4 tiles [n/32 * k/256 * 5120] uint8: uniform nibbles, d = bf16(|N|*0.02), m = bf16(-8d)."""
+    t = (n // 32) * (k // 256)
+    w = torch.randint(0, 256, (t, Q4_TILE_BYTES), dtype=torch.uint8, device=device, generator=gen)
+    d = (torch.randn((t, 256), device=device, generator=gen).abs() * 0.02).to(torch.bfloat16)
+    m = (d.float() * -8.0).to(torch.bfloat16)
+    w[:, 0:512] = d.view(torch.uint8).reshape(t, 512)
+    w[:, 512:1024] = m.view(torch.uint8).reshape(t, 512)
+    return w.reshape(-1)
+
+
+def random_q8_tiles(n: int, k: int, gen: torch.Generator, device) -> torch.Tensor:
+    """q8 tiles: int8 codes uniform in [-127, 127], s = bf16(|N|*0.01)."""
+    t = (n // 32) * (k // 256)
+    w = torch.empty((t, Q8_TILE_BYTES), dtype=torch.uint8, device=device)
+    w[:, 512:] = torch.randint(-127, 128, (t, 8192), dtype=torch.int8, device=device,
+                               generator=gen).view(torch.uint8)
+    s = (torch.randn((t, 256), device=device, generator=gen).abs() * 0.01).to(torch.bfloat16)
+    w[:, 0:512] = s.view(torch.uint8).reshape(t, 512)
+    return w.reshape(-1)
+
+
+def random_norm(n: int, gen: torch.Generator, device) -> torch.Tensor:
+    return (1.0 + 0.1 * torch.randn(n, device=device, generator=gen)).to(torch.bfloat16)
+
+
+class GraniteDecoder:
+    """Decode state for up to `max_batch` sequences of up to `max_len` positions.
+
+    `step()` runs one token for every sequence at its own position; `generate()` runs the
+    greedy loop on the device from a HIP graph of one step."""
+
+    def __init__(self, weights: GraniteWeights, max_batch: int = 1, max_len: int = 4096,
+                 device="cuda"):
+        c = weights.cfg
+        self.cfg, self.w = c, weights
+        self.dev = torch.device(device)
+        self.max_batch = max_batch
+        self.max_len = (max_len + 63) // 64 * 64
+        b, dev = max_batch, self.dev
+        kv_shape = (b, c.n_kv, self.max_len, c.head_dim)
+        self.k_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.n_layers)]
+        self.v_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.n_layers)]
+        self.rope = ops.rope_table(self.max_len, c.head_dim, c.theta, device=dev)
+        self.h = torch.zeros((b, c.hidden), dtype=torch.float32, device=dev)
+        self.q = torch.zeros((b, c.q_dim), dtype=torch.bfloat16, device=dev)
+        self.attn = torch.zeros((b, c.n_q, c.head_dim), dtype=torch.bfloat16, device=dev)
+        self.mlp = torch.zeros((b, c.inter), dtype=torch.bfloat16, device=dev)
+        self.hf = torch.zeros((b, c.hidden), dtype=torch.bfloat16, device=dev)
+        self.logits = torch.zeros((b, c.vocab), dtype=torch.float32, device=dev)
+        self.tokens = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.lens = torch.ones(b, dtype=torch.int32, device=dev)
+        self.ws = ops.Workspace(ops.WS_COUNTER_BYTES + (64 << 20), device=dev)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.graph_batch = 0
+        self.calls = 0
+        self.seconds = 0.0
+
+    # ------------------------------------------------------------ one step, eager
+    def _launch_step(self, b: int) -> None:
+        """Every kernel of one decode step for the first b sequences (no allocation)."""
+        c, w = self.cfg, self.w
+        kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
+        h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
+        ops.embed_q8(w.lm_head, self.tokens[:b], c.vocab, c.hidden, out=h)
+        self.lens[:b].copy_(self.pos[:b] + 1)
+        for li, L in enumerate(w.layers):
+            kc, vc = self.k_cache[li], self.v_cache[li]
+            ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
+                         kc, vc, q_out=q, norm_w=L["norm_in"], eps=c.eps, ws=self.ws)
+            ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
+                           max_len=self.max_len, out=attn, ws=self.ws)
+            ops.gemv(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q, residual=h,
+                     out=h, ws=self.ws)
+            ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
+                               norm_w=L["norm_post"], eps=c.eps, ws=self.ws)
+            ops.gemv(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h, ws=self.ws)
+        ops.rmsnorm(h, w.norm_final, c.eps, out=self.hf[:b])
+        ops.gemv(w.lm_head, "q8", self.hf[:b], c.vocab // 32, kt_h, out=self.logits[:b], ws=self.ws)
+
+    def step(self, tokens, positions) -> torch.Tensor:
+        """One decode step, eager: tokens/positions for B sequences -> fp32 logits [B, V]."""
+        tokens = torch.as_tensor(tokens, dtype=torch.int32).reshape(-1)
+        positions = torch.as_tensor(positions, dtype=torch.int32).reshape(-1)
+        b = tokens.numel()
+        if b > self.max_batch or positions.numel() != b:
+            raise ValueError("batch exceeds max_batch or positions do not match tokens")
+        if int(positions.max()) >= self.max_len or int(positions.min()) < 0:
+            raise ValueError(f"positions must be in [0, {self.max_len})")
+        self.tokens[:b].copy_(tokens)
+        self.pos[:b].copy_(positions)
+        self._launch_step(b)
+        return self.logits[:b]
+
+    # ------------------------------------------------------------ graph + greedy loop
+    def capture(self, b: int) -> None:
+        """Capture one greedy step for b sequences: kernels, argmax into `tokens`, pos += 1."""
+        self._launch_step(b)                       # warm: sizes every workspace
+        ops.argmax(self.logits[:b], out=self.tokens[:b])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._launch_step(b)
+            ops.argmax(self.logits[:b], out=self.tokens[:b])
+            self.pos[:b].add_(1)
+        self.graph, self.graph_batch = g, b
+
+    def generate(self, first_tokens, start_pos, n_new: int, record_logits: bool = False):
+        """Greedy decode of n_new tokens for B sequences from `first_tokens` at `start_pos`.
+        Returns (tokens [B, n_new] int32 on the host, per-step logits list or None)."""
+        first = torch.as_tensor(first_tokens, dtype=torch.int32).reshape(-1)
+        start = torch.as_tensor(start_pos, dtype=torch.int32).reshape(-1)
+        b = first.numel()
+        if int(start.max()) + n_new > self.max_len:
+            raise ValueError("max_len too small for this many new tokens")
+        if self.graph is None or self.graph_batch != b:
+            self.pos[:b].copy_(start)
+            self.tokens[:b].copy_(first)
+            self.capture(b)
+        self.tokens[:b].copy_(first)
+        self.pos[:b].copy_(start)
+        out = torch.empty((n_new, b), dtype=torch.int32, device=self.dev)
+        logs = [] if record_logits else None
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n_new):
+            self.graph.replay()
+            out[i].copy_(self.tokens[:b])
+            if record_logits:
+                logs.append(self.logits[:b].clone())
+        torch.cuda.synchronize()
+        self.seconds += time.perf_counter() - t0
+        self.calls += n_new
+        return out.t().contiguous().cpu().numpy(), logs
+
+    def seed_cache(self, ctx: int, seed: int = 0) -> None:
+        """Fill positions [0, ctx) of every layer's K/V cache with bf16 N(0,1) (a synthetic
+        context; no prefill runs through the model)."""
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(seed)
+        for kc, vc in zip(self.k_cache, self.v_cache):
+            for t in (kc, vc):
+                t.zero_()
+                t[:, :, :ctx] = torch.randn(t[:, :, :ctx].shape, device=self.dev, generator=g).to(torch.bfloat16)

@@ -124,7 +124,7 @@ def set_split_tiles(tiles_per_workgroup: int) -> None:
 # ---------------------------------------------------------------- elementwise
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5,
-            want_f32: bool = False):
+            want_f32: bool = False, out: torch.Tensor | None = None):
     """bf16 RMSNorm of x (bf16 or fp32, [C] or [B, C]); returns y or (y, y_f32)."""
     _dev(x, "x")
     _dev(w, "w", torch.bfloat16)
@@ -132,7 +132,8 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5,
         raise TypeError("x must be bfloat16 or float32")
     cols = x.shape[-1]
     b = x.numel() // cols
-    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _dev(y, "out", torch.bfloat16)
     yf = torch.empty(x.shape, dtype=torch.float32, device=x.device) if want_f32 else None
     _lib.call("q4nx_rmsnorm", _ptr(x), int(x.dtype == torch.float32), _ptr(w), _ptr(y),
               _ptr(yf), cols, b, float(eps), _stream())

@@ -38,20 +38,23 @@ static void tile_row(const job_t *j, int tr) {
     for (int rb = 0; rb < 2; ++rb)
       for (int k = 0; k < 256; ++k) {
         const int kb = k >> 5;
+        float wv[16];
         for (int r = 0; r < 16; ++r) {
           const int g = kb * 32 + rb * 16 + r;
-          float wv;
           if (j->kind == 4) {
             const int i = rb * 4096 + k * 16 + r;
             const uint8_t byte = t[1024 + (i >> 1)];
             const int code = (i & 1) ? (byte >> 4) : (byte & 15);
-            wv = (float)code * bf16f(t + 2 * g) + bf16f(t + 512 + 2 * g);
+            wv[r] = (float)code * bf16f(t + 2 * g) + bf16f(t + 512 + 2 * g);
           } else {
             const int code = (int8_t)t[512 + rb * 4096 + k * 16 + r];
-            wv = (float)code * bf16f(t + 2 * g);
+            wv[r] = (float)code * bf16f(t + 2 * g);
           }
-          for (int b = 0; b < j->batch; ++b)
-            acc[b][rb * 16 + r] += (double)wv * (double)j->x[(size_t)b * K + kt * 256 + k];
+        }
+        for (int b = 0; b < j->batch; ++b) {
+          const double xk = (double)j->x[(size_t)b * K + kt * 256 + k];
+          double *a = acc[b] + rb * 16;
+          for (int r = 0; r < 16; ++r) a[r] += (double)wv[r] * xk;
         }
       }
   }

@@ -191,12 +191,15 @@ class DecodeOracle:
     float32 reference with bf16 narrowing at the same points as the GPU path; slow,
     meant for reduced layer counts in tests."""
 
-    def __init__(self, w: DecodeWeights, k_cache: list, v_cache: list, max_pos: int):
+    def __init__(self, w: DecodeWeights, k_cache: list, v_cache: list, max_pos: int,
+                 gemv=None):
         self.w = w
         self.cfg = w.cfg
         self.k_cache = k_cache      # per layer: bf16 bits [B, Hkv, Lmax, hd]
         self.v_cache = v_cache
         self.table = rope_table(max_pos, self.cfg.head_dim, self.cfg.theta)
+        # float64 GEMV from tile bytes: the numpy restatement, or the equal C one
+        self.gemv = gemv or (lambda raw, kind, x, n_t, k_t: qo.gemv(raw, kind, x, n_t, k_t, acc=np.float64))
 
     def step(self, tokens, pos) -> np.ndarray:
         """One decode step for B sequences at positions pos[b]; returns fp32 logits [B, V]
@@ -212,9 +215,9 @@ class DecodeOracle:
         h = embed_rows(w.lm_head, tokens, c.vocab, c.hidden).astype(np.float32)
         for layer in range(c.n_layers):
             xn = qo.bf16_round(rmsnorm(h, w.norm_in[layer], c.eps).astype(np.float32))
-            q_raw = qo.gemv(w.wq[layer], "q4", xn, c.n_q * c.head_dim // 32, kt_h)
-            k_raw = qo.gemv(w.wk[layer], "q4", xn, c.n_kv * c.head_dim // 32, kt_h)
-            v_raw = qo.gemv(w.wv[layer], "q4", xn, c.n_kv * c.head_dim // 32, kt_h)
+            q_raw = self.gemv(w.wq[layer], "q4", xn, c.n_q * c.head_dim // 32, kt_h)
+            k_raw = self.gemv(w.wk[layer], "q4", xn, c.n_kv * c.head_dim // 32, kt_h)
+            v_raw = self.gemv(w.wv[layer], "q4", xn, c.n_kv * c.head_dim // 32, kt_h)
             qr, kr, vr = qkv_rope_from_raw(q_raw.reshape(b_n, -1), k_raw.reshape(b_n, -1),
                                            v_raw.reshape(b_n, -1), pos, self.table, c.head_dim)
             qb = qo.bf16_round(qr.astype(np.float32))
@@ -228,13 +231,13 @@ class DecodeOracle:
             att = gqa_attention(qo.bf16_to_f32(qb), qo.bf16_to_f32(kc), qo.bf16_to_f32(vc),
                                 lens, c.scale)
             ab = qo.bf16_round(att.astype(np.float32).reshape(b_n, -1))
-            o = qo.gemv(w.wo[layer], "q4", ab, c.hidden // 32, kt_q)
-            h = (h + o.reshape(b_n, -1)).astype(np.float32)
+            o = self.gemv(w.wo[layer], "q4", ab, c.hidden // 32, kt_q)
+            h = (h + o.reshape(b_n, -1)).astype(np.float32)   # fp32 residual add
             xn2 = qo.bf16_round(rmsnorm(h, w.norm_post[layer], c.eps).astype(np.float32))
-            g_raw = qo.gemv(w.wg[layer], "q4", xn2, c.inter // 32, kt_h)
-            u_raw = qo.gemv(w.wu[layer], "q4", xn2, c.inter // 32, kt_h)
+            g_raw = self.gemv(w.wg[layer], "q4", xn2, c.inter // 32, kt_h)
+            u_raw = self.gemv(w.wu[layer], "q4", xn2, c.inter // 32, kt_h)
             m = qo.bf16_round(swiglu_from_raw(g_raw, u_raw).astype(np.float32)).reshape(b_n, -1)
-            dn = qo.gemv(w.wd[layer], "q4", m, c.hidden // 32, kt_i)
+            dn = self.gemv(w.wd[layer], "q4", m, c.hidden // 32, kt_i)
             h = (h + dn.reshape(b_n, -1)).astype(np.float32)
         hf = qo.bf16_round(rmsnorm(h, w.norm_final, c.eps).astype(np.float32))
-        return qo.gemv(w.lm_head, "q8", hf, c.vocab // 32, kt_h).reshape(b_n, -1)
+        return self.gemv(w.lm_head, "q8", hf, c.vocab // 32, kt_h).reshape(b_n, -1)
