@@ -30,6 +30,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from llmnputest_amd import ops  # noqa: E402
+from llmnputest_amd.granite import GraniteConfig, GraniteDecoder, GraniteWeights  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 HIDDEN, INTER = 2560, 8192
@@ -112,6 +113,74 @@ def gemv_bench(steps: int, warmup: int, rot: int, dev) -> dict:
     }
 
 
+def decode_bytes_per_token(cfg: GraniteConfig, ctx: int, n_new: int) -> float:
+    """Algorithmic HBM bytes of one decode step, averaged over the generated positions:
+    every weight tile once, the K/V cache up to the current position (read) plus one
+    appended row, norm weights, the embedding row and the logits."""
+    mean_len = ctx + (n_new + 1) / 2.0
+    kv = cfg.n_layers * cfg.n_kv * cfg.head_dim * 2 * 2 * (mean_len + 1)
+    norms = (2 * cfg.n_layers + 1) * cfg.hidden * 2
+    return (cfg.n_layers * cfg.layer_bytes() + cfg.lm_head_bytes() + kv + norms
+            + cfg.hidden * 4 + cfg.vocab * 4)
+
+
+def decode_bench(ctx: int, n_new: int, dev, cpu_tokens: int) -> dict:
+    cfg = GraniteConfig()
+    w = GraniteWeights.synthetic(cfg, seed=5, device=dev)
+    dec = GraniteDecoder(w, max_batch=1, max_len=ctx + n_new, device=dev)
+    dec.seed_cache(ctx, seed=6)
+    first = int(np.random.default_rng(7).integers(0, cfg.vocab))
+    dec.generate([first], [ctx], 4)                     # capture + warm
+    dec.seed_cache(ctx, seed=6)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    toks, _ = dec.generate([first], [ctx], n_new)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3
+    bpt = decode_bytes_per_token(cfg, ctx, n_new)
+    out = {"tok_s": n_new / sec, "ms_per_token": sec / n_new * 1e3,
+           "bytes_per_token": int(bpt), "gbs": bpt * n_new / sec / 1e9, "ctx": ctx,
+           "new_tokens": n_new}
+    if cpu_tokens > 0:
+        out["cpu"] = decode_cpu_baseline(w, dec, first, ctx, toks[0], cpu_tokens)
+    return out
+
+
+def decode_cpu_baseline(w, dec, first, ctx, gpu_tokens, n_tok: int) -> dict | None:
+    """The CPU oracle's decode step (C float64 GEMVs from the same tiles + numpy for the
+    rest) on this host, timed over a few teacher-forced tokens of the same workload."""
+    try:
+        from oracle import cpu_oracle
+        from oracle import decode_oracle as do
+    except Exception as e:  # pragma: no cover
+        print(f"cpu decode baseline unavailable: {e}", file=sys.stderr)
+        return None
+    c = w.cfg
+    bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    hw = do.DecodeWeights(do.DecodeConfig(n_layers=c.n_layers))
+    for L in w.layers:
+        for key, dst in (("q", hw.wq), ("k", hw.wk), ("v", hw.wv), ("o", hw.wo),
+                         ("gate", hw.wg), ("up", hw.wu), ("down", hw.wd)):
+            dst.append(L[key].cpu().numpy().reshape(-1, 5120))
+        hw.norm_in.append(bits(L["norm_in"]))
+        hw.norm_post.append(bits(L["norm_post"]))
+    hw.norm_final = bits(w.norm_final)
+    hw.lm_head = w.lm_head.cpu().numpy().reshape(-1, 8704)
+    dec.seed_cache(ctx, seed=6)
+    oracle = do.DecodeOracle(hw, [bits(t) for t in dec.k_cache], [bits(t) for t in dec.v_cache],
+                             dec.max_len, gemv=cpu_oracle.gemv)
+    toks = [first] + [int(t) for t in gpu_tokens]
+    s = time.perf_counter()
+    for i in range(n_tok):
+        oracle.step([toks[i]], [ctx + i])
+    sec = (time.perf_counter() - s) / n_tok
+    return {"value": round(1.0 / sec, 4), "unit": "tok/s", "cores": cpu_oracle.host_threads(),
+            "kind": "port", "sample": f"{n_tok} decode steps of the same 40-layer workload, "
+                                      f"float64 C GEMVs + numpy"}
+
+
 def cpu_baseline(sample_iters: int) -> dict | None:
     """The reference's own CPU GEMV (designs/granite_gemv/cpu_baseline.cpp, built from its
     source into oracle/_ref/) on the same shapes, all host cores; else the C port."""
@@ -161,6 +230,10 @@ def main() -> int:
     ap.add_argument("--rot", type=int, default=16, help="distinct layers rotated per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=400)
+    ap.add_argument("--ctx", type=int, default=2048, help="decode context length")
+    ap.add_argument("--new-tokens", type=int, default=128)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-decode-tokens", type=int, default=2)
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -176,6 +249,9 @@ def main() -> int:
 
     r = gemv_bench(a.steps, a.warmup, a.rot, dev)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
+    dec = None
+    if not a.no_decode:
+        dec = decode_bench(a.ctx, a.new_tokens, dev, 0 if a.no_cpu else a.cpu_decode_tokens)
     gbs = r["gbs"]
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) + decode tok/s, granite-3B shape, batch 1",
@@ -212,6 +288,17 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    if dec is not None:
+        line["decode"] = {
+            "workload": f"granite-3B-shaped decode, 40 layers q4nx q4 + q8 lm_head 2560->100352, "
+                        f"batch 1, context {dec['ctx']}, {dec['new_tokens']} greedy tokens",
+            "tok_s": round(dec["tok_s"], 1),
+            "ms_per_token": round(dec["ms_per_token"], 4),
+            "bytes_per_token": dec["bytes_per_token"],
+            "GB/s": round(dec["gbs"], 1),
+            "roofline_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+            "cpu_baseline": dec.get("cpu"),
+        }
     print(json.dumps(line), flush=True)
     return 0
 

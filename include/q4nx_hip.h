@@ -78,8 +78,21 @@ int q4nx_gemv_q8(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
                  int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
                  const float *residual, void *ws, size_t ws_bytes, void *stream);
 
-/* Tuning knob: tiles of K per workgroup (1..8), 0 = automatic. Process-wide. */
-int q4nx_set_split_tiles(int tiles_per_workgroup);
+/* General form of the two above: y = residual + W * f(x), where f is the identity on a
+ * bf16 x, or, when norm_w != NULL, RMSNorm(x; norm_w, eps) of an fp32 x rounded to bf16
+ * in the prologue (granite_rmsnorm.h:45-80 fused into the GEMV). kind is Q4NX_KIND_Q4 or
+ * Q4NX_KIND_Q8. argmax_keys (optional, uint64 [batch][n_tile_rows]) receives for every
+ * tile-row an order-preserving key of (max y over its 32 rows, first such row);
+ * q4nx_decode_advance reduces them. y may be NULL when only the keys are wanted. No
+ * reference counterpart for the fusions: the reference runs the final norm and argmax
+ * on the host (chat.py:74-78 through transformers' generate). */
+int q4nx_gemv_ex(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const void *x,
+                 int64_t x_stride, const uint16_t *norm_w, float eps, int batch, float *y,
+                 int64_t y_stride, const float *residual, uint64_t *argmax_keys,
+                 void *stream);
+
+/* Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
+int q4nx_set_split_tiles(int tiles_per_wave);
 
 /* ---------------------------------------------------------------- elementwise
  * RMSNorm y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, bf16 out (+ optional fp32
@@ -159,6 +172,12 @@ int q4nx_embed_q8(const uint8_t *w, const int32_t *tokens, float *h, int vocab,
 /* idx[b] = argmax_n logits[b][n] (first maximum), max[b] its value (optional). */
 int q4nx_argmax(const float *logits, int n, int batch, int64_t stride, int32_t *idx,
                 float *max_val, void *stream);
+/* Greedy-loop bookkeeping in one small launch: tokens[b] = the row whose key is the
+ * largest of keys[b][0..n_slots) (from q4nx_gemv_ex), pos[b] += 1, lens[b] = pos[b] + 1,
+ * history[step][b] = tokens[b] while step < history_len; then step += 1. */
+int q4nx_decode_advance(const uint64_t *keys, int n_slots, int32_t *tokens, int32_t *pos,
+                        int32_t *lens, int32_t *history, int32_t *step, int history_len,
+                        int batch, void *stream);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,8 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_gemv_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
     "q4nx_gemv_q4": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_p]),
     "q4nx_gemv_q8": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_p]),
+    "q4nx_gemv_ex": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_i, c_p, c_i64, c_p, c_p,
+                           c_p]),
     "q4nx_set_split_tiles": (c_i, [c_i]),
     "q4nx_rmsnorm": (c_i, [c_p, c_i, c_p, c_p, c_p, c_i, c_i, c_f, c_p]),
     "q4nx_rope": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_i, c_p]),
@@ -44,6 +46,7 @@ SIGNATURES: dict[str, tuple] = {
                               c_i64, c_f, c_i, c_p, c_sz, c_p]),
     "q4nx_embed_q8": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
     "q4nx_argmax": (c_i, [c_p, c_i, c_i, c_i64, c_p, c_p, c_p]),
+    "q4nx_decode_advance": (c_i, [c_p, c_i, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p]),
 }
 
 _lib = None

@@ -33,6 +33,8 @@ struct AttnArgs {
 
 typedef short bf16x2_t __attribute__((ext_vector_type(2)));
 
+constexpr int kSplitChunk = 16;   // splits merged per LDS pass
+
 __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                         __builtin_bit_cast(bf16x2_t, b), c, false);
@@ -43,6 +45,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
   __shared__ float s_m[4][G], s_l[4][G];
   __shared__ float s_acc[4][G][64];
   __shared__ float s_fin[G][66];
+  __shared__ float s_part[kSplitChunk * G * 66];
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -80,53 +83,65 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
   const uint16_t* kbase = a.k + (size_t)b * a.kv_b_stride + (size_t)kvh * a.kv_h_stride + dg * 16;
   const uint16_t* vbase = a.v + (size_t)b * a.kv_b_stride + (size_t)kvh * a.kv_h_stride + dg * 16;
 
-  for (int t0 = start + wave * 16; t0 < end; t0 += 64) {
-    const int t = t0 + tl;
-    const bool valid = t < end;
-    uint4 k0 = make_uint4(0, 0, 0, 0), k1 = k0, v0 = k0, v1 = k0;
-    if (valid) {
-      const uint4* kp = (const uint4*)(kbase + (size_t)t * 64);
-      const uint4* vp = (const uint4*)(vbase + (size_t)t * 64);
-      k0 = kp[0];
-      k1 = kp[1];
-      v0 = vp[0];
-      v1 = vp[1];
-    }
-    const uint32_t kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-    float s[G];
+  // Two 16-position steps per trip, both steps' K/V loads issued before any arithmetic.
+  for (int t0 = start + wave * 16; t0 < end; t0 += 128) {
+    uint4 kk4[2][2], vv4[2][2];
+    bool valid[2];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float d = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) d = dot2bf(qv[h][i], kk[i], d);
-      d += __shfl_xor(d, 1);
-      d += __shfl_xor(d, 2);
-      s[h] = valid ? d * a.scale_l2 : -INFINITY;
-    }
-    const uint32_t vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    float vf[16];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      vf[2 * i] = bf16lo(vv[i]);
-      vf[2 * i + 1] = bf16hi(vv[i]);
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float bm = s[h];
-#pragma unroll
-      for (int o = 4; o < 64; o <<= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
-      const float mn = fmaxf(m[h], bm);
-      if (mn != m[h]) {  // wave-uniform: rescale what is accumulated
-        const float corr = (m[h] == -INFINITY) ? 0.f : exp2f(m[h] - mn);
-        l[h] *= corr;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[h][i] *= corr;
-        m[h] = mn;
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + u * 64 + tl;
+      valid[u] = t < end;
+      kk4[u][0] = kk4[u][1] = vv4[u][0] = vv4[u][1] = make_uint4(0, 0, 0, 0);
+      if (valid[u]) {
+        const uint4* kp = (const uint4*)(kbase + (size_t)t * 64);
+        const uint4* vp = (const uint4*)(vbase + (size_t)t * 64);
+        kk4[u][0] = kp[0];
+        kk4[u][1] = kp[1];
+        vv4[u][0] = vp[0];
+        vv4[u][1] = vp[1];
       }
-      const float p = (s[h] == -INFINITY) ? 0.f : exp2f(s[h] - m[h]);
-      l[h] += p;
+    }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
+    for (int u = 0; u < 2; ++u) {
+      if (t0 + u * 64 >= end) break;   // wave-uniform
+      const uint32_t kk[8] = {kk4[u][0].x, kk4[u][0].y, kk4[u][0].z, kk4[u][0].w,
+                              kk4[u][1].x, kk4[u][1].y, kk4[u][1].z, kk4[u][1].w};
+      float s[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d = dot2bf(qv[h][i], kk[i], d);
+        d += __shfl_xor(d, 1);
+        d += __shfl_xor(d, 2);
+        s[h] = valid[u] ? d * a.scale_l2 : -INFINITY;
+      }
+      const uint32_t vv[8] = {vv4[u][0].x, vv4[u][0].y, vv4[u][0].z, vv4[u][0].w,
+                              vv4[u][1].x, vv4[u][1].y, vv4[u][1].z, vv4[u][1].w};
+      float vf[16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        vf[2 * i] = bf16lo(vv[i]);
+        vf[2 * i + 1] = bf16hi(vv[i]);
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float bm = s[h];
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
+        const float mn = fmaxf(m[h], bm);
+        if (mn != m[h]) {  // wave-uniform: rescale what is accumulated
+          const float corr = (m[h] == -INFINITY) ? 0.f : exp2f(m[h] - mn);
+          l[h] *= corr;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[h][i] *= corr;
+          m[h] = mn;
+        }
+        const float p = (s[h] == -INFINITY) ? 0.f : exp2f(s[h] - m[h]);
+        l[h] += p;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
+      }
     }
   }
 
@@ -173,8 +188,8 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
 
   if (a.n_split > 1) {
     float* part = a.partial + ((size_t)bk * a.n_split + split) * (G * 66);
-    for (int e = tid; e < G * 66; e += 256) part[e] = s_fin[e / 66][e % 66];
-    __threadfence();
+    for (int e = tid; e < G * 66; e += 256) store_sys(part + e, s_fin[e / 66][e % 66]);
+    wait_vm();
     __syncthreads();
     if (tid == 0) {
       const unsigned prev = atomicAdd(&a.counters[bk], 1u);
@@ -182,22 +197,57 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
+    // Merge all splits in split order, kSplitChunk at a time: every partial of the chunk
+    // is loaded into LDS with many loads in flight, then each thread folds its (h, d).
     const float* base = a.partial + (size_t)bk * a.n_split * (G * 66);
-    for (int e = tid; e < G * 64; e += 256) {
-      const int h = e >> 6, d = e & 63;
-      float M = -INFINITY;
-      for (int sp = 0; sp < a.n_split; ++sp) M = fmaxf(M, base[sp * G * 66 + h * 66 + 64]);
-      float Ls = 0.f, As = 0.f;
-      for (int sp = 0; sp < a.n_split; ++sp) {
-        const float* ps = base + sp * G * 66 + h * 66;
-        const float f = (ps[64] == -INFINITY) ? 0.f : exp2f(ps[64] - M);
-        Ls = fmaf(ps[65], f, Ls);
-        As = fmaf(ps[d], f, As);
+    // running state of this thread's (h, d) outputs e = tid + j*256 (G*64 <= 512)
+    float Mr[2] = {-INFINITY, -INFINITY}, Lr[2] = {0.f, 0.f}, Ar[2] = {0.f, 0.f};
+    for (int cs = 0; cs < a.n_split; cs += kSplitChunk) {
+      const int ns = min(kSplitChunk, a.n_split - cs);
+      const float* src = base + (size_t)cs * G * 66;
+      const int n = ns * G * 66;
+      for (int e = tid; e < n; e += 4 * 256) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (e + j * 256 < n) ? load_sys(src + e + j * 256) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (e + j * 256 < n) s_part[e + j * 256] = v[j];
       }
-      // s_fin is only read by this thread for its own (h, d) below
-      s_fin[h][d] = As;
-      if (d == 0) s_fin[h][65] = Ls;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int e = tid + j * 256;
+        if (e < G * 64) {
+          const int h = e >> 6, d = e & 63;
+          float M = Mr[j];
+          for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, s_part[(sp * G + h) * 66 + 64]);
+          float Ls = Lr[j], As = Ar[j];
+          if (Mr[j] != -INFINITY && M != Mr[j]) {
+            const float f = exp2f(Mr[j] - M);
+            Ls *= f;
+            As *= f;
+          }
+          for (int sp = 0; sp < ns; ++sp) {
+            const float* ps = s_part + (sp * G + h) * 66;
+            const float f = (ps[64] == -INFINITY) ? 0.f : exp2f(ps[64] - M);
+            Ls = fmaf(ps[65], f, Ls);
+            As = fmaf(ps[d], f, As);
+          }
+          Mr[j] = M;
+          Lr[j] = Ls;
+          Ar[j] = As;
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = tid + j * 256;
+      if (e < G * 64) {
+        s_fin[e >> 6][e & 63] = Ar[j];
+        if ((e & 63) == 0) s_fin[e >> 6][65] = Lr[j];
+      }
     }
     if (tid == 0) a.counters[bk] = 0u;
     __syncthreads();

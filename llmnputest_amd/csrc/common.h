@@ -48,6 +48,19 @@ __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel)
   return __builtin_amdgcn_perm(s0, s1, sel);
 }
 
+// Cross-workgroup publication without flushing the XCD L2s: partial results go out with
+// system-scope (L2-bypassing, write-through) stores, `wait_vm` waits until they are
+// acknowledged, and the workgroup that reads them back uses system-scope loads. An
+// agent-scope __threadfence() here would write back and invalidate the whole L2 of the
+// XCD for every workgroup (buffer_wbl2 / buffer_inv), which costs tens of microseconds.
+__device__ __forceinline__ void store_sys(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float load_sys(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Sum over the wave (64 lanes) via xor shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

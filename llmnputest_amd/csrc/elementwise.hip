@@ -170,6 +170,42 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
   }
 }
 
+// ------------------------------------------------------------------ decode bookkeeping
+// keys: [batch][n_slots] order-preserving argmax keys (one per lm_head tile-row).
+__global__ __launch_bounds__(1024) void decode_advance_kernel(
+    const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
+    int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
+    int32_t* __restrict__ step, int history_len, int batch) {
+  __shared__ unsigned long long sk[16];
+  const int tid = threadIdx.x;
+  const int s = step[0];
+  for (int b = 0; b < batch; ++b) {
+    unsigned long long k = 0ull;
+    for (int i = tid; i < n_slots; i += blockDim.x) {
+      const unsigned long long v = keys[(int64_t)b * n_slots + i];
+      k = v > k ? v : k;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long v = __shfl_xor(k, o);
+      k = v > k ? v : k;
+    }
+    if ((tid & 63) == 0) sk[tid >> 6] = k;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < (int)(blockDim.x >> 6); ++w) k = sk[w] > k ? sk[w] : k;
+      const int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+      tokens[b] = tok;
+      const int32_t p = pos[b] + 1;
+      pos[b] = p;
+      lens[b] = p + 1;
+      if (history != nullptr && s < history_len) history[(int64_t)s * batch + b] = tok;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) step[0] = s + 1;
+}
+
 }  // namespace q4nx
 
 using namespace q4nx;
@@ -234,6 +270,19 @@ int q4nx_argmax(const float* logits, int n, int batch, int64_t stride, int32_t* 
   hipLaunchKernelGGL(argmax_kernel, dim3(batch), dim3(1024), 0, (hipStream_t)stream, logits, n,
                      stride, idx, max_val);
   return check_launch("q4nx_argmax");
+}
+
+int q4nx_decode_advance(const uint64_t* keys, int n_slots, int32_t* tokens, int32_t* pos,
+                        int32_t* lens, int32_t* history, int32_t* step, int history_len,
+                        int batch, void* stream) {
+  Q4NX_REQUIRE(keys && tokens && pos && lens && step, Q4NX_ERR_ARG,
+               "q4nx_decode_advance: keys, tokens, pos, lens and step are required");
+  Q4NX_REQUIRE(batch >= 1 && batch <= Q4NX_MAX_BATCH && n_slots >= 1, Q4NX_ERR_SHAPE,
+               "q4nx_decode_advance: batch=%d n_slots=%d", batch, n_slots);
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream,
+                     (const unsigned long long*)keys, n_slots, tokens, pos, lens, history, step,
+                     history_len, batch);
+  return check_launch("q4nx_decode_advance");
 }
 
 }  // extern "C"

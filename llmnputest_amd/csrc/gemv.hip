@@ -69,7 +69,19 @@ struct GemvArgs {
   // gate/up
   uint16_t* h_out;
   int64_t h_stride;
+  // plain: optional argmax keys, uint64 [batch][n_tile_rows] (order-preserving (value, -row))
+  unsigned long long* argmax_keys;
 };
+
+// 64-bit key whose unsigned order is numpy's argmax order: larger value first, NaN above
+// everything, and on ties the smaller index (stored inverted in the low word).
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+  const uint32_t u = __float_as_uint(v);
+  uint32_t ord;
+  if ((u & 0x7fffffffu) > 0x7f800000u) ord = 0xffffffffu;
+  else ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - idx);
+}
 
 constexpr int kMaxWaves = 16;
 
@@ -105,6 +117,7 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   __shared__ float sred[kMaxWaves][B][32];
   __shared__ float sgrp[B][64];
   __shared__ float snorm[kMaxWaves][B];
+  __shared__ unsigned long long skey[B];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int W = blockDim.x >> 6;
@@ -367,14 +380,21 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
 
   // ---- 8. epilogue on the whole group
   if (a.op == OP_PLAIN) {
+    if (a.argmax_keys != nullptr && tid < B) skey[tid] = 0ull;
+    if (a.argmax_keys != nullptr) __syncthreads();
     for (int e = tid; e < B * 32; e += blockDim.x) {
       const int b = e >> 5, r = e & 31;
       if (b < a.batch) {
         const int64_t n = (int64_t)tr * 32 + r;
         float v = sgrp[b][r];
         if (a.residual != nullptr) v += a.residual[b * a.y_stride + n];
-        a.y[b * a.y_stride + n] = v;
+        if (a.y != nullptr) a.y[b * a.y_stride + n] = v;
+        if (a.argmax_keys != nullptr) atomicMax(&skey[b], argmax_key(v, (uint32_t)n));
       }
+    }
+    if (a.argmax_keys != nullptr) {   // one slot per (batch row, tile-row): no contention
+      __syncthreads();
+      if (tid < a.batch) a.argmax_keys[(int64_t)tid * a.n_tr[0] + tr] = skey[tid];
     }
   } else if (a.op == OP_GATEUP) {
     for (int e = tid; e < B * 32; e += blockDim.x) {
@@ -512,17 +532,24 @@ static int check_x(const void* x, int64_t x_stride, int k_tiles, const char* wha
   return Q4NX_OK;
 }
 
-static int gemv_plain(int kind, const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows,
-                      int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
-                      const float* residual, void* stream, const char* what) {
+static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t* norm_w,
+                      float eps, float* y, int n_tile_rows, int k_tiles, int batch,
+                      int64_t x_stride, int64_t y_stride, const float* residual,
+                      unsigned long long* argmax_keys, void* stream, const char* what) {
   int rc = check_common(w, n_tile_rows, k_tiles, batch, what);
   if (rc) return rc;
   rc = check_x(x, x_stride, k_tiles, what);
   if (rc) return rc;
-  Q4NX_REQUIRE(y != nullptr && Q4NX_ALIGNED(y, 4), Q4NX_ERR_ARG,
-               "%s: y must be a non-null 4-byte aligned device pointer", what);
-  Q4NX_REQUIRE(y_stride >= (int64_t)n_tile_rows * 32, Q4NX_ERR_SHAPE,
+  Q4NX_REQUIRE(norm_w == nullptr || Q4NX_ALIGNED(norm_w, 16), Q4NX_ERR_ARG,
+               "%s: norm_w must be 16-byte aligned", what);
+  Q4NX_REQUIRE((y != nullptr && Q4NX_ALIGNED(y, 4)) || (y == nullptr && argmax_keys != nullptr),
+               Q4NX_ERR_ARG, "%s: y must be a 4-byte aligned device pointer", what);
+  Q4NX_REQUIRE(y == nullptr || y_stride >= (int64_t)n_tile_rows * 32, Q4NX_ERR_SHAPE,
                "%s: y_stride=%lld < N=%d", what, (long long)y_stride, n_tile_rows * 32);
+  Q4NX_REQUIRE(residual == nullptr || y != nullptr, Q4NX_ERR_ARG,
+               "%s: a residual needs an output", what);
+  Q4NX_REQUIRE(argmax_keys == nullptr || Q4NX_ALIGNED(argmax_keys, 8), Q4NX_ERR_ARG,
+               "%s: argmax keys must be 8-byte aligned", what);
   GemvArgs a{};
   a.w[0] = w;
   a.n_tr[0] = n_tile_rows;
@@ -530,11 +557,18 @@ static int gemv_plain(int kind, const uint8_t* w, const uint16_t* x, float* y, i
   a.G = 1;
   a.k_t = k_tiles;
   a.batch = batch;
-  a.x = x;
+  if (norm_w) {
+    a.hres = (const float*)x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+  } else {
+    a.x = (const uint16_t*)x;
+  }
   a.x_stride = x_stride;
   a.y = y;
   a.y_stride = y_stride;
   a.residual = residual;
+  a.argmax_keys = argmax_keys;
   return launch(kind, a, n_tile_rows, (hipStream_t)stream, what);
 }
 
@@ -562,16 +596,25 @@ int q4nx_gemv_q4(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
   (void)ws; (void)ws_bytes;
-  return gemv_plain(4, w, x, y, n_tile_rows, k_tiles, batch, x_stride, y_stride, residual,
-                    stream, "q4nx_gemv_q4");
+  return gemv_plain(4, w, x, nullptr, 0.f, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
+                    residual, nullptr, stream, "q4nx_gemv_q4");
 }
 
 int q4nx_gemv_q8(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
   (void)ws; (void)ws_bytes;
-  return gemv_plain(8, w, x, y, n_tile_rows, k_tiles, batch, x_stride, y_stride, residual,
-                    stream, "q4nx_gemv_q8");
+  return gemv_plain(8, w, x, nullptr, 0.f, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
+                    residual, nullptr, stream, "q4nx_gemv_q8");
+}
+
+int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const void* x,
+                 int64_t x_stride, const uint16_t* norm_w, float eps, int batch, float* y,
+                 int64_t y_stride, const float* residual, uint64_t* argmax_keys, void* stream) {
+  Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
+               "q4nx_gemv_ex: kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", kind);
+  return gemv_plain(kind, w, x, norm_w, eps, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
+                    residual, (unsigned long long*)argmax_keys, stream, "q4nx_gemv_ex");
 }
 
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {

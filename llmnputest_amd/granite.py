@@ -11,8 +11,10 @@ groups the projections by shared input:
     [RMSNorm, gate, up, SwiGLU]           q4nx_gate_up_swiglu (norm fused)
     [down, residual add]                  q4nx_gemv_q4
 
-then the final RMSNorm, the tied q8 lm_head GEMV and a device-side argmax. A whole step
-is captured once in a HIP graph and replayed; the greedy loop never leaves the device.
+then one q8 lm_head launch (final RMSNorm fused as its prologue, the greedy argmax folded
+into its epilogue as a 64-bit atomic max) and one bookkeeping launch that turns the argmax
+into the next token and advances positions. A whole step is captured once in a HIP graph
+and replayed; the greedy loop never leaves the device.
 
 Conventions (the reference fixes none of them): fp32 residual stream, pre-norm
 Llama/Granite order, final RMSNorm, tied q8 lm_head whose dequantised row t is the
@@ -185,11 +187,13 @@ class GraniteDecoder:
         self.q = torch.zeros((b, c.q_dim), dtype=torch.bfloat16, device=dev)
         self.attn = torch.zeros((b, c.n_q, c.head_dim), dtype=torch.bfloat16, device=dev)
         self.mlp = torch.zeros((b, c.inter), dtype=torch.bfloat16, device=dev)
-        self.hf = torch.zeros((b, c.hidden), dtype=torch.bfloat16, device=dev)
         self.logits = torch.zeros((b, c.vocab), dtype=torch.float32, device=dev)
         self.tokens = torch.zeros(b, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(b, dtype=torch.int32, device=dev)
         self.lens = torch.ones(b, dtype=torch.int32, device=dev)
+        self.keys = torch.zeros((b, c.vocab // 32), dtype=torch.int64, device=dev)  # argmax keys
+        self.history = torch.zeros((self.max_len, b), dtype=torch.int32, device=dev)
+        self.step_ctr = torch.zeros(1, dtype=torch.int32, device=dev)
         self.ws = ops.Workspace(ops.WS_COUNTER_BYTES + (64 << 20), device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
         self.graph_batch = 0
@@ -203,7 +207,6 @@ class GraniteDecoder:
         kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
         h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
         ops.embed_q8(w.lm_head, self.tokens[:b], c.vocab, c.hidden, out=h)
-        self.lens[:b].copy_(self.pos[:b] + 1)
         for li, L in enumerate(w.layers):
             kc, vc = self.k_cache[li], self.v_cache[li]
             ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
@@ -215,8 +218,9 @@ class GraniteDecoder:
             ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
                                norm_w=L["norm_post"], eps=c.eps, ws=self.ws)
             ops.gemv(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h, ws=self.ws)
-        ops.rmsnorm(h, w.norm_final, c.eps, out=self.hf[:b])
-        ops.gemv(w.lm_head, "q8", self.hf[:b], c.vocab // 32, kt_h, out=self.logits[:b], ws=self.ws)
+        # final RMSNorm fused into the lm_head prologue, greedy argmax into its epilogue
+        ops.gemv_ex(w.lm_head, "q8", h, c.vocab // 32, kt_h, norm_w=w.norm_final, eps=c.eps,
+                    out=self.logits[:b], argmax_keys=self.keys[:b])
 
     def step(self, tokens, positions) -> torch.Tensor:
         """One decode step, eager: tokens/positions for B sequences -> fp32 logits [B, V]."""
@@ -229,21 +233,30 @@ class GraniteDecoder:
             raise ValueError(f"positions must be in [0, {self.max_len})")
         self.tokens[:b].copy_(tokens)
         self.pos[:b].copy_(positions)
+        self.lens[:b].copy_(positions + 1)
         self._launch_step(b)
         return self.logits[:b]
 
     # ------------------------------------------------------------ graph + greedy loop
+    def _advance(self, b: int) -> None:
+        ops.decode_advance(self.keys[:b], self.cfg.vocab // 32, self.tokens[:b], self.pos[:b],
+                           self.lens[:b], self.step_ctr,
+                           self.history[:, :b] if b == self.max_batch else None)
+
     def capture(self, b: int) -> None:
-        """Capture one greedy step for b sequences: kernels, argmax into `tokens`, pos += 1."""
+        """Capture one greedy step for b sequences: the step's kernels, then one launch that
+        turns the argmax key into the next token and advances positions and history."""
+        snap = (self.tokens.clone(), self.pos.clone(), self.lens.clone())
         self._launch_step(b)                       # warm: sizes every workspace
-        ops.argmax(self.logits[:b], out=self.tokens[:b])
+        self._advance(b)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self._launch_step(b)
-            ops.argmax(self.logits[:b], out=self.tokens[:b])
-            self.pos[:b].add_(1)
+            self._advance(b)
         self.graph, self.graph_batch = g, b
+        for t, s0 in zip((self.tokens, self.pos, self.lens), snap):
+            t.copy_(s0)
 
     def generate(self, first_tokens, start_pos, n_new: int, record_logits: bool = False):
         """Greedy decode of n_new tokens for B sequences from `first_tokens` at `start_pos`.
@@ -253,25 +266,28 @@ class GraniteDecoder:
         b = first.numel()
         if int(start.max()) + n_new > self.max_len:
             raise ValueError("max_len too small for this many new tokens")
+        if b != self.max_batch:
+            raise ValueError("generate() runs all max_batch sequences; size the decoder to them")
         if self.graph is None or self.graph_batch != b:
             self.pos[:b].copy_(start)
+            self.lens[:b].copy_(start + 1)
             self.tokens[:b].copy_(first)
             self.capture(b)
         self.tokens[:b].copy_(first)
         self.pos[:b].copy_(start)
-        out = torch.empty((n_new, b), dtype=torch.int32, device=self.dev)
+        self.lens[:b].copy_(start + 1)
+        self.step_ctr.zero_()
         logs = [] if record_logits else None
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for i in range(n_new):
+        for _ in range(n_new):
             self.graph.replay()
-            out[i].copy_(self.tokens[:b])
             if record_logits:
                 logs.append(self.logits[:b].clone())
         torch.cuda.synchronize()
         self.seconds += time.perf_counter() - t0
         self.calls += n_new
-        return out.t().contiguous().cpu().numpy(), logs
+        return self.history[:n_new, :b].t().contiguous().cpu().numpy(), logs
 
     def seed_cache(self, ctx: int, seed: int = 0) -> None:
         """Fill positions [0, ctx) of every layer's K/V cache with bf16 N(0,1) (a synthetic

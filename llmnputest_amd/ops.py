@@ -116,9 +116,45 @@ def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_ti
     return out.reshape(n) if squeeze else out
 
 
-def set_split_tiles(tiles_per_workgroup: int) -> None:
-    """Tuning: K-tiles per workgroup for all GEMVs (0 = automatic)."""
-    _lib.call("q4nx_set_split_tiles", int(tiles_per_workgroup))
+def gemv_ex(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
+            norm_w: torch.Tensor | None = None, eps: float = 1e-5,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            argmax_keys: torch.Tensor | None = None, want_y: bool = True):
+    """General GEMV: y = residual + W f(x), f = RMSNorm(x; norm_w) when norm_w is given
+    (x fp32 [B, K]) else identity (x bf16). argmax_keys: int64 [B, n_tile_rows] receives one
+    order-preserving (max, first row) key per tile-row -- reduced by `decode_advance`."""
+    _tiles(tiles, kind, n_tile_rows, k_tiles)
+    _dev(x, "x", torch.float32 if norm_w is not None else torch.bfloat16)
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    b = x2.shape[0]
+    n = n_tile_rows * 32
+    if norm_w is not None:
+        _dev(norm_w, "norm_w", torch.bfloat16)
+    if out is None and want_y:
+        out = torch.empty((b, n), dtype=torch.float32, device=x.device)
+    if argmax_keys is not None:
+        _dev(argmax_keys, "argmax_keys", torch.int64)
+        if argmax_keys.numel() < b * n_tile_rows:
+            raise ValueError("argmax_keys needs batch * n_tile_rows entries")
+    _lib.call("q4nx_gemv_ex", KIND[kind], _ptr(tiles), n_tile_rows, k_tiles, _ptr(x2),
+              x2.shape[1], _ptr(norm_w), float(eps), b, _ptr(out), n, _ptr(residual),
+              _ptr(argmax_keys), _stream())
+    return out
+
+
+def decode_advance(keys: torch.Tensor, n_slots: int, tokens: torch.Tensor, pos: torch.Tensor,
+                   lens: torch.Tensor, step: torch.Tensor, history: torch.Tensor | None = None) -> None:
+    """tokens = argmax over keys [B, n_slots], pos += 1, lens = pos + 1, history[step] =
+    tokens while step < len(history), step += 1 -- one launch, no host round trip."""
+    b = tokens.numel()
+    hl = 0 if history is None else history.shape[0]
+    _lib.call("q4nx_decode_advance", _ptr(keys), int(n_slots), _ptr(tokens), _ptr(pos),
+              _ptr(lens), _ptr(history), _ptr(step), hl, b, _stream())
+
+
+def set_split_tiles(tiles_per_wave: int) -> None:
+    """Tuning: K-tiles per wave for all GEMVs (0 = automatic, else 1, 2 or 4)."""
+    _lib.call("q4nx_set_split_tiles", int(tiles_per_wave))
 
 
 # ---------------------------------------------------------------- elementwise
