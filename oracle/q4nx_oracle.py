@@ -121,22 +121,24 @@ def dequant_tile_bruteforce(tile: np.ndarray, kind: str) -> np.ndarray:
     written straight from the format description (tools/q4nx.py:10-18) and the kernel
     comments (designs/q4nx_unpack/q4nx_unpack.cc:12-19, designs/lm_head/lm_head.h:21-29).
     Slow; for a few tiles only."""
-    t = np.asarray(tile, dtype=np.uint8)
+    t = [int(v) for v in np.asarray(tile, dtype=np.uint8)]
+    le16 = lambda off: bf16_to_f32(np.array([t[off] | (t[off + 1] << 8)], np.uint16))[0]
     out = np.empty((32, 256), np.float32)
     for rb in range(2):
         for k in range(256):
             for r in range(16):
                 g = (k // 32) * 32 + rb * 16 + r
                 if kind == "q4":
-                    d = bf16_to_f32(np.array([t[2 * g] | (t[2 * g + 1] << 8)], np.uint16))[0]
-                    m = bf16_to_f32(np.array([t[512 + 2 * g] | (t[512 + 2 * g + 1] << 8)], np.uint16))[0]
+                    d = le16(2 * g)
+                    m = le16(512 + 2 * g)
                     i = rb * 4096 + k * 16 + r
-                    byte = int(t[1024 + (i >> 1)])
+                    byte = t[1024 + (i >> 1)]
                     code = (byte & 0xF) if (i % 2 == 0) else (byte >> 4)
                     out[rb * 16 + r, k] = np.float32(np.float32(code) * d + m)
                 else:
-                    s = bf16_to_f32(np.array([t[2 * g] | (t[2 * g + 1] << 8)], np.uint16))[0]
-                    code = int(np.int8(np.uint8(t[512 + rb * 4096 + k * 16 + r])))
+                    s = le16(2 * g)
+                    b = t[512 + rb * 4096 + k * 16 + r]
+                    code = b - 256 if b >= 128 else b
                     out[rb * 16 + r, k] = np.float32(code) * s
     return out
 

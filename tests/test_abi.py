@@ -1,0 +1,92 @@
+"""The C ABI without a GPU: the library loads, exports every function include/q4nx_hip.h
+declares, rejects bad arguments with the documented codes (mirroring the reference's
+CPU-forceable failures: wrong tile size, K not a multiple of 256, bad factoring), and its
+host-side RoPE table equals the oracle's."""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from llmnputest_amd import _lib
+from oracle import decode_oracle as do
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "q4nx_hip.h"
+ERR_ARG, ERR_SHAPE, ERR_WS = -1, -2, -3
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(q4nx_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    h = C.CDLL(str(_lib.LIB_PATH))
+    names = declared()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(h, n)]
+    assert not missing, missing
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+    assert _lib.lib().q4nx_abi_version() == 1
+
+
+def rc_msg(name, *args):
+    rc = getattr(_lib.lib(), name)(*args)
+    return rc, _lib.lib().q4nx_last_error().decode()
+
+
+def test_gemv_argument_errors():
+    fake = C.c_void_p(0x10000)       # aligned, never dereferenced: validation fails first
+    rc, msg = rc_msg("q4nx_gemv_q4", None, fake, fake, 8, 10, 1, 2560, 256, None, None, 0, None)
+    assert rc == ERR_ARG and "weights" in msg
+    rc, msg = rc_msg("q4nx_gemv_q4", C.c_void_p(0x10001), fake, fake, 8, 10, 1, 2560, 256,
+                     None, None, 0, None)
+    assert rc == ERR_ARG                                   # misaligned tiles
+    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 0, 10, 1, 2560, 256, None, None, 0, None)
+    assert rc == ERR_SHAPE and "n_tile_rows" in msg
+    rc, msg = rc_msg("q4nx_gemv_q8", fake, fake, fake, 8, 4, 9, 1024, 256, None, None, 0, None)
+    assert rc == ERR_SHAPE and "batch" in msg
+    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 8, 10, 1, 2000, 256, None, None, 0, None)
+    assert rc == ERR_SHAPE and "x_stride" in msg           # K = 2560 does not fit a 2000 row
+    rc, msg = rc_msg("q4nx_gemv_ex", 5, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), 1, fake,
+                     256, None, None, None)
+    assert rc == ERR_ARG and "kind" in msg
+    rc, msg = rc_msg("q4nx_set_split_tiles", 3)
+    assert rc == ERR_ARG
+
+
+def test_fused_and_attention_argument_errors():
+    fake = C.c_void_p(0x10000)
+    rc, msg = rc_msg("q4nx_qkv_rope", fake, fake, fake, 40, 7, 10, fake, 2560, None,
+                     C.c_float(1e-5), 1, fake, fake, 512, fake, fake, fake, 8 * 512 * 64,
+                     512 * 64, None, None, None, 0, None)
+    assert rc == ERR_SHAPE and "n_kv_heads" in msg         # 40 % 7 != 0
+    rc, msg = rc_msg("q4nx_gqa_decode", fake, fake, fake, fake, None, 1, 40, 8, 128, fake, 512,
+                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 0, None, 0, None)
+    assert rc == ERR_SHAPE and "head_dim" in msg
+    rc, msg = rc_msg("q4nx_gqa_decode", fake, fake, fake, fake, None, 1, 40, 8, 64, fake, 4096,
+                     8 * 4096 * 64, 4096 * 64, C.c_float(0.125), 8, None, 0, None)
+    assert rc == ERR_WS and "workspace" in msg
+    rc, msg = rc_msg("q4nx_embed_q8", fake, fake, fake, 100, 2560, 1, None)
+    assert rc == ERR_SHAPE                                 # vocab not a multiple of 32
+    rc, msg = rc_msg("q4nx_dequant_q4", fake, None, 1, 1, 0, 0, None)
+    assert rc == ERR_ARG
+
+
+def test_ws_queries():
+    lib = _lib.lib()
+    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1) == 0       # GEMVs reduce inside one workgroup
+    assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64) == 0  # one split: no workspace
+    big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768)
+    assert big >= 65536 + 8 * 5 * 66 * 4 * 2
+
+
+@pytest.mark.parametrize("max_pos,theta", [(4096, 10000.0), (64, 500000.0)])
+def test_rope_table_host(max_pos, theta):
+    tab = np.empty((max_pos, 2, 32), np.float32)
+    _lib.call("q4nx_rope_table_host", tab.ctypes.data, max_pos, 64, C.c_double(theta))
+    ref = do.rope_table(max_pos, 64, theta)
+    assert np.abs(tab - ref).max() <= 6e-8
+    assert np.array_equal(tab[0, 0], np.ones(32, np.float32)) and not tab[0, 1].any()

@@ -1,0 +1,66 @@
+"""Host logic of the drop-in surface: the q4nx container reader, projection shapes and the
+stored-shape cross-check (tools/q4nx.py, designs/granite_gemv/granite_gemv.py:90-102,
+282-288), and the design metadata of the GPU NpuDesign (reference/npu.py:41-114)."""
+
+import numpy as np
+import pytest
+
+from llmnputest_amd import npu, q4nx, synth
+
+GRANITE = {"hidden_size": 2560, "intermediate_size": 8192, "num_attention_heads": 40,
+           "num_key_value_heads": 8, "head_dim": 64, "vocab_size": 100352}
+
+
+def test_container_roundtrip(tmp_path):
+    rng = np.random.default_rng(0)
+    w4 = synth.q4_tiles(rng, 64, 512)
+    w8 = synth.q8_tiles(rng, 64, 256)
+    norm = synth.random_bf16(rng, 512)
+    path = tmp_path / "m.q4nx"
+    q4nx.write_q4nx(path, {"a.weight": ("q4", w4), "lm_head.weight": ("q8", w8),
+                           "model.norm.weight": norm})
+    f = q4nx.Q4NX(path)
+    assert f.names() == ["a.weight", "lm_head.weight", "model.norm.weight"]
+    kind, t = f.tiles("a.weight")
+    assert kind == "q4" and np.array_equal(t, w4.reshape(-1, 5120))
+    kind, t = f.tiles("lm_head.weight")
+    assert kind == "q8" and np.array_equal(t, w8.reshape(-1, 8704))
+    assert np.array_equal(f.plain("model.norm.weight"), norm)
+    assert f.raw("a.weight") == w4.tobytes()
+    with pytest.raises(q4nx.Q4NXFormatError):
+        f.tiles("model.norm.weight")
+
+
+def test_projection_shapes_and_factoring():
+    assert q4nx.projection_shape("model.layers.0.mlp.gate_proj.weight", GRANITE) == (8192, 2560)
+    assert q4nx.projection_shape("model.layers.3.mlp.down_proj.weight", GRANITE) == (2560, 8192)
+    assert q4nx.projection_shape("model.layers.0.self_attn.k_proj.weight", GRANITE) == (512, 2560)
+    assert q4nx.projection_shape("lm_head.weight", GRANITE) == (100352, 2560)
+    # gate and down are both stored as [2560, 5120]; only the config tells them apart
+    q4nx.check_stored_shape([2560, 5120], 8192, 2560)
+    q4nx.check_stored_shape([2560, 5120], 2560, 8192)
+    q4nx.check_stored_shape([256, 10, 5120], 8192, 2560)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        q4nx.check_stored_shape([256, 10, 5120], 2560, 8192)   # wrong factoring
+    with pytest.raises(q4nx.Q4NXFormatError):
+        q4nx.tiled_shape(100, 2560)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        q4nx.tiled_shape(2560, 1000)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        q4nx.kind_of_tile_bytes(5121)
+    q4nx.check_tile_bytes(256 * 10 * 5120, "q4", 8192, 2560)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        q4nx.check_tile_bytes(256 * 10 * 5120 - 1, "q4", 8192, 2560)
+
+
+def test_design_meta():
+    m = npu._meta_for("lm_head", None)
+    assert m["kind"] == "q8" and m["n_rows"] == 248320 and m["k"] == 1024
+    assert m["buffers"] == [7760 * 4 * 8704, 2048, 248320 * 4]
+    # the reference's design.json has no kind; it follows from the weight buffer size
+    m = npu._meta_for("granite", {"n_rows": 8192, "k": 2560, "buffers": [256 * 10 * 5120, 0, 0]})
+    assert m["kind"] == "q4" and m["tile_rows"] == 256
+    with pytest.raises(SystemExit):
+        npu._meta_for("no_such_design", None)
+    with pytest.raises(ValueError):
+        npu._meta_for("x", {"kind": "q4", "n_rows": 100, "k": 256})
