@@ -113,6 +113,33 @@ def gemv_bench(steps: int, warmup: int, rot: int, dev) -> dict:
     }
 
 
+def copy_calibration(mib: int, reps: int, dev) -> int:
+    """A plain device copy of `mib` MiB, `reps` times: the known-size kernel that scales the
+    FETCH_SIZE / WRITE_SIZE counters (read mib MiB and write mib MiB per launch)."""
+    n = mib << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "reps": reps}),
+          flush=True)
+    return 0
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_q4_gemv_granite_b1.json"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per GEMV launch from the committed counter runs (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy calibration), averaged over the bench's 2 gate/up : 1 down mix."""
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+        return int(t["bytes_per_launch_mix"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def decode_bytes_per_token(cfg: GraniteConfig, ctx: int, n_new: int) -> float:
     """Algorithmic HBM bytes of one decode step, averaged over the generated positions:
     every weight tile once, the K/V cache up to the current position (read) plus one
@@ -234,6 +261,8 @@ def main() -> int:
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-decode-tokens", type=int, default=2)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (counter calibration) and exit")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -246,6 +275,8 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if a.calibrate_copy:
+        return copy_calibration(a.calibrate_copy, 10, dev)
 
     r = gemv_bench(a.steps, a.warmup, a.rot, dev)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
@@ -279,7 +310,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "per_shape": {
             "gate_up_2560x8192": {"GB/s": round(r["gate_up_gbs"], 1), "us": round(r["gate_up_us"], 3)},
