@@ -93,6 +93,10 @@ int q4nx_gemv_ex(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const
 
 /* Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
 int q4nx_set_split_tiles(int tiles_per_wave);
+/* Tuning knob: workgroups per output group along K (1..8), 0 = automatic (split only
+ * launches with too few groups to fill the GPU, when a large enough workspace is given).
+ * Process-wide. No reference counterpart: on the NPU each core owned whole rows. */
+int q4nx_set_gemv_ksplit(int parts);
 
 /* ---------------------------------------------------------------- elementwise
  * RMSNorm y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, bf16 out (+ optional fp32
@@ -162,6 +166,11 @@ int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *
                     int n_kv_heads, int head_dim, const int32_t *lens, int max_len,
                     int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
                     void *ws, size_t ws_bytes, void *stream);
+
+/* y[i] = bf16(x[i]), round to nearest even, NaN kept quiet: the device form of the bf16
+ * rounding every kernel applies to its outputs (tools/q4nx.py:97-111 rounds the same way
+ * on the host). */
+int q4nx_round_bf16(const float *x, uint16_t *y, int64_t n, void *stream);
 
 /* ---------------------------------------------------------------- decode-step helpers
  * h[b][:] = fp32 row tokens[b] of a q8-tiled [vocab][hidden] matrix (a tied lm_head

@@ -26,12 +26,19 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
 __device__ __forceinline__ float bf16lo(uint32_t d) { return __uint_as_float(d << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32); a NaN keeps its upper payload
+// bits and becomes quiet, as the software rounding (u >> 16) | 0x40 does.
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_v v = {lo, hi};
+  uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
+  const uint32_t ul = __float_as_uint(lo), uh = __float_as_uint(hi);
+  if ((ul & 0x7FFFFFFFu) > 0x7F800000u) r = (r & 0xFFFF0000u) | ((ul >> 16) | 0x40u);
+  if ((uh & 0x7FFFFFFFu) > 0x7F800000u) r = (r & 0x0000FFFFu) | (((uh >> 16) | 0x40u) << 16);
+  return r;
 }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return (uint16_t)pack_bf16x2(f, 0.f); }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
@@ -61,16 +68,79 @@ __device__ __forceinline__ float load_sys(const float* p) {
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Sum over the wave (64 lanes) via xor shuffles.
+// 16-byte system-coherent (sc0 sc1) loads and stores through a raw buffer resource over
+// [base, base + bytes): the compiler tracks their completion like any other load, and
+// out-of-range offsets read 0 / drop the store (the buffer unit's own bounds check).
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+constexpr int kCacheSys = 0x11;  // sc0 | sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 ld16_sys(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCacheSys);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+__device__ __forceinline__ void st16_sys(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 u) {
+  const v4i_t v = {(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kCacheSys);
+}
+
+// Pins a value at this point of the program: arithmetic on it cannot be hoisted above,
+// and (with the memory clobber) loads issued before stay before. Used so that waits for
+// activation loads land after a wave has issued its weight stream.
+__device__ __forceinline__ void pin(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w) : : "memory");
+}
+__device__ __forceinline__ void pin(float4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w) : : "memory");
+}
+
+// DPP lane exchanges (a VALU operand modifier, no LDS traffic).
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8 lanes
+constexpr int kDppRor4 = 0x124;       // rotate by 4 inside each row of 16 lanes
+constexpr int kDppRor8 = 0x128;       // rotate by 8 inside each row of 16 lanes
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// All-reduce over aligned groups of 16 or 32 lanes; every lane of the group ends with the
+// bit-identical result (each step combines the same two values in either order).
+__device__ __forceinline__ float group16_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  return fmaxf(v, dpp<kDppRor8>(v));
+}
+__device__ __forceinline__ float group16_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  return v + dpp<kDppRor8>(v);
+}
+__device__ __forceinline__ float group32_max(float v) {
+  v = group16_max(v);
+  return fmaxf(v, __shfl_xor(v, 16));
+}
+__device__ __forceinline__ float group32_sum(float v) {
+  v = group16_sum(v);
+  return v + __shfl_xor(v, 16);
+}
+
+// Sum / max over the wave: DPP inside each row of 16 lanes, then the four row results read
+// into scalars and combined in a fixed order (every lane gets the same value).
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = group16_sum(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = group16_max(v);
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 }  // namespace q4nx

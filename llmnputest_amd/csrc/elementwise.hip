@@ -98,6 +98,13 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ g,
   if (y_f32) y_f32[i] = h;
 }
 
+// ------------------------------------------------------------------ fp32 -> bf16 rounding
+__global__ __launch_bounds__(256) void round_bf16_kernel(const float* __restrict__ x,
+                                                         uint16_t* __restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = f32_to_bf16(x[i]);
+}
+
 // ------------------------------------------------------------------ embedding row of a q8 matrix
 __global__ __launch_bounds__(256) void embed_q8_kernel(const uint8_t* __restrict__ w,
                                                        const int32_t* __restrict__ tokens,
@@ -250,6 +257,16 @@ int q4nx_swiglu(const void* g, const void* u, int in_f32, uint16_t* y, float* y_
   else
     hipLaunchKernelGGL(swiglu_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, g, u, y, y_f32, total);
   return check_launch("q4nx_swiglu");
+}
+
+int q4nx_round_bf16(const float* x, uint16_t* y, int64_t n, void* stream) {
+  Q4NX_REQUIRE(x && y, Q4NX_ERR_ARG, "q4nx_round_bf16: x and y are required");
+  Q4NX_REQUIRE(n >= 0 && n < ((int64_t)1 << 40), Q4NX_ERR_SHAPE, "q4nx_round_bf16: n=%lld",
+               (long long)n);
+  if (n == 0) return Q4NX_OK;
+  hipLaunchKernelGGL(round_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, y, n);
+  return check_launch("q4nx_round_bf16");
 }
 
 int q4nx_embed_q8(const uint8_t* w, const int32_t* tokens, float* h, int vocab, int hidden,

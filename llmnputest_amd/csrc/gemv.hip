@@ -8,10 +8,12 @@
 //   One workgroup owns one output *group*: the tile-rows an epilogue needs together --
 //   one tile-row for a plain GEMV, the two tile-rows of an attention head for
 //   [q,k,v,RoPE] (RoPE pairs dim i with i+32), or the same tile-row of gate and up for
-//   SwiGLU. Each wave of the workgroup owns TPW consecutive K-tiles of one tile-row,
-//   so a workgroup covers the whole K of its group and no cross-workgroup reduction
-//   (and no workspace) is needed. Waves combine through LDS once, in a fixed order,
-//   so results are bit-reproducible.
+//   SwiGLU. Each wave of the workgroup owns TPW consecutive K-tiles of one tile-row and
+//   the waves combine through LDS once, in a fixed order. When a launch has too few
+//   groups to fill the GPU (the 2560-row projections, the attention heads), K is also
+//   split over `ksplit` workgroups per group: each publishes its partial sums with
+//   system-scope stores, and the last to arrive adds the parts in part order and runs the
+//   epilogue, so results stay bit-reproducible.
 //
 // Data path (decode is HBM-bound: every byte is read once, straight into registers)
 //   Four lanes own one (row-block, 32-K group) "unit" of a tile: lane l reads the 64
@@ -71,6 +73,11 @@ struct GemvArgs {
   int64_t h_stride;
   // plain: optional argmax keys, uint64 [batch][n_tile_rows] (order-preserving (value, -row))
   unsigned long long* argmax_keys;
+  // split K: partial sums [group][part][batch][G*32] fp32 and one arrival counter per group
+  int ksplit;
+  float* part;
+  uint32_t part_bytes;
+  unsigned* counters;
 };
 
 // 64-bit key whose unsigned order is numpy's argmax order: larger value first, NaN above
@@ -98,14 +105,14 @@ __device__ __forceinline__ void transpose_reduce4(const float (&v)[16], float (&
   for (int i = 0; i < 8; ++i) {
     const float keep = up1 ? v[i + 8] : v[i];
     const float send = up1 ? v[i] : v[i + 8];
-    t8[i] = keep + __shfl_xor(send, 2);
+    t8[i] = keep + dpp<kDppXor2>(send);
   }
   const bool up0 = (lane & 1) != 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float keep = up0 ? t8[i + 4] : t8[i];
     const float send = up0 ? t8[i] : t8[i + 4];
-    o[i] = keep + __shfl_xor(send, 1);
+    o[i] = keep + dpp<kDppXor1>(send);
   }
 }
 
@@ -118,12 +125,18 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   __shared__ float sgrp[B][64];
   __shared__ float snorm[kMaxWaves][B];
   __shared__ unsigned long long skey[B];
+  __shared__ int s_last;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave-uniform values live in scalar registers: the weight pointer below must be known
+  // without a memory round trip, or every wave waits for it before streaming its tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int W = blockDim.x >> 6;
   const int WM = W / a.G;             // waves per member tile-row
   const int member = wave / WM, chunk = wave % WM;
-  const int group = blockIdx.x;
+  const int ks = a.ksplit;
+  const int group = blockIdx.x / ks, kpart = blockIdx.x - group * ks;
+  const int kt_lo = kpart * a.k_t / ks, kt_hi = (kpart + 1) * a.k_t / ks;
 
   int seg, tr;
   if (a.op == OP_PLAIN) {
@@ -147,39 +160,47 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
     tr = 2 * hg + member;
   }
   const int K = a.k_t * kTileK;
-  const int kt0 = chunk * TPW;
-  const int ntw = max(0, min(TPW, a.k_t - kt0));    // tiles this wave really owns
+  const int kt0 = kt_lo + chunk * TPW;
+  const int ntw = max(0, min(TPW, kt_hi - kt0));    // tiles this wave really owns
 
   // lane roles: q = lane bits 0-1 (8-K quarter), kb = bits 2-4, rb = bit 5
   const int q = lane & 3, kb = (lane >> 2) & 7, rb = lane >> 5;
   const int kx = kb * kGroup + q * 8;                // first K of this lane inside a tile
   const bool norm = a.norm_w != nullptr;
 
-  // ---- 1. activations first (so their wait does not include the weight stream)
-  uint4 xr[B][TPW];       // 8 bf16 per lane per tile
-  float hx[B][TPW][8];    // fp32 residual values (RMSNorm prologue only)
+  // ---- 1. activations. Every load is unconditional, from a valid address (clamped row,
+  //         or the weights as a stand-in), so nothing waits before the weight stream is
+  //         issued; rows past the batch are masked where the values are used.
+  uint4 ar[B][TPW][2];    // raw activation bytes: 8 bf16 x (first 16 B) or 8 fp32 h (32 B)
   uint4 nw[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    const int kt = min(kt0 + t, a.k_t - 1);
+    const int kt = min(kt0 + t, kt_hi - 1);
     const int k = kt * kTileK + kx;
-    nw[t] = make_uint4(0, 0, 0, 0);
-    if (norm) nw[t] = *(const uint4*)(a.norm_w + k);
+    nw[t] = *(const uint4*)(norm ? (const void*)(a.norm_w + k) : (const void*)a.w[0]);
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      xr[b][t] = make_uint4(0, 0, 0, 0);
+      const int bb = min(b, a.batch - 1);
+      const uint4* src = norm ? (const uint4*)(a.hres + bb * a.x_stride + k)
+                              : (const uint4*)(a.x + bb * a.x_stride + k);
+      ar[b][t][0] = src[0];
+      ar[b][t][1] = src[norm ? 1 : 0];
+    }
+  }
+
+  // with K split, this workgroup's tiles see only part of the row: the RMSNorm sum of
+  // squares reads the whole row (strided over all threads; three float4 per thread cover
+  // K <= 12 * blockDim, a remainder loop the rest)
+  constexpr int kSsqIt = 3;
+  float4 hs[B][kSsqIt];
+  const bool split_norm = norm && ks > 1;
+  if (split_norm) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) hx[b][t][i] = 0.f;
-      if (b < a.batch) {
-        if (norm) {
-          const float4 h0 = *(const float4*)(a.hres + b * a.x_stride + k);
-          const float4 h1 = *(const float4*)(a.hres + b * a.x_stride + k + 4);
-          hx[b][t][0] = h0.x; hx[b][t][1] = h0.y; hx[b][t][2] = h0.z; hx[b][t][3] = h0.w;
-          hx[b][t][4] = h1.x; hx[b][t][5] = h1.y; hx[b][t][6] = h1.z; hx[b][t][7] = h1.w;
-        } else {
-          xr[b][t] = *(const uint4*)(a.x + b * a.x_stride + k);
-        }
-      }
+    for (int it = 0; it < kSsqIt; ++it) {
+      const int i = min(tid + it * (int)blockDim.x, K / 4 - 1);
+#pragma unroll
+      for (int b = 0; b < B; ++b)
+        hs[b][it] = *(const float4*)(a.hres + min(b, a.batch - 1) * a.x_stride + 4 * i);
     }
   }
 
@@ -187,11 +208,12 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   uint4 wq[TPW][NCH];
   uint2 md[TPW], mm[TPW];
   {
-    const uint8_t* rowp = a.w[seg] + (size_t)tr * a.k_t * TB;
+    const uint8_t* wseg = seg == 0 ? a.w[0] : seg == 1 ? a.w[1] : a.w[2];
+    const uint8_t* rowp = wseg + (size_t)tr * a.k_t * TB;
     const int g = kb * 32 + rb * 16 + q * 4;          // meta index of this lane's 4 rows
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const uint8_t* tile = rowp + (size_t)min(kt0 + t, a.k_t - 1) * TB;
+      const uint8_t* tile = rowp + (size_t)min(kt0 + t, kt_hi - 1) * TB;
       const uint4* src = (const uint4*)(tile + CODE_OFF + lane * (NCH * 16));
 #pragma unroll
       for (int c = 0; c < NCH; ++c) wq[t][c] = src[c];
@@ -201,25 +223,79 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
     }
   }
 
+  // the activations are used from here on (their waits come after the weight stream)
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    pin(nw[t]);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      pin(ar[b][t][0]);
+      pin(ar[b][t][1]);
+    }
+  }
+  if (split_norm) {
+#pragma unroll
+    for (int it = 0; it < kSsqIt; ++it)
+#pragma unroll
+      for (int b = 0; b < B; ++b) pin(hs[b][it]);
+  }
+
+  uint4 xr[B][TPW];       // 8 bf16 per lane per tile
+  float hx[B][TPW][8];    // fp32 residual values (RMSNorm prologue only)
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool live = b < a.batch;
+      const uint32_t r[8] = {ar[b][t][0].x, ar[b][t][0].y, ar[b][t][0].z, ar[b][t][0].w,
+                             ar[b][t][1].x, ar[b][t][1].y, ar[b][t][1].z, ar[b][t][1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hx[b][t][i] = (norm && live) ? __uint_as_float(r[i]) : 0.f;
+      xr[b][t] = (!norm && live) ? ar[b][t][0] : make_uint4(0, 0, 0, 0);
+    }
+
   // ---- 3. RMSNorm prologue: sum of squares over K from member-0 waves, row-block-0 lanes
+  //         (or from the whole-row pass above when K is split)
+  float ssq[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    ssq[b] = 0.f;
+    if (split_norm) {
+#pragma unroll
+      for (int it = 0; it < kSsqIt; ++it) {
+        const float4 h = hs[b][it];
+        const bool live = b < a.batch && tid + it * (int)blockDim.x < K / 4;
+        if (live)
+          ssq[b] = fmaf(h.x, h.x, fmaf(h.y, h.y, fmaf(h.z, h.z, fmaf(h.w, h.w, ssq[b]))));
+      }
+      if (b < a.batch)
+        for (int i = tid + kSsqIt * (int)blockDim.x; i < K / 4; i += blockDim.x) {
+          const float4 h = *(const float4*)(a.hres + b * a.x_stride + 4 * i);
+          ssq[b] = fmaf(h.x, h.x, fmaf(h.y, h.y, fmaf(h.z, h.z, fmaf(h.w, h.w, ssq[b]))));
+        }
+    }
+  }
   if (norm) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      float s = 0.f;
+      float s = ssq[b];
+      if (ks == 1) {
 #pragma unroll
-      for (int t = 0; t < TPW; ++t)
-        if (t < ntw && rb == 0 && member == 0) {
+        for (int t = 0; t < TPW; ++t)
+          if (t < ntw && rb == 0 && member == 0) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) s = fmaf(hx[b][t][i], hx[b][t][i], s);
-        }
+            for (int i = 0; i < 8; ++i) s = fmaf(hx[b][t][i], hx[b][t][i], s);
+          }
+      }
       s = wave_sum(s);
       if (lane == 0) snorm[wave][b] = s;
     }
     __syncthreads();
+    const int n_sum_waves = ks == 1 ? WM : W;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       float s = 0.f;
-      for (int w = 0; w < WM; ++w) s += snorm[w][b];
+      for (int w = 0; w < n_sum_waves; ++w) s += snorm[w][b];
       const float inv = 1.0f / sqrtf(s / (float)K + a.eps);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
@@ -310,8 +386,8 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         }
         float r4[4];   // lo(2q), full(2q), lo(2q+1), full(2q+1): rows 4q .. 4q+3
         transpose_reduce4(pv, r4, lane);
-        X += __shfl_xor(X, 1);
-        X += __shfl_xor(X, 2);
+        X += dpp<kDppXor1>(X);
+        X += dpp<kDppXor2>(X);
         const float se0 = r4[0] * 16777216.0f, so0 = (r4[1] - r4[0]) * 1048576.0f;
         const float se1 = r4[2] * 16777216.0f, so1 = (r4[3] - r4[2]) * 1048576.0f;
         acc[b][0] += fmaf(bf16lo(md[t].x), se0, bf16lo(mm[t].x) * X);
@@ -342,8 +418,8 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         }
         float r4[4];
         transpose_reduce4(v, r4, lane);
-        X += __shfl_xor(X, 1);
-        X += __shfl_xor(X, 2);
+        X += dpp<kDppXor1>(X);
+        X += dpp<kDppXor2>(X);
         const float bias = 128.0f * X;
         acc[b][0] += bf16lo(md[t].x) * fmaf(r4[0], 16777216.0f, -bias);
         acc[b][1] += bf16hi(md[t].x) * fmaf(r4[1], 16777216.0f, -bias);
@@ -360,9 +436,9 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float v = acc[b][i];
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
-      v += __shfl_xor(v, 16);
+      v += dpp<kDppRor4>(v);      // kb 0..3 of the row of 16 (lane bits 2-3)
+      v += dpp<kDppRor8>(v);
+      v += __shfl_xor(v, 16);     // kb 4..7
       if ((lane & 28) == 0) sred[wave][b][rb * 16 + q * 4 + i] = v * sc;
     }
   }
@@ -377,6 +453,49 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
     sgrp[b][m * 32 + r] = s;
   }
   __syncthreads();
+
+  // ---- 7b. split K: publish this part, the last workgroup of the group adds all parts
+  if (ks > 1) {
+    const int gw = a.G * 32;                     // outputs per batch row of a group
+    const int nrec = a.batch * gw;               // floats per part record
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part, a.part_bytes);
+    const uint32_t rec = (uint32_t)((group * ks + kpart) * nrec) * 4u;
+    for (int e = tid; e < nrec / 4; e += blockDim.x) {
+      const int b = (4 * e) / gw, r = (4 * e) % gw;
+      st16_sys(pr, rec + 16u * e,
+               make_uint4(__float_as_uint(sgrp[b][r]), __float_as_uint(sgrp[b][r + 1]),
+                          __float_as_uint(sgrp[b][r + 2]), __float_as_uint(sgrp[b][r + 3])));
+    }
+    wait_vm();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&a.counters[group], 1u) == (unsigned)(ks - 1) ? 1 : 0;
+    __syncthreads();
+    if (!s_last) return;
+    const uint32_t rec0 = (uint32_t)(group * ks * nrec) * 4u;
+    for (int e = tid; e < nrec / 4; e += blockDim.x) {
+      uint4 v[8];
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        if (p < ks) v[p] = ld16_sys(pr, rec0 + (uint32_t)(p * nrec) * 4u + 16u * e);
+      float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        if (p < ks) {
+          acc4.x += __uint_as_float(v[p].x);
+          acc4.y += __uint_as_float(v[p].y);
+          acc4.z += __uint_as_float(v[p].z);
+          acc4.w += __uint_as_float(v[p].w);
+        }
+      const int b = (4 * e) / gw, r = (4 * e) % gw;
+      sgrp[b][r] = acc4.x;
+      sgrp[b][r + 1] = acc4.y;
+      sgrp[b][r + 2] = acc4.z;
+      sgrp[b][r + 3] = acc4.w;
+    }
+    if (tid == 0)  // ready for the next launch
+      __hip_atomic_store(&a.counters[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+  }
 
   // ---- 8. epilogue on the whole group
   if (a.op == OP_PLAIN) {
@@ -487,26 +606,68 @@ static void launch_b(const GemvArgs& a, int tpw, int blocks, int threads, hipStr
   }
 }
 
-static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char* what) {
+static int g_ksplit = 0;   // 0: automatic
+
+// Workgroups per group along K: enough groups x parts to fill the GPU (about 240
+// workgroups) when a launch has few output groups of many tiles (a group of 10 tiles
+// finishes sooner whole than split, the merge costs more than it saves), at least 2
+// K-tiles per part, at most 8.
+static int plan_ksplit(int n_groups, int G, int k_t) {
+  int ks;
+  if (g_ksplit > 0) {
+    ks = g_ksplit;
+  } else {
+    if (n_groups >= 192 || G * k_t < 20) return 1;
+    ks = (240 + n_groups - 1) / n_groups;
+    ks = ks < k_t / 2 ? ks : k_t / 2;
+  }
+  ks = ks > 8 ? 8 : ks;
+  ks = ks > k_t ? k_t : ks;
+  return ks < 1 ? 1 : ks;
+}
+
+static size_t split_bytes(int n_groups, int G, int ks, int batch) {
+  if (ks <= 1 || n_groups > Q4NX_WS_COUNTER_BYTES / 4) return 0;
+  return (size_t)Q4NX_WS_COUNTER_BYTES + (size_t)n_groups * ks * batch * G * 32 * 4;
+}
+
+static size_t ws_need(int n_groups, int G, int k_t, int batch) {
+  return split_bytes(n_groups, G, plan_ksplit(n_groups, G, k_t), batch);
+}
+
+static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char* what,
+                  void* ws = nullptr, size_t ws_bytes = 0) {
   const int B = round_batch(a.batch);
-  const int tpw = plan_tpw(a.G, a.k_t, a.batch);
+  int ks = plan_ksplit(n_groups, a.G, a.k_t);
+  const size_t need = split_bytes(n_groups, a.G, ks, a.batch);
+  if (ks > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256)))
+    ks = 1;   // no (or too small a) workspace: one workgroup per group
+  a.ksplit = ks;
+  if (ks > 1) {
+    a.counters = (unsigned*)ws;
+    a.part = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
+    a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
+  }
+  const int kpp = (a.k_t + ks - 1) / ks;   // largest part
+  const int tpw = plan_tpw(a.G, kpp, a.batch);
   Q4NX_REQUIRE(tpw > 0, Q4NX_ERR_SHAPE, "%s: K=%d is longer than one workgroup covers", what,
                a.k_t * 256);
-  const int wm = (a.k_t + tpw - 1) / tpw;
+  const int wm = (kpp + tpw - 1) / tpw;
   const int threads = a.G * wm * 64;
+  const int blocks = n_groups * ks;
   if (kind == 4) {
     switch (B) {
-      case 1: launch_b<4, 1>(a, tpw, n_groups, threads, s); break;
-      case 2: launch_b<4, 2>(a, tpw, n_groups, threads, s); break;
-      case 4: launch_b<4, 4>(a, tpw, n_groups, threads, s); break;
-      default: launch_b<4, 8>(a, tpw, n_groups, threads, s); break;
+      case 1: launch_b<4, 1>(a, tpw, blocks, threads, s); break;
+      case 2: launch_b<4, 2>(a, tpw, blocks, threads, s); break;
+      case 4: launch_b<4, 4>(a, tpw, blocks, threads, s); break;
+      default: launch_b<4, 8>(a, tpw, blocks, threads, s); break;
     }
   } else {
     switch (B) {
-      case 1: launch_b<8, 1>(a, tpw, n_groups, threads, s); break;
-      case 2: launch_b<8, 2>(a, tpw, n_groups, threads, s); break;
-      case 4: launch_b<8, 4>(a, tpw, n_groups, threads, s); break;
-      default: launch_b<8, 8>(a, tpw, n_groups, threads, s); break;
+      case 1: launch_b<8, 1>(a, tpw, blocks, threads, s); break;
+      case 2: launch_b<8, 2>(a, tpw, blocks, threads, s); break;
+      case 4: launch_b<8, 4>(a, tpw, blocks, threads, s); break;
+      default: launch_b<8, 8>(a, tpw, blocks, threads, s); break;
     }
   }
   return check_launch(what);
@@ -535,7 +696,8 @@ static int check_x(const void* x, int64_t x_stride, int k_tiles, const char* wha
 static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t* norm_w,
                       float eps, float* y, int n_tile_rows, int k_tiles, int batch,
                       int64_t x_stride, int64_t y_stride, const float* residual,
-                      unsigned long long* argmax_keys, void* stream, const char* what) {
+                      unsigned long long* argmax_keys, void* stream, const char* what,
+                      void* ws = nullptr, size_t ws_bytes = 0) {
   int rc = check_common(w, n_tile_rows, k_tiles, batch, what);
   if (rc) return rc;
   rc = check_x(x, x_stride, k_tiles, what);
@@ -569,7 +731,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
   a.y_stride = y_stride;
   a.residual = residual;
   a.argmax_keys = argmax_keys;
-  return launch(kind, a, n_tile_rows, (hipStream_t)stream, what);
+  return launch(kind, a, n_tile_rows, (hipStream_t)stream, what, ws, ws_bytes);
 }
 
 }  // namespace q4nx
@@ -578,6 +740,13 @@ using namespace q4nx;
 
 extern "C" {
 
+int q4nx_set_gemv_ksplit(int parts) {
+  Q4NX_REQUIRE(parts >= 0 && parts <= 8, Q4NX_ERR_ARG,
+               "K parts per group must be 0 (automatic) or 1..8, got %d", parts);
+  g_ksplit = parts;
+  return Q4NX_OK;
+}
+
 int q4nx_set_split_tiles(int tiles) {
   Q4NX_REQUIRE(tiles == 0 || tiles == 1 || tiles == 2 || tiles == 4, Q4NX_ERR_ARG,
                "tiles per wave must be 0 (automatic), 1, 2 or 4, got %d", tiles);
@@ -585,27 +754,26 @@ int q4nx_set_split_tiles(int tiles) {
   return Q4NX_OK;
 }
 
-// The GEMVs reduce inside one workgroup and need no workspace; the queries stay so a
-// caller written against the workspace convention keeps working.
+// Workspace of a split-K launch (0 when the launch has enough groups to fill the GPU).
+// Without it the launches still run, one workgroup per group.
 size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch) {
-  (void)kind; (void)n_tile_rows; (void)k_tiles; (void)batch;
-  return 0;
+  (void)kind;
+  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1 || batch > Q4NX_MAX_BATCH) return 0;
+  return ws_need(n_tile_rows, 1, k_tiles, batch);
 }
 
 int q4nx_gemv_q4(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
-  (void)ws; (void)ws_bytes;
   return gemv_plain(4, w, x, nullptr, 0.f, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
-                    residual, nullptr, stream, "q4nx_gemv_q4");
+                    residual, nullptr, stream, "q4nx_gemv_q4", ws, ws_bytes);
 }
 
 int q4nx_gemv_q8(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
-  (void)ws; (void)ws_bytes;
   return gemv_plain(8, w, x, nullptr, 0.f, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
-                    residual, nullptr, stream, "q4nx_gemv_q8");
+                    residual, nullptr, stream, "q4nx_gemv_q8", ws, ws_bytes);
 }
 
 int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const void* x,
@@ -618,8 +786,9 @@ int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const
 }
 
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {
-  (void)n_q_heads; (void)n_kv_heads; (void)k_tiles; (void)batch;
-  return 0;
+  if (n_q_heads < 1 || n_kv_heads < 1 || k_tiles < 1 || batch < 1 || batch > Q4NX_MAX_BATCH)
+    return 0;
+  return ws_need(n_q_heads + 2 * n_kv_heads, 2, k_tiles, batch);
 }
 
 int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n_q_heads,
@@ -628,7 +797,6 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
                   const float* rope_tab, int max_pos, uint16_t* q_out, uint16_t* k_cache,
                   uint16_t* v_cache, int64_t kv_b_stride, int64_t kv_h_stride, float* raw_out,
                   uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
-  (void)ws; (void)ws_bytes;
   const char* what = "q4nx_qkv_rope";
   for (const void* p : {(const void*)wq, (const void*)wk, (const void*)wv}) {
     int rc = check_common(p, 2, k_tiles, batch, what);
@@ -681,19 +849,18 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
   a.n_q_heads = n_q_heads;
   a.n_kv_heads = n_kv_heads;
   a.raw_out = raw_out;
-  return launch(4, a, n_q_heads + 2 * n_kv_heads, (hipStream_t)stream, what);
+  return launch(4, a, n_q_heads + 2 * n_kv_heads, (hipStream_t)stream, what, ws, ws_bytes);
 }
 
 size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch) {
-  (void)n_tile_rows; (void)k_tiles; (void)batch;
-  return 0;
+  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1 || batch > Q4NX_MAX_BATCH) return 0;
+  return ws_need(n_tile_rows, 2, k_tiles, batch);
 }
 
 int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, int k_tiles,
                         const void* x, int64_t x_stride, const uint16_t* norm_w, float eps,
                         int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
                         uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
-  (void)ws; (void)ws_bytes;
   const char* what = "q4nx_gate_up_swiglu";
   for (const void* p : {(const void*)wg, (const void*)wu}) {
     int rc = check_common(p, n_tile_rows, k_tiles, batch, what);
@@ -728,7 +895,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
   a.h_out = h_out;
   a.h_stride = h_stride;
   a.raw_out = raw_out;
-  return launch(4, a, n_tile_rows, (hipStream_t)stream, what);
+  return launch(4, a, n_tile_rows, (hipStream_t)stream, what, ws, ws_bytes);
 }
 
 }  // extern "C"

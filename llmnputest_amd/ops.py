@@ -152,9 +152,22 @@ def decode_advance(keys: torch.Tensor, n_slots: int, tokens: torch.Tensor, pos: 
               _ptr(lens), _ptr(history), _ptr(step), hl, b, _stream())
 
 
+def round_bf16(x: torch.Tensor) -> torch.Tensor:
+    """bf16 rounding of an fp32 device tensor on the GPU (round to nearest even)."""
+    _dev(x, "x", torch.float32)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    _lib.call("q4nx_round_bf16", _ptr(x), _ptr(y), x.numel(), _stream())
+    return y
+
+
 def set_split_tiles(tiles_per_wave: int) -> None:
     """Tuning: K-tiles per wave for all GEMVs (0 = automatic, else 1, 2 or 4)."""
     _lib.call("q4nx_set_split_tiles", int(tiles_per_wave))
+
+
+def set_gemv_ksplit(parts: int) -> None:
+    """Tuning: workgroups per output group along K (0 = automatic, else 1..8)."""
+    _lib.call("q4nx_set_gemv_ksplit", int(parts))
 
 
 # ---------------------------------------------------------------- elementwise
@@ -291,7 +304,7 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     ws = ws or default_workspace()
     need = _lib.lib().q4nx_gqa_decode_ws_bytes(b, hq, hkv, max_len)
     if n_split:
-        need = max(need, WS_COUNTER_BYTES + b * hkv * n_split * (hq // hkv) * 66 * 4)
+        need = max(need, WS_COUNTER_BYTES + b * hkv * n_split * (hq // hkv) * 68 * 4)
     wp, wn = ws.get(need)
     _lib.call("q4nx_gqa_decode", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(of), b,
               hq, hkv, d, _ptr(lens), max_len, k_cache.stride(0), k_cache.stride(1),

@@ -77,10 +77,16 @@ def test_fused_and_attention_argument_errors():
 
 def test_ws_queries():
     lib = _lib.lib()
-    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1) == 0       # GEMVs reduce inside one workgroup
+    # 80 tile-rows do not fill the GPU: K is split 3 ways, partials [80][3][1][32] fp32
+    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1) == 65536 + 80 * 3 * 32 * 4
+    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 1) == 0      # enough tile-rows: no split
+    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9) == 0      # batch out of range
+    # 56 heads of 2 tile-rows: 5 parts of 2 K-tiles, [56][5][batch 2][64]
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2) == 65536 + 56 * 5 * 2 * 64 * 4
+    assert lib.q4nx_gate_up_ws_bytes(256, 10, 1) == 0
     assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64) == 0  # one split: no workspace
-    big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768)
-    assert big >= 65536 + 8 * 5 * 66 * 4 * 2
+    big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768)    # 64 splits of (acc[64], m, l, pad)
+    assert big == 65536 + 8 * 64 * 5 * 68 * 4
 
 
 @pytest.mark.parametrize("max_pos,theta", [(4096, 10000.0), (64, 500000.0)])

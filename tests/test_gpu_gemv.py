@@ -126,6 +126,31 @@ def test_gemv_tiles_per_wave(dev, k, tiles_per_wave):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))  # deterministic
 
 
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("parts,batch,n,k", [(2, 1, 2560, 2560), (3, 3, 2560, 8192),
+                                             (5, 1, 1024, 2560), (8, 8, 512, 8192),
+                                             (0, 1, 2560, 8192), (0, 2, 2560, 2560)])
+def test_gemv_ksplit(dev, kind, parts, batch, n, k):
+    """K split over several workgroups per tile-row (last one adds the parts in order):
+    same answer as the oracle, with a residual, bit-identical run after run."""
+    raw, rng = _tiles(kind, n, k, 11)
+    x = synth.random_bf16(rng, (batch, k))
+    res = rng.standard_normal((batch, n)).astype(np.float32)
+    w, xd, rd = _dev_u8(raw, dev), _dev_bf16(x, dev), torch.from_numpy(res).to(dev)
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64).reshape(batch, n) + res
+    ws = ops.Workspace(1 << 20, device=dev)
+    ops.set_gemv_ksplit(parts)
+    try:
+        y1 = ops.gemv(w, kind, xd, n // 32, k // 256, residual=rd, ws=ws).cpu().numpy()
+        y2 = ops.gemv(w, kind, xd, n // 32, k // 256, residual=rd, ws=ws).cpu().numpy()
+    finally:
+        ops.set_gemv_ksplit(0)
+    for b in range(batch):
+        rel, cos = qo.metrics(y1[b], ref[b])
+        assert rel < REL and cos > COS, (b, rel, cos)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
 def test_gemv_residual_and_ones(dev):
     n, k = 2560, 2560
     raw, rng = _tiles("q4", n, k, 7)

@@ -43,6 +43,26 @@ def assert_bf16_close(got_bits, ref_f64, max_frac=1e-3):
     assert (diff > 0).mean() <= max_frac, float((diff > 0).mean())
 
 
+# ------------------------------------------------------------------ bf16 rounding
+
+def test_round_bf16_bitexact(dev):
+    """The device rounding every kernel uses equals the oracle's RNE on every class of
+    input: both parities of exact halfway cases, subnormals, infinities, extremes, NaN."""
+    rng = np.random.default_rng(9)
+    halves = (np.arange(1 << 16, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    near = (np.arange(1 << 16, dtype=np.uint32) << 16 | 0x7FFF).view(np.float32)
+    sub = (rng.integers(1, 1 << 23, 20000, dtype=np.uint32)).view(np.float32)
+    edge = np.array([0.0, -0.0, np.inf, -np.inf, 3.4028235e38, -3.4028235e38, 1e-45, 2 ** -126,
+                     3.3961776e38, 65504.0], np.float32)
+    x = np.concatenate([halves, near, sub, -sub, edge,
+                        rng.standard_normal(100000).astype(np.float32) * 1e3])
+    finite_or_inf = ~np.isnan(x)
+    got = bits(ops.round_bf16(torch.from_numpy(x).to(dev)))
+    want = qo.bf16_round(x)
+    assert np.array_equal(got[finite_or_inf], want[finite_or_inf])
+    assert np.isnan(qo.bf16_to_f32(got[~finite_or_inf])).all()
+
+
 # ------------------------------------------------------------------ RMSNorm
 
 @pytest.mark.parametrize("xdtype", ["bf16", "f32"])
@@ -109,8 +129,18 @@ def test_swiglu(dev, in_f32):
 
 # ------------------------------------------------------------------ fused [q,k,v,RoPE]
 
-@pytest.mark.parametrize("batch,norm", [(1, False), (1, True), (3, True)])
-def test_qkv_rope(dev, batch, norm):
+@pytest.fixture
+def ksplit(request):
+    """Force the GEMV K-split (0 = automatic) for one test, then restore automatic."""
+    ops.set_gemv_ksplit(request.param)
+    yield request.param
+    ops.set_gemv_ksplit(0)
+
+
+@pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (1, True, 0), (3, True, 0),
+                                               (3, True, 1), (2, True, 8)],
+                         indirect=["ksplit"])
+def test_qkv_rope(dev, batch, norm, ksplit):
     rng = np.random.default_rng(13)
     hq, hkv, hid, lmax = 40, 8, 2560, 512
     kt = hid // 256
@@ -164,8 +194,9 @@ def test_qkv_rope(dev, batch, norm):
 
 # ------------------------------------------------------------------ fused [gate,up,SwiGLU]
 
-@pytest.mark.parametrize("batch,norm", [(1, False), (2, True)])
-def test_gate_up_swiglu(dev, batch, norm):
+@pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (2, True, 0), (1, True, 2),
+                                               (3, True, 5)], indirect=["ksplit"])
+def test_gate_up_swiglu(dev, batch, norm, ksplit):
     rng = np.random.default_rng(14)
     hid, inter = 2560, 8192
     kt = hid // 256
@@ -232,6 +263,25 @@ def test_gqa_decode_uniform_softmax(dev):
                         want_f32=True)[1]
     expect = np.repeat(qo.bf16_to_f32(v).astype(np.float64).mean(axis=2), 5, axis=1)
     assert_close(of.cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("hq,hkv,L", [(8, 8, 300), (16, 2, 1500), (64, 8, 700), (24, 8, 129)])
+def test_gqa_decode_group_sizes(dev, hq, hkv, L):
+    """Other query-group sizes (1, 8, 8, 3 query heads per kv head), called twice on one
+    workspace so the split counters must have been left at zero."""
+    rng = np.random.default_rng(19 + hq)
+    q = synth.random_bf16(rng, (2, hq, 64))
+    k = synth.random_bf16(rng, (2, hkv, L, 64))
+    v = synth.random_bf16(rng, (2, hkv, L, 64))
+    lens = np.array([L, max(1, L // 3)], np.int32)
+    ws = ops.Workspace(8 << 20, device=dev)
+    args = (bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev), torch.from_numpy(lens).to(dev),
+            0.125)
+    of1 = ops.gqa_decode(*args, want_f32=True, ws=ws)[1].cpu().numpy()
+    of2 = ops.gqa_decode(*args, want_f32=True, ws=ws)[1].cpu().numpy()
+    ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v), lens, 0.125)
+    assert_close(of1, ref)
+    assert np.array_equal(of1, of2)
 
 
 @pytest.mark.parametrize("n_split", [1, 2, 7, 33])
