@@ -83,13 +83,18 @@ int q4nx_gemv_q8(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
  * in the prologue (granite_rmsnorm.h:45-80 fused into the GEMV). kind is Q4NX_KIND_Q4 or
  * Q4NX_KIND_Q8. argmax_keys (optional, uint64 [batch][n_tile_rows]) receives for every
  * tile-row an order-preserving key of (max y over its 32 rows, first such row);
- * q4nx_decode_advance reduces them. y may be NULL when only the keys are wanted. No
- * reference counterpart for the fusions: the reference runs the final norm and argmax
- * on the host (chat.py:74-78 through transformers' generate). */
+ * q4nx_decode_advance reduces them. y may be NULL when only the keys are wanted.
+ * ssq_out (optional, fp32 [batch][n_tile_rows]): sum of y^2 over each tile-row's 32
+ * outputs. ssq_in (optional, with norm_w; fp32 [batch][K/32], K <= 8192): the same
+ * partial sums for x, as the producer of x wrote them; the prologue then adds these
+ * (in a fixed order) instead of reducing x across the workgroup. ws as for the GEMVs
+ * above (K split when the launch has few tile-rows). No reference counterpart for the
+ * fusions: the reference runs the final norm and argmax on the host (chat.py:74-78
+ * through transformers' generate). */
 int q4nx_gemv_ex(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const void *x,
-                 int64_t x_stride, const uint16_t *norm_w, float eps, int batch, float *y,
-                 int64_t y_stride, const float *residual, uint64_t *argmax_keys,
-                 void *stream);
+                 int64_t x_stride, const uint16_t *norm_w, float eps, const float *ssq_in,
+                 int batch, float *y, int64_t y_stride, const float *residual, float *ssq_out,
+                 uint64_t *argmax_keys, void *ws, size_t ws_bytes, void *stream);
 
 /* Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
 int q4nx_set_split_tiles(int tiles_per_wave);
@@ -133,11 +138,13 @@ int q4nx_swiglu(const void *g, const void *u, int in_f32, uint16_t *y, float *y_
  * [batch][x_stride] normalised in the prologue (RMSNorm with norm_w, eps).
  * Cache layout: k_cache[b][kv_head][l][64] with strides (kv_b_stride, kv_h_stride) in
  * elements; l < max_pos. raw_out (optional): fp32 [batch][(n_q+2*n_kv)*64] GEMV outputs
- * before narrowing. xn_out (optional): bf16 [batch][K] normalised input. */
+ * before narrowing. xn_out (optional): bf16 [batch][K] normalised input. ssq_in: as in
+ * q4nx_gemv_ex. */
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch);
 int q4nx_qkv_rope(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, int n_q_heads,
                   int n_kv_heads, int k_tiles, const void *x, int64_t x_stride,
-                  const uint16_t *norm_w, float eps, int batch, const int32_t *positions,
+                  const uint16_t *norm_w, float eps, const float *ssq_in, int batch,
+                  const int32_t *positions,
                   const float *rope_tab, int max_pos, uint16_t *q_out, uint16_t *k_cache,
                   uint16_t *v_cache, int64_t kv_b_stride, int64_t kv_h_stride,
                   float *raw_out, uint16_t *xn_out, void *ws, size_t ws_bytes, void *stream);
@@ -149,7 +156,8 @@ int q4nx_qkv_rope(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, int n
 size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch);
 int q4nx_gate_up_swiglu(const uint8_t *wg, const uint8_t *wu, int n_tile_rows,
                         int k_tiles, const void *x, int64_t x_stride,
-                        const uint16_t *norm_w, float eps, int batch, uint16_t *h_out,
+                        const uint16_t *norm_w, float eps, const float *ssq_in, int batch,
+                        uint16_t *h_out,
                         int64_t h_stride, float *raw_out, uint16_t *xn_out, void *ws,
                         size_t ws_bytes, void *stream);
 
@@ -174,10 +182,11 @@ int q4nx_round_bf16(const float *x, uint16_t *y, int64_t n, void *stream);
 
 /* ---------------------------------------------------------------- decode-step helpers
  * h[b][:] = fp32 row tokens[b] of a q8-tiled [vocab][hidden] matrix (a tied lm_head
- * used as the embedding table). No reference counterpart: the reference has no token
- * loop (README.md:295-311). */
-int q4nx_embed_q8(const uint8_t *w, const int32_t *tokens, float *h, int vocab,
-                  int hidden, int batch, void *stream);
+ * used as the embedding table); ssq_out (optional, [batch][hidden/32]) as in
+ * q4nx_gemv_ex. No reference counterpart: the reference has no token loop
+ * (README.md:295-311). */
+int q4nx_embed_q8(const uint8_t *w, const int32_t *tokens, float *h, float *ssq_out,
+                  int vocab, int hidden, int batch, void *stream);
 /* idx[b] = argmax_n logits[b][n] (first maximum), max[b] its value (optional). */
 int q4nx_argmax(const float *logits, int n, int batch, int64_t stride, int32_t *idx,
                 float *max_val, void *stream);

@@ -28,8 +28,8 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_gemv_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
     "q4nx_gemv_q4": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_p]),
     "q4nx_gemv_q8": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_p]),
-    "q4nx_gemv_ex": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_i, c_p, c_i64, c_p, c_p,
-                           c_p]),
+    "q4nx_gemv_ex": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p, c_i64, c_p,
+                           c_p, c_p, c_p, c_sz, c_p]),
     "q4nx_set_split_tiles": (c_i, [c_i]),
     "q4nx_set_gemv_ksplit": (c_i, [c_i]),
     "q4nx_rmsnorm": (c_i, [c_p, c_i, c_p, c_p, c_p, c_i, c_i, c_f, c_p]),
@@ -37,16 +37,16 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_rope_table_host": (c_i, [c_p, c_i, c_i, c_d]),
     "q4nx_swiglu": (c_i, [c_p, c_p, c_i, c_p, c_p, c_i, c_i, c_p]),
     "q4nx_qkv_rope_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
-    "q4nx_qkv_rope": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_i64, c_p, c_f, c_i, c_p, c_p,
-                            c_i, c_p, c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_sz, c_p]),
+    "q4nx_qkv_rope": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p,
+                            c_p, c_i, c_p, c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_sz, c_p]),
     "q4nx_gate_up_ws_bytes": (c_sz, [c_i, c_i, c_i]),
-    "q4nx_gate_up_swiglu": (c_i, [c_p, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_i, c_p, c_i64,
-                                  c_p, c_p, c_p, c_sz, c_p]),
+    "q4nx_gate_up_swiglu": (c_i, [c_p, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p,
+                                  c_i64, c_p, c_p, c_p, c_sz, c_p]),
     "q4nx_gqa_decode_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
     "q4nx_gqa_decode": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
                               c_i64, c_f, c_i, c_p, c_sz, c_p]),
     "q4nx_round_bf16": (c_i, [c_p, c_p, c_i64, c_p]),
-    "q4nx_embed_q8": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
+    "q4nx_embed_q8": (c_i, [c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
     "q4nx_argmax": (c_i, [c_p, c_i, c_i, c_i64, c_p, c_p, c_p]),
     "q4nx_decode_advance": (c_i, [c_p, c_i, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p]),
 }

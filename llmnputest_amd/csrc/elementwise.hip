@@ -108,24 +108,28 @@ __global__ __launch_bounds__(256) void round_bf16_kernel(const float* __restrict
 // ------------------------------------------------------------------ embedding row of a q8 matrix
 __global__ __launch_bounds__(256) void embed_q8_kernel(const uint8_t* __restrict__ w,
                                                        const int32_t* __restrict__ tokens,
-                                                       float* __restrict__ h, int vocab,
+                                                       float* __restrict__ h,
+                                                       float* __restrict__ ssq_out, int vocab,
                                                        int hidden) {
   const int b = blockIdx.y;
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= hidden) return;
+  const int c = blockIdx.x * 256 + threadIdx.x;   // hidden % 256 == 0: every lane is live
   const int t = tokens[b];
-  if (t < 0 || t >= vocab) {
-    h[(size_t)b * hidden + c] = __builtin_nanf("");
-    return;
+  float v = __builtin_nanf("");
+  if (t >= 0 && t < vocab) {
+    const int k_t = hidden / 256;
+    const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
+    const int kt = c >> 8, k = c & 255, kb = k >> 5;
+    const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
+    const int g = kb * 32 + rb * 16 + r;
+    const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
+    const int code = (int)(int8_t)tile[kMetaBytes + rb * 4096 + k * 16 + r];
+    v = (float)code * bf16_to_f32(s);
   }
-  const int k_t = hidden / 256;
-  const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
-  const int kt = c >> 8, k = c & 255, kb = k >> 5;
-  const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
-  const int g = kb * 32 + rb * 16 + r;
-  const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
-  const int code = (int)(int8_t)tile[kMetaBytes + rb * 4096 + k * 16 + r];
-  h[(size_t)b * hidden + c] = (float)code * bf16_to_f32(s);
+  h[(size_t)b * hidden + c] = v;
+  if (ssq_out != nullptr) {   // sum of squares per 32 entries, for a following RMSNorm
+    const float s32 = group32_sum(v * v);
+    if ((c & 31) == 0) ssq_out[(size_t)b * (hidden / 32) + (c >> 5)] = s32;
+  }
 }
 
 // ------------------------------------------------------------------ argmax
@@ -269,13 +273,13 @@ int q4nx_round_bf16(const float* x, uint16_t* y, int64_t n, void* stream) {
   return check_launch("q4nx_round_bf16");
 }
 
-int q4nx_embed_q8(const uint8_t* w, const int32_t* tokens, float* h, int vocab, int hidden,
-                  int batch, void* stream) {
+int q4nx_embed_q8(const uint8_t* w, const int32_t* tokens, float* h, float* ssq_out, int vocab,
+                  int hidden, int batch, void* stream) {
   Q4NX_REQUIRE(w && tokens && h, Q4NX_ERR_ARG, "q4nx_embed_q8: w, tokens and h are required");
   Q4NX_REQUIRE(vocab > 0 && vocab % 32 == 0 && hidden > 0 && hidden % 256 == 0 && batch > 0,
                Q4NX_ERR_SHAPE, "q4nx_embed_q8: vocab=%d hidden=%d batch=%d", vocab, hidden, batch);
   hipLaunchKernelGGL(embed_q8_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0,
-                     (hipStream_t)stream, w, tokens, h, vocab, hidden);
+                     (hipStream_t)stream, w, tokens, h, ssq_out, vocab, hidden);
   return check_launch("q4nx_embed_q8");
 }
 

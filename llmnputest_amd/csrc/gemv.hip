@@ -53,11 +53,13 @@ struct GemvArgs {
   int64_t x_stride;
   const uint16_t* norm_w;
   float eps;
+  const float* ssq_in;   // optional [batch][K/32] sums of squares of x, per 32 entries
   uint16_t* xn_out;
   // plain
   float* y;
   int64_t y_stride;
   const float* residual;
+  float* ssq_out;        // optional [batch][n_tile_rows] sums of squares of y per tile-row
   // qkv
   uint16_t* q_out;
   uint16_t* k_cache;
@@ -188,12 +190,25 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  // with K split, this workgroup's tiles see only part of the row: the RMSNorm sum of
-  // squares reads the whole row (strided over all threads; three float4 per thread cover
-  // K <= 12 * blockDim, a remainder loop the rest)
+  // RMSNorm sum of squares handed over by the producer of x: K/32 partials per row, every
+  // wave sums them itself (same order everywhere) and needs no other wave
+  const bool pre_ssq = norm && a.ssq_in != nullptr;
+  const int n_ss = K / 32;
+  float sq[B][4];
+  if (pre_ssq) {
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sq[b][j] = a.ssq_in[min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1)];
+  }
+
+  // with K split and no partials given, this workgroup's tiles see only part of the row:
+  // the sum of squares reads the whole row (strided over all threads; three float4 per
+  // thread cover K <= 12 * blockDim, a remainder loop the rest)
   constexpr int kSsqIt = 3;
   float4 hs[B][kSsqIt];
-  const bool split_norm = norm && ks > 1;
+  const bool split_norm = norm && ks > 1 && !pre_ssq;
   if (split_norm) {
 #pragma unroll
     for (int it = 0; it < kSsqIt; ++it) {
@@ -239,6 +254,14 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int b = 0; b < B; ++b) pin(hs[b][it]);
   }
+  if (pre_ssq) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float4 v = make_float4(sq[b][0], sq[b][1], sq[b][2], sq[b][3]);
+      pin(v);
+      sq[b][0] = v.x; sq[b][1] = v.y; sq[b][2] = v.z; sq[b][3] = v.w;
+    }
+  }
 
   uint4 xr[B][TPW];       // 8 bf16 per lane per tile
   float hx[B][TPW][8];    // fp32 residual values (RMSNorm prologue only)
@@ -275,7 +298,17 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         }
     }
   }
-  if (norm) {
+  float inv_rms[B];
+  if (pre_ssq) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < n_ss) s += sq[b][j];
+      inv_rms[b] = 1.0f / sqrtf(wave_sum(s) / (float)K + a.eps);
+    }
+  } else if (norm) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       float s = ssq[b];
@@ -296,17 +329,21 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
     for (int b = 0; b < B; ++b) {
       float s = 0.f;
       for (int w = 0; w < n_sum_waves; ++w) s += snorm[w][b];
-      const float inv = 1.0f / sqrtf(s / (float)K + a.eps);
+      inv_rms[b] = 1.0f / sqrtf(s / (float)K + a.eps);
+    }
+  }
+  if (norm) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const float inv = inv_rms[b];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const uint32_t wv[4] = {nw[t].x, nw[t].y, nw[t].z, nw[t].w};
         uint32_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint16_t lo = f32_to_bf16((hx[b][t][2 * i] * inv) * bf16lo(wv[i]));
-          const uint16_t hi = f32_to_bf16((hx[b][t][2 * i + 1] * inv) * bf16hi(wv[i]));
-          o[i] = (uint32_t)lo | ((uint32_t)hi << 16);
-        }
+        for (int i = 0; i < 4; ++i)
+          o[i] = pack_bf16x2((hx[b][t][2 * i] * inv) * bf16lo(wv[i]),
+                             (hx[b][t][2 * i + 1] * inv) * bf16hi(wv[i]));
         xr[b][t] = b < a.batch ? make_uint4(o[0], o[1], o[2], o[3]) : make_uint4(0, 0, 0, 0);
         if (a.xn_out != nullptr && group == 0 && member == 0 && rb == 0 && t < ntw &&
             b < a.batch)
@@ -501,14 +538,21 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   if (a.op == OP_PLAIN) {
     if (a.argmax_keys != nullptr && tid < B) skey[tid] = 0ull;
     if (a.argmax_keys != nullptr) __syncthreads();
-    for (int e = tid; e < B * 32; e += blockDim.x) {
+    for (int e0 = 0; e0 < B * 32; e0 += blockDim.x) {   // uniform trip count: 32-lane sums
+      const int e = e0 + tid;
       const int b = e >> 5, r = e & 31;
-      if (b < a.batch) {
+      const bool live = e < B * 32 && b < a.batch;
+      float v = 0.f;
+      if (live) {
         const int64_t n = (int64_t)tr * 32 + r;
-        float v = sgrp[b][r];
+        v = sgrp[b][r];
         if (a.residual != nullptr) v += a.residual[b * a.y_stride + n];
         if (a.y != nullptr) a.y[b * a.y_stride + n] = v;
         if (a.argmax_keys != nullptr) atomicMax(&skey[b], argmax_key(v, (uint32_t)n));
+      }
+      if (a.ssq_out != nullptr) {   // sum of squares of the tile-row's 32 outputs
+        const float sq32 = group32_sum(v * v);
+        if (live && r == 0) a.ssq_out[(int64_t)b * a.n_tr[0] + tr] = sq32;
       }
     }
     if (a.argmax_keys != nullptr) {   // one slot per (batch row, tile-row): no contention
@@ -693,15 +737,28 @@ static int check_x(const void* x, int64_t x_stride, int k_tiles, const char* wha
   return Q4NX_OK;
 }
 
+static int check_ssq_in(const float* ssq_in, const uint16_t* norm_w, int k_tiles,
+                        const char* what) {
+  Q4NX_REQUIRE(ssq_in == nullptr || (norm_w != nullptr && Q4NX_ALIGNED(ssq_in, 4)),
+               Q4NX_ERR_ARG, "%s: ssq_in goes with norm_w (4-byte aligned)", what);
+  Q4NX_REQUIRE(ssq_in == nullptr || k_tiles <= 32, Q4NX_ERR_SHAPE,
+               "%s: ssq_in supports K <= 8192, K=%d", what, k_tiles * 256);
+  return Q4NX_OK;
+}
+
 static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t* norm_w,
-                      float eps, float* y, int n_tile_rows, int k_tiles, int batch,
-                      int64_t x_stride, int64_t y_stride, const float* residual,
-                      unsigned long long* argmax_keys, void* stream, const char* what,
-                      void* ws = nullptr, size_t ws_bytes = 0) {
+                      float eps, const float* ssq_in, float* y, int n_tile_rows, int k_tiles,
+                      int batch, int64_t x_stride, int64_t y_stride, const float* residual,
+                      float* ssq_out, unsigned long long* argmax_keys, void* stream,
+                      const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
   int rc = check_common(w, n_tile_rows, k_tiles, batch, what);
   if (rc) return rc;
   rc = check_x(x, x_stride, k_tiles, what);
   if (rc) return rc;
+  rc = check_ssq_in(ssq_in, norm_w, k_tiles, what);
+  if (rc) return rc;
+  Q4NX_REQUIRE(ssq_out == nullptr || (y != nullptr && Q4NX_ALIGNED(ssq_out, 4)), Q4NX_ERR_ARG,
+               "%s: ssq_out goes with y (4-byte aligned)", what);
   Q4NX_REQUIRE(norm_w == nullptr || Q4NX_ALIGNED(norm_w, 16), Q4NX_ERR_ARG,
                "%s: norm_w must be 16-byte aligned", what);
   Q4NX_REQUIRE((y != nullptr && Q4NX_ALIGNED(y, 4)) || (y == nullptr && argmax_keys != nullptr),
@@ -723,6 +780,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
     a.hres = (const float*)x;
     a.norm_w = norm_w;
     a.eps = eps;
+    a.ssq_in = ssq_in;
   } else {
     a.x = (const uint16_t*)x;
   }
@@ -730,6 +788,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
   a.y = y;
   a.y_stride = y_stride;
   a.residual = residual;
+  a.ssq_out = ssq_out;
   a.argmax_keys = argmax_keys;
   return launch(kind, a, n_tile_rows, (hipStream_t)stream, what, ws, ws_bytes);
 }
@@ -765,24 +824,26 @@ size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch) {
 int q4nx_gemv_q4(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
-  return gemv_plain(4, w, x, nullptr, 0.f, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
-                    residual, nullptr, stream, "q4nx_gemv_q4", ws, ws_bytes);
+  return gemv_plain(4, w, x, nullptr, 0.f, nullptr, y, n_tile_rows, k_tiles, batch, x_stride,
+                    y_stride, residual, nullptr, nullptr, stream, "q4nx_gemv_q4", ws, ws_bytes);
 }
 
 int q4nx_gemv_q8(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
                  size_t ws_bytes, void* stream) {
-  return gemv_plain(8, w, x, nullptr, 0.f, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
-                    residual, nullptr, stream, "q4nx_gemv_q8", ws, ws_bytes);
+  return gemv_plain(8, w, x, nullptr, 0.f, nullptr, y, n_tile_rows, k_tiles, batch, x_stride,
+                    y_stride, residual, nullptr, nullptr, stream, "q4nx_gemv_q8", ws, ws_bytes);
 }
 
 int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const void* x,
-                 int64_t x_stride, const uint16_t* norm_w, float eps, int batch, float* y,
-                 int64_t y_stride, const float* residual, uint64_t* argmax_keys, void* stream) {
+                 int64_t x_stride, const uint16_t* norm_w, float eps, const float* ssq_in,
+                 int batch, float* y, int64_t y_stride, const float* residual, float* ssq_out,
+                 uint64_t* argmax_keys, void* ws, size_t ws_bytes, void* stream) {
   Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
                "q4nx_gemv_ex: kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", kind);
-  return gemv_plain(kind, w, x, norm_w, eps, y, n_tile_rows, k_tiles, batch, x_stride, y_stride,
-                    residual, (unsigned long long*)argmax_keys, stream, "q4nx_gemv_ex");
+  return gemv_plain(kind, w, x, norm_w, eps, ssq_in, y, n_tile_rows, k_tiles, batch, x_stride,
+                    y_stride, residual, ssq_out, (unsigned long long*)argmax_keys, stream,
+                    "q4nx_gemv_ex", ws, ws_bytes);
 }
 
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {
@@ -793,7 +854,8 @@ size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int ba
 
 int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n_q_heads,
                   int n_kv_heads, int k_tiles, const void* x, int64_t x_stride,
-                  const uint16_t* norm_w, float eps, int batch, const int32_t* positions,
+                  const uint16_t* norm_w, float eps, const float* ssq_in, int batch,
+                  const int32_t* positions,
                   const float* rope_tab, int max_pos, uint16_t* q_out, uint16_t* k_cache,
                   uint16_t* v_cache, int64_t kv_b_stride, int64_t kv_h_stride, float* raw_out,
                   uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
@@ -806,6 +868,8 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
                "%s: n_q_heads=%d must be a positive multiple of n_kv_heads=%d", what, n_q_heads,
                n_kv_heads);
   int rc = check_x(x, x_stride, k_tiles, what);
+  if (rc) return rc;
+  rc = check_ssq_in(ssq_in, norm_w, k_tiles, what);
   if (rc) return rc;
   Q4NX_REQUIRE(norm_w == nullptr || Q4NX_ALIGNED(norm_w, 16), Q4NX_ERR_ARG,
                "%s: norm_w must be 16-byte aligned", what);
@@ -833,6 +897,7 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
     a.hres = (const float*)x;
     a.norm_w = norm_w;
     a.eps = eps;
+    a.ssq_in = ssq_in;
   } else {
     a.x = (const uint16_t*)x;
   }
@@ -859,7 +924,7 @@ size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch) {
 
 int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, int k_tiles,
                         const void* x, int64_t x_stride, const uint16_t* norm_w, float eps,
-                        int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
+                        const float* ssq_in, int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
                         uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
   const char* what = "q4nx_gate_up_swiglu";
   for (const void* p : {(const void*)wg, (const void*)wu}) {
@@ -867,6 +932,8 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
     if (rc) return rc;
   }
   int rc = check_x(x, x_stride, k_tiles, what);
+  if (rc) return rc;
+  rc = check_ssq_in(ssq_in, norm_w, k_tiles, what);
   if (rc) return rc;
   Q4NX_REQUIRE(norm_w == nullptr || Q4NX_ALIGNED(norm_w, 16), Q4NX_ERR_ARG,
                "%s: norm_w must be 16-byte aligned", what);
@@ -887,6 +954,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
     a.hres = (const float*)x;
     a.norm_w = norm_w;
     a.eps = eps;
+    a.ssq_in = ssq_in;
   } else {
     a.x = (const uint16_t*)x;
   }

@@ -184,6 +184,8 @@ class GraniteDecoder:
         self.v_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.n_layers)]
         self.rope = ops.rope_table(self.max_len, c.head_dim, c.theta, device=dev)
         self.h = torch.zeros((b, c.hidden), dtype=torch.float32, device=dev)
+        # sums of h^2 per 32 entries, written by each producer of h for the next RMSNorm
+        self.ssq = torch.zeros((b, c.hidden // 32), dtype=torch.float32, device=dev)
         self.q = torch.zeros((b, c.q_dim), dtype=torch.bfloat16, device=dev)
         self.attn = torch.zeros((b, c.n_q, c.head_dim), dtype=torch.bfloat16, device=dev)
         self.mlp = torch.zeros((b, c.inter), dtype=torch.bfloat16, device=dev)
@@ -206,21 +208,24 @@ class GraniteDecoder:
         c, w = self.cfg, self.w
         kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
         h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
-        ops.embed_q8(w.lm_head, self.tokens[:b], c.vocab, c.hidden, out=h)
+        ssq = self.ssq[:b]
+        ops.embed_q8(w.lm_head, self.tokens[:b], c.vocab, c.hidden, out=h, ssq_out=ssq)
         for li, L in enumerate(w.layers):
             kc, vc = self.k_cache[li], self.v_cache[li]
             ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
-                         kc, vc, q_out=q, norm_w=L["norm_in"], eps=c.eps, ws=self.ws)
+                         kc, vc, q_out=q, norm_w=L["norm_in"], eps=c.eps, ws=self.ws,
+                         ssq_in=ssq)
             ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
                            max_len=self.max_len, out=attn, ws=self.ws)
-            ops.gemv(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q, residual=h,
-                     out=h, ws=self.ws)
+            ops.gemv_ex(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q, residual=h,
+                        out=h, ssq_out=ssq, ws=self.ws)
             ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
-                               norm_w=L["norm_post"], eps=c.eps, ws=self.ws)
-            ops.gemv(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h, ws=self.ws)
+                               norm_w=L["norm_post"], eps=c.eps, ws=self.ws, ssq_in=ssq)
+            ops.gemv_ex(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h,
+                        ssq_out=ssq, ws=self.ws)
         # final RMSNorm fused into the lm_head prologue, greedy argmax into its epilogue
         ops.gemv_ex(w.lm_head, "q8", h, c.vocab // 32, kt_h, norm_w=w.norm_final, eps=c.eps,
-                    out=self.logits[:b], argmax_keys=self.keys[:b])
+                    out=self.logits[:b], argmax_keys=self.keys[:b], ssq_in=ssq, ws=self.ws)
 
     def step(self, tokens, positions) -> torch.Tensor:
         """One decode step, eager: tokens/positions for B sequences -> fp32 logits [B, V]."""

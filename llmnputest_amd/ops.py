@@ -116,13 +116,24 @@ def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_ti
     return out.reshape(n) if squeeze else out
 
 
+def _ssq(t, name, b, n):
+    if t is not None:
+        _dev(t, name, torch.float32)
+        if t.numel() < b * n:
+            raise ValueError(f"{name} needs batch * {n} entries")
+
+
 def gemv_ex(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
             norm_w: torch.Tensor | None = None, eps: float = 1e-5,
             residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
-            argmax_keys: torch.Tensor | None = None, want_y: bool = True):
+            argmax_keys: torch.Tensor | None = None, want_y: bool = True,
+            ssq_in: torch.Tensor | None = None, ssq_out: torch.Tensor | None = None,
+            ws: Workspace | None = None):
     """General GEMV: y = residual + W f(x), f = RMSNorm(x; norm_w) when norm_w is given
     (x fp32 [B, K]) else identity (x bf16). argmax_keys: int64 [B, n_tile_rows] receives one
-    order-preserving (max, first row) key per tile-row -- reduced by `decode_advance`."""
+    order-preserving (max, first row) key per tile-row -- reduced by `decode_advance`.
+    ssq_out: fp32 [B, n_tile_rows] sums of y^2 per tile-row; ssq_in: the same for x
+    ([B, K/32], written by x's producer) so the norm needs no cross-wave reduction."""
     _tiles(tiles, kind, n_tile_rows, k_tiles)
     _dev(x, "x", torch.float32 if norm_w is not None else torch.bfloat16)
     x2 = x.reshape(1, -1) if x.dim() == 1 else x
@@ -136,9 +147,13 @@ def gemv_ex(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k
         _dev(argmax_keys, "argmax_keys", torch.int64)
         if argmax_keys.numel() < b * n_tile_rows:
             raise ValueError("argmax_keys needs batch * n_tile_rows entries")
+    _ssq(ssq_in, "ssq_in", b, k_tiles * 8)
+    _ssq(ssq_out, "ssq_out", b, n_tile_rows)
+    ws = ws or default_workspace()
+    wp, wn = ws.get(_lib.lib().q4nx_gemv_ws_bytes(KIND[kind], n_tile_rows, k_tiles, b))
     _lib.call("q4nx_gemv_ex", KIND[kind], _ptr(tiles), n_tile_rows, k_tiles, _ptr(x2),
-              x2.shape[1], _ptr(norm_w), float(eps), b, _ptr(out), n, _ptr(residual),
-              _ptr(argmax_keys), _stream())
+              x2.shape[1], _ptr(norm_w), float(eps), _ptr(ssq_in), b, _ptr(out), n,
+              _ptr(residual), _ptr(ssq_out), _ptr(argmax_keys), wp, wn, _stream())
     return out
 
 
@@ -233,8 +248,9 @@ def qkv_rope(wq, wk, wv, n_q_heads: int, n_kv_heads: int, k_tiles: int, x: torch
              positions: torch.Tensor, table: torch.Tensor, k_cache: torch.Tensor,
              v_cache: torch.Tensor, q_out: torch.Tensor | None = None,
              norm_w: torch.Tensor | None = None, eps: float = 1e-5, raw_out=None, xn_out=None,
-             ws: Workspace | None = None) -> torch.Tensor:
-    """[q,k,v,RoPE] in one launch. x: bf16 [B, K], or fp32 residual [B, K] with norm_w.
+             ws: Workspace | None = None, ssq_in: torch.Tensor | None = None) -> torch.Tensor:
+    """[q,k,v,RoPE] in one launch. x: bf16 [B, K], or fp32 residual [B, K] with norm_w
+    (and optionally its per-32 sums of squares ssq_in [B, K/32]).
     Caches: bf16 [B, Hkv, Lmax, 64]. Returns q_out bf16 [B, Hq*64]."""
     for t, n, kk in ((wq, "wq", n_q_heads), (wk, "wk", n_kv_heads), (wv, "wv", n_kv_heads)):
         _tiles(t, "q4", kk * 2, k_tiles, n)
@@ -254,7 +270,8 @@ def qkv_rope(wq, wk, wv, n_q_heads: int, n_kv_heads: int, k_tiles: int, x: torch
     wp, wn = ws.get(_lib.lib().q4nx_qkv_rope_ws_bytes(n_q_heads, n_kv_heads, k_tiles, b))
     lmax = k_cache.shape[2]
     _lib.call("q4nx_qkv_rope", _ptr(wq), _ptr(wk), _ptr(wv), n_q_heads, n_kv_heads, k_tiles,
-              _ptr(x), x.shape[1], _ptr(norm_w), float(eps), b, _ptr(positions), _ptr(table),
+              _ptr(x), x.shape[1], _ptr(norm_w), float(eps), _ptr(ssq_in), b, _ptr(positions),
+              _ptr(table),
               table.shape[0] if table.shape[0] < lmax else lmax, _ptr(q_out), _ptr(k_cache),
               _ptr(v_cache), k_cache.stride(0), k_cache.stride(1), _ptr(raw_out), _ptr(xn_out),
               wp, wn, _stream())
@@ -264,7 +281,8 @@ def qkv_rope(wq, wk, wv, n_q_heads: int, n_kv_heads: int, k_tiles: int, x: torch
 def gate_up_swiglu(wg, wu, n_tile_rows: int, k_tiles: int, x: torch.Tensor,
                    h_out: torch.Tensor | None = None, norm_w: torch.Tensor | None = None,
                    eps: float = 1e-5, raw_out=None, xn_out=None,
-                   ws: Workspace | None = None) -> torch.Tensor:
+                   ws: Workspace | None = None,
+                   ssq_in: torch.Tensor | None = None) -> torch.Tensor:
     """[gate, up, SwiGLU] in one launch; returns bf16 h [B, N]."""
     _tiles(wg, "q4", n_tile_rows, k_tiles, "wg")
     _tiles(wu, "q4", n_tile_rows, k_tiles, "wu")
@@ -276,7 +294,7 @@ def gate_up_swiglu(wg, wu, n_tile_rows: int, k_tiles: int, x: torch.Tensor,
     ws = ws or default_workspace()
     wp, wn = ws.get(_lib.lib().q4nx_gate_up_ws_bytes(n_tile_rows, k_tiles, b))
     _lib.call("q4nx_gate_up_swiglu", _ptr(wg), _ptr(wu), n_tile_rows, k_tiles, _ptr(x),
-              x.shape[1], _ptr(norm_w), float(eps), b, _ptr(h_out), h_out.stride(0),
+              x.shape[1], _ptr(norm_w), float(eps), _ptr(ssq_in), b, _ptr(h_out), h_out.stride(0),
               _ptr(raw_out), _ptr(xn_out), wp, wn, _stream())
     return h_out
 
@@ -315,13 +333,16 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
 # ---------------------------------------------------------------- decode helpers
 
 def embed_q8(tiles: torch.Tensor, tokens: torch.Tensor, vocab: int, hidden: int,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None,
+             ssq_out: torch.Tensor | None = None) -> torch.Tensor:
     _tiles(tiles, "q8", vocab // 32, hidden // 256, "tiles")
     _dev(tokens, "tokens", torch.int32)
     b = tokens.numel()
     if out is None:
         out = torch.empty((b, hidden), dtype=torch.float32, device=tiles.device)
-    _lib.call("q4nx_embed_q8", _ptr(tiles), _ptr(tokens), _ptr(out), vocab, hidden, b, _stream())
+    _ssq(ssq_out, "ssq_out", b, hidden // 32)
+    _lib.call("q4nx_embed_q8", _ptr(tiles), _ptr(tokens), _ptr(out), _ptr(ssq_out), vocab, hidden,
+              b, _stream())
     return out
 
 

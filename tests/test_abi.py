@@ -50,9 +50,14 @@ def test_gemv_argument_errors():
     assert rc == ERR_SHAPE and "batch" in msg
     rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 8, 10, 1, 2000, 256, None, None, 0, None)
     assert rc == ERR_SHAPE and "x_stride" in msg           # K = 2560 does not fit a 2000 row
-    rc, msg = rc_msg("q4nx_gemv_ex", 5, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), 1, fake,
-                     256, None, None, None)
+    rc, msg = rc_msg("q4nx_gemv_ex", 5, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), None, 1,
+                     fake, 256, None, None, None, None, 0, None)
     assert rc == ERR_ARG and "kind" in msg
+    rc, msg = rc_msg("q4nx_gemv_ex", 4, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), fake, 1,
+                     fake, 256, None, None, None, None, 0, None)
+    assert rc == ERR_ARG and "ssq_in" in msg               # partial sums without a norm
+    rc, msg = rc_msg("q4nx_set_gemv_ksplit", 9)
+    assert rc == ERR_ARG
     rc, msg = rc_msg("q4nx_set_split_tiles", 3)
     assert rc == ERR_ARG
 
@@ -60,7 +65,7 @@ def test_gemv_argument_errors():
 def test_fused_and_attention_argument_errors():
     fake = C.c_void_p(0x10000)
     rc, msg = rc_msg("q4nx_qkv_rope", fake, fake, fake, 40, 7, 10, fake, 2560, None,
-                     C.c_float(1e-5), 1, fake, fake, 512, fake, fake, fake, 8 * 512 * 64,
+                     C.c_float(1e-5), None, 1, fake, fake, 512, fake, fake, fake, 8 * 512 * 64,
                      512 * 64, None, None, None, 0, None)
     assert rc == ERR_SHAPE and "n_kv_heads" in msg         # 40 % 7 != 0
     rc, msg = rc_msg("q4nx_gqa_decode", fake, fake, fake, fake, None, 1, 40, 8, 128, fake, 512,
@@ -69,7 +74,7 @@ def test_fused_and_attention_argument_errors():
     rc, msg = rc_msg("q4nx_gqa_decode", fake, fake, fake, fake, None, 1, 40, 8, 64, fake, 4096,
                      8 * 4096 * 64, 4096 * 64, C.c_float(0.125), 8, None, 0, None)
     assert rc == ERR_WS and "workspace" in msg
-    rc, msg = rc_msg("q4nx_embed_q8", fake, fake, fake, 100, 2560, 1, None)
+    rc, msg = rc_msg("q4nx_embed_q8", fake, fake, fake, None, 100, 2560, 1, None)
     assert rc == ERR_SHAPE                                 # vocab not a multiple of 32
     rc, msg = rc_msg("q4nx_dequant_q4", fake, None, 1, 1, 0, 0, None)
     assert rc == ERR_ARG

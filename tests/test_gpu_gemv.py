@@ -151,6 +151,51 @@ def test_gemv_ksplit(dev, kind, parts, batch, n, k):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
+@pytest.mark.parametrize("parts", [0, 1])
+def test_gemv_ex_norm_ssq_and_keys(dev, parts):
+    """gemv_ex: RMSNorm prologue from an fp32 residual (with and without the producer's
+    per-32 sums of squares), the sums of squares of its own output per tile-row, and
+    argmax keys that decode_advance turns into the first maximal row."""
+    rng = np.random.default_rng(12)
+    n, k, batch = 2560, 8192, 2
+    raw, _ = _tiles("q4", n, k, 12)
+    w = _dev_u8(raw, dev)
+    h = (rng.standard_normal((batch, k)) * 5).astype(np.float32)
+    nw = qo.bf16_round((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    res = rng.standard_normal((batch, n)).astype(np.float32)
+    hd, nwd = torch.from_numpy(h).to(dev), _dev_bf16(nw, dev)
+    ss_in = torch.from_numpy((h.astype(np.float64).reshape(batch, -1, 32) ** 2).sum(-1)
+                             .astype(np.float32)).to(dev)
+    ss_out = torch.empty((batch, n // 32), dtype=torch.float32, device=dev)
+    keys = torch.zeros((batch, n // 32), dtype=torch.int64, device=dev)
+    ops.set_gemv_ksplit(parts)
+    try:
+        ys = []
+        for sin in (None, ss_in):
+            ys.append(ops.gemv_ex(w, "q4", hd, n // 32, k // 256, norm_w=nwd, eps=1e-5,
+                                  residual=torch.from_numpy(res).to(dev), ssq_in=sin,
+                                  ssq_out=ss_out, argmax_keys=keys).cpu().numpy())
+    finally:
+        ops.set_gemv_ksplit(0)
+    hf = h.astype(np.float64)
+    xn = qo.bf16_round((hf / np.sqrt((hf ** 2).mean(1, keepdims=True) + 1e-5)
+                        * qo.bf16_to_f32(nw)).astype(np.float32))
+    ref = qo.gemv(raw, "q4", xn, n // 32, k // 256, acc=np.float64).reshape(batch, n) + res
+    for y in ys:
+        for b in range(batch):
+            rel, cos = qo.metrics(y[b], ref[b])
+            assert rel < 1e-4 and cos > 0.999999, (b, rel, cos)   # xn may flip a bf16 ulp
+    y = ys[-1]
+    sref = (y.astype(np.float64).reshape(batch, -1, 32) ** 2).sum(-1)
+    assert np.abs(ss_out.cpu().numpy() - sref).max() <= 1e-6 * sref.max()
+    tok = torch.zeros(batch, dtype=torch.int32, device=dev)
+    pos = torch.zeros(batch, dtype=torch.int32, device=dev)
+    lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+    step = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.decode_advance(keys, n // 32, tok, pos, lens, step)
+    assert tok.cpu().numpy().tolist() == np.argmax(y, axis=1).tolist()
+
+
 def test_gemv_residual_and_ones(dev):
     n, k = 2560, 2560
     raw, rng = _tiles("q4", n, k, 7)

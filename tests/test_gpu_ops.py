@@ -192,6 +192,36 @@ def test_qkv_rope(dev, batch, norm, ksplit):
         assert not kcn[b][:, mask].any() and not vcn[b][:, mask].any()   # nothing else written
 
 
+@pytest.mark.parametrize("batch,ksplit", [(1, 0), (3, 0), (2, 1)], indirect=["ksplit"])
+def test_qkv_rope_ssq_in(dev, batch, ksplit):
+    """The norm fed the producer's per-32 sums of squares gives the same normalised input
+    (to bf16 rounding) and GEMV outputs as the oracle on that input."""
+    rng = np.random.default_rng(23)
+    hq, hkv, hid, lmax = 40, 8, 2560, 128
+    kt = hid // 256
+    wq = synth.q4_tiles(rng, hq * 64, hid).reshape(-1, 5120)
+    wk = synth.q4_tiles(rng, hkv * 64, hid).reshape(-1, 5120)
+    wv = synth.q4_tiles(rng, hkv * 64, hid).reshape(-1, 5120)
+    pos = rng.integers(0, lmax, batch).astype(np.int32)
+    tab = ops.rope_table(lmax, 64, 10000.0)
+    kc = torch.zeros((batch, hkv, lmax, 64), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    raw = torch.empty((batch, (hq + 2 * hkv) * 64), dtype=torch.float32, device=dev)
+    xn = torch.empty((batch, hid), dtype=torch.bfloat16, device=dev)
+    nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+    h = (rng.standard_normal((batch, hid)) * 20).astype(np.float32)
+    ss = torch.from_numpy(ssq32(h).astype(np.float32)).to(dev)
+    d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
+    ops.qkv_rope(d(wq), d(wk), d(wv), hq, hkv, kt, torch.from_numpy(h).to(dev),
+                 torch.from_numpy(pos).to(dev), tab, kc, vc, norm_w=bf16_dev(nw, dev),
+                 raw_out=raw, xn_out=xn, ssq_in=ss)
+    assert_bf16_close(bits(xn), do.rmsnorm(h, nw, 1e-5), max_frac=2e-3)
+    x_used = bits(xn)
+    ref = np.concatenate([qo.gemv(w_, "q4", x_used, n, kt, acc=np.float64).reshape(batch, -1)
+                          for w_, n in ((wq, hq * 2), (wk, hkv * 2), (wv, hkv * 2))], axis=1)
+    assert_close(raw.cpu().numpy(), ref)
+
+
 # ------------------------------------------------------------------ fused [gate,up,SwiGLU]
 
 @pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (2, True, 0), (1, True, 2),
@@ -300,14 +330,22 @@ def test_gqa_decode_splits(dev, n_split):
 
 # ------------------------------------------------------------------ helpers
 
+def ssq32(y):
+    """float64 sums of squares over consecutive 32 entries of each row."""
+    y = np.asarray(y, np.float64)
+    return (y.reshape(y.shape[0], -1, 32) ** 2).sum(-1)
+
+
 def test_embed_and_argmax(dev):
     rng = np.random.default_rng(18)
     vocab, hid = 1024, 512
     w = synth.q8_tiles(rng, vocab, hid).reshape(-1, 8704)
     toks = np.array([0, 31, 32, 1023], np.int32)
+    ss = torch.empty((4, hid // 32), dtype=torch.float32, device=dev)
     h = ops.embed_q8(torch.from_numpy(w.reshape(-1)).to(dev), torch.from_numpy(toks).to(dev),
-                     vocab, hid).cpu().numpy()
+                     vocab, hid, ssq_out=ss).cpu().numpy()
     assert np.array_equal(h, do.embed_rows(w, toks, vocab, hid))
+    assert_close(ss.cpu().numpy(), ssq32(h), rel=1e-6)
     logits = rng.standard_normal((3, 100352)).astype(np.float32)
     logits[1, 5000] = logits[1, 7000] = 99.0         # first maximum wins
     idx = ops.argmax(torch.from_numpy(logits).to(dev)).cpu().numpy()
