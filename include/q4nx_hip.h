@@ -36,6 +36,7 @@ extern "C" {
 #define Q4NX_ERR_ARG (-1)     /* null or misaligned pointer, bad enum            */
 #define Q4NX_ERR_SHAPE (-2)   /* K % 256, N % 32, Hq % Hkv, head_dim, batch ...  */
 #define Q4NX_ERR_WS (-3)      /* workspace missing or too small                  */
+#define Q4NX_ERR_TIMEOUT (-5) /* a multi-stage launch gave up waiting            */
 #define Q4NX_ERR_LAUNCH (-4)  /* the HIP runtime refused the launch              */
 
 #define Q4NX_KIND_Q4 4
@@ -160,6 +161,25 @@ int q4nx_gate_up_swiglu(const uint8_t *wg, const uint8_t *wu, int n_tile_rows,
                         uint16_t *h_out,
                         int64_t h_stride, float *raw_out, uint16_t *xn_out, void *ws,
                         size_t ws_bytes, void *stream);
+
+/* Everything between attention and the next layer in one launch (three stages): o-proj
+ * h += Wo attn (and per-32 sums of squares of h into ssq), then RMSNorm(h; norm_w) with
+ * [gate, up, SwiGLU] into mlp (bf16 [batch][inter]), then down h += Wd mlp (ssq again).
+ * Each stage streams its weights while the previous one runs and reads its inputs once
+ * that stage is complete. Same arithmetic as q4nx_gemv_ex + q4nx_gate_up_swiglu +
+ * q4nx_gemv_ex. attn: bf16 [batch][q_dim]; h: fp32 [batch][hidden], updated in place;
+ * ssq: fp32 [batch][hidden/32]. Replaces the o-proj and MLP designs of one reference
+ * layer (designs/granite_gemv/granite_layer.py:11-14, granite_mlp.py:48-133); no
+ * single reference kernel does all three. */
+size_t q4nx_layer_tail_ws_bytes(int hidden, int q_dim, int inter, int batch);
+int q4nx_layer_tail(const uint8_t *wo, const uint8_t *wg, const uint8_t *wu,
+                    const uint8_t *wd, int hidden, int q_dim, int inter,
+                    const uint16_t *attn, float *h, float *ssq, const uint16_t *norm_w,
+                    float eps, uint16_t *mlp, int batch, void *ws, size_t ws_bytes,
+                    void *stream);
+/* Synchronises the stream and returns Q4NX_ERR_TIMEOUT (clearing the flag) if a
+ * multi-stage launch on this workspace gave up waiting since the last check. */
+int q4nx_ws_check(void *ws, void *stream);
 
 /* ---------------------------------------------------------------- attention
  * GQA flash-decode: one query token per sequence, out[b][h] = softmax(scale * K q) V

@@ -42,6 +42,10 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_gate_up_ws_bytes": (c_sz, [c_i, c_i, c_i]),
     "q4nx_gate_up_swiglu": (c_i, [c_p, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p,
                                   c_i64, c_p, c_p, c_p, c_sz, c_p]),
+    "q4nx_layer_tail_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
+    "q4nx_layer_tail": (c_i, [c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_p, c_p, c_f, c_p, c_i,
+                              c_p, c_sz, c_p]),
+    "q4nx_ws_check": (c_i, [c_p, c_p]),
     "q4nx_gqa_decode_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
     "q4nx_gqa_decode": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
                               c_i64, c_f, c_i, c_p, c_sz, c_p]),

@@ -25,14 +25,16 @@
 // Arithmetic (exact inputs, fp32 accumulate)
 //   x is converted to fp16 with one power-of-two scale per wave, chosen from max|x| over
 //   the wave's K range (bf16 values convert exactly in fp16's normal range). A 4-bit code
-//   c placed in the low bits of an fp16 is the subnormal c * 2^-24, exactly, and
-//   v_dot2_f32_f16 multiplies two of them by two x values with exact products. For a
-//   byte b = lo | hi<<4 holding two rows at one k, a v_perm_b32 builds
-//   [b(k0), 0, b(k1), 0] = (lo + 16 hi) * 2^-24 for two k, and the same dword masked with
-//   0x000F000F gives lo alone: two dot2 per 4 weights recover both rows' sums
-//   (hi = (full - lo) / 16). q8 codes are biased by 128 (xor 0x80) into 1..255 and the
-//   bias is removed with 128 * sum(x). The Q4_1 minimum factors out of the K sum
-//   (granite_gemv.h:19-29): y_r += d_r * sum(c x) + m_r * sum(x) per 32-K group.
+//   c placed in bits 4-7 of an fp16 is the subnormal c * 2^-20, exactly, and
+//   v_dot2_f32_f16 multiplies two of them by two x values with exact products. The low
+//   nibbles of a weight dword are shifted up and the high ones masked in place (two ops
+//   per dword, shared by its four bytes), then a v_perm_b32 builds [c(k0), 0, c(k1), 0]
+//   for one row and two k: one permute and one dot2 per 2 weights. (v_dot2's adder keeps
+//   fewer bits when a subnormal operand has leading zeros; codes in bits 0-3 cost about
+//   six bits against the largest term on heavy-tailed activations, bits 4-7 two at most.)
+//   q8 codes are biased by 128 (xor 0x80) into 1..255 and the bias is removed with
+//   128 * sum(x). The Q4_1 minimum factors out of the K sum (granite_gemv.h:19-29):
+//   y_r += d_r * sum(c x) + m_r * sum(x) per 32-K group.
 
 #include "common.h"
 
@@ -80,7 +82,54 @@ struct GemvArgs {
   float* part;
   uint32_t part_bytes;
   unsigned* counters;
+  // stage of a multi-stage launch: activations come from an earlier stage of the same
+  // launch (read and written system-coherent), after wait_cnt reaches wait_target
+  int sys_io;
+  const unsigned* wait_cnt;
+  unsigned wait_target;
+  unsigned* err;
 };
+
+// Output stores: plain, or system-coherent when a later stage of the same launch reads them.
+template <typename T>
+__device__ __forceinline__ void put(T* p, T v, int sys) {
+  if (sys) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  else *p = v;
+}
+__device__ __forceinline__ void put4(uint4* p, uint4 v, int sys) {
+  if (sys) {
+    uint32_t* q = (uint32_t*)p;
+    __hip_atomic_store(q, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(q + 1, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(q + 2, v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(q + 3, v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  } else {
+    *p = v;
+  }
+}
+
+constexpr int kCounterReplicas = 8;   // one per XCD (workgroup i runs on XCD i mod 8)
+
+// Waits (one thread, bounded) until an earlier stage has completed `target` items; the
+// rest of the workgroup waits at the barrier. On timeout the error flag is raised and the
+// workgroup goes on (its results are then invalid), so every wave always finishes.
+__device__ __forceinline__ void stage_wait(const unsigned* cnt, unsigned target, unsigned* err) {
+  if (threadIdx.x == 0) {
+    // each XCD's workgroups poll their own replica of the counter (the producers add to
+    // all of them), so no single memory channel serves every poll
+    const unsigned* c = cnt + (blockIdx.x & (kCounterReplicas - 1));
+    unsigned spins = 0;
+    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) < target) {
+      if (++spins > (1u << 22) ||
+          __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != 0u) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+  }
+  __syncthreads();
+}
 
 // 64-bit key whose unsigned order is numpy's argmax order: larger value first, NaN above
 // everything, and on ties the smaller index (stored inverted in the low word).
@@ -118,8 +167,10 @@ __device__ __forceinline__ void transpose_reduce4(const float (&v)[16], float (&
   }
 }
 
+// One work item (an output group, or one K part of it) of a GEMV launch. Returns true when
+// this workgroup ran the epilogue (for a split group, only the last part to arrive does).
 template <int KIND, int B, int TPW>
-__global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
+__device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   constexpr int TB = KIND == 4 ? kQ4TileBytes : kQ8TileBytes;
   constexpr int NCH = KIND == 4 ? 4 : 8;              // 16-byte chunks per lane per tile
   constexpr int CODE_OFF = KIND == 4 ? 1024 : 512;    // start of the codes in a tile
@@ -137,7 +188,7 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   const int WM = W / a.G;             // waves per member tile-row
   const int member = wave / WM, chunk = wave % WM;
   const int ks = a.ksplit;
-  const int group = blockIdx.x / ks, kpart = blockIdx.x - group * ks;
+  const int group = blk / ks, kpart = blk - group * ks;
   const int kt_lo = kpart * a.k_t / ks, kt_hi = (kpart + 1) * a.k_t / ks;
 
   int seg, tr;
@@ -172,52 +223,75 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
 
   // ---- 1. activations. Every load is unconditional, from a valid address (clamped row,
   //         or the weights as a stand-in), so nothing waits before the weight stream is
-  //         issued; rows past the batch are masked where the values are used.
+  //         issued; rows past the batch are masked where the values are used. A stage of a
+  //         multi-stage launch loads them after its weights, once the producer is done, and
+  //         system-coherent (the producer may have run on another XCD).
   uint4 ar[B][TPW][2];    // raw activation bytes: 8 bf16 x (first 16 B) or 8 fp32 h (32 B)
   uint4 nw[TPW];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int kt = min(kt0 + t, kt_hi - 1);
-    const int k = kt * kTileK + kx;
-    nw[t] = *(const uint4*)(norm ? (const void*)(a.norm_w + k) : (const void*)a.w[0]);
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int bb = min(b, a.batch - 1);
-      const uint4* src = norm ? (const uint4*)(a.hres + bb * a.x_stride + k)
-                              : (const uint4*)(a.x + bb * a.x_stride + k);
-      ar[b][t][0] = src[0];
-      ar[b][t][1] = src[norm ? 1 : 0];
-    }
-  }
-
-  // RMSNorm sum of squares handed over by the producer of x: K/32 partials per row, every
-  // wave sums them itself (same order everywhere) and needs no other wave
   const bool pre_ssq = norm && a.ssq_in != nullptr;
   const int n_ss = K / 32;
   float sq[B][4];
-  if (pre_ssq) {
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        sq[b][j] = a.ssq_in[min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1)];
-  }
-
-  // with K split and no partials given, this workgroup's tiles see only part of the row:
-  // the sum of squares reads the whole row (strided over all threads; three float4 per
-  // thread cover K <= 12 * blockDim, a remainder loop the rest)
   constexpr int kSsqIt = 3;
   float4 hs[B][kSsqIt];
   const bool split_norm = norm && ks > 1 && !pre_ssq;
-  if (split_norm) {
+  const int sys = a.sys_io;
+  auto load_acts = [&]() {
+    const void* xbase = norm ? (const void*)a.hres : (const void*)a.x;
+    const uint32_t xbytes = (uint32_t)((size_t)a.batch * a.x_stride * (norm ? 4 : 2));
+    const __amdgpu_buffer_rsrc_t xr_ = make_rsrc(xbase, xbytes);
 #pragma unroll
-    for (int it = 0; it < kSsqIt; ++it) {
-      const int i = min(tid + it * (int)blockDim.x, K / 4 - 1);
+    for (int t = 0; t < TPW; ++t) {
+      const int kt = min(kt0 + t, kt_hi - 1);
+      const int k = kt * kTileK + kx;
+      nw[t] = *(const uint4*)(norm ? (const void*)(a.norm_w + k) : (const void*)a.w[0]);
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int bb = min(b, a.batch - 1);
+        const uint32_t off = (uint32_t)(((size_t)bb * a.x_stride + k) * (norm ? 4 : 2));
+        if (sys) {
+          ar[b][t][0] = ld16_sys(xr_, off);
+          ar[b][t][1] = ld16_sys(xr_, norm ? off + 16 : off);
+        } else {
+          const uint4* src = (const uint4*)((const uint8_t*)xbase + off);
+          ar[b][t][0] = src[0];
+          ar[b][t][1] = src[norm ? 1 : 0];
+        }
+      }
+    }
+    // RMSNorm sum of squares handed over by the producer of x: K/32 partials per row,
+    // every wave sums them itself (same order everywhere) and needs no other wave
+    if (pre_ssq) {
 #pragma unroll
       for (int b = 0; b < B; ++b)
-        hs[b][it] = *(const float4*)(a.hres + min(b, a.batch - 1) * a.x_stride + 4 * i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float* src = a.ssq_in + min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1);
+          sq[b][j] = sys ? load_sys(src) : *src;
+        }
     }
-  }
+    // with K split and no partials given, this workgroup's tiles see only part of the row:
+    // the sum of squares reads the whole row (strided over all threads; three float4 per
+    // thread cover K <= 12 * blockDim, a remainder loop the rest)
+    if (split_norm) {
+#pragma unroll
+      for (int it = 0; it < kSsqIt; ++it) {
+        const int i = min(tid + it * (int)blockDim.x, K / 4 - 1);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+          const uint32_t off = (uint32_t)(((size_t)min(b, a.batch - 1) * a.x_stride + 4 * i) * 4);
+          if (sys) {
+            const uint4 u = ld16_sys(xr_, off);
+            hs[b][it] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y),
+                                    __uint_as_float(u.z), __uint_as_float(u.w));
+          } else {
+            hs[b][it] = *(const float4*)((const uint8_t*)a.hres + off);
+          }
+        }
+      }
+    }
+  };
+  const bool staged = a.wait_cnt != nullptr;
+  if (!staged) load_acts();
 
   // ---- 2. weights and per-group metadata of every tile of this wave
   uint4 wq[TPW][NCH];
@@ -236,6 +310,11 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
       mm[t] = make_uint2(0, 0);
       if (KIND == 4) mm[t] = *(const uint2*)(tile + kMetaBytes + 2 * g);
     }
+  }
+
+  if (staged) {
+    stage_wait(a.wait_cnt, a.wait_target, a.err);
+    load_acts();
   }
 
   // the activations are used from here on (their waits come after the weight stream)
@@ -293,7 +372,10 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
       }
       if (b < a.batch)
         for (int i = tid + kSsqIt * (int)blockDim.x; i < K / 4; i += blockDim.x) {
-          const float4 h = *(const float4*)(a.hres + b * a.x_stride + 4 * i);
+          const float* hp = a.hres + b * a.x_stride + 4 * i;
+          const float4 h = sys ? make_float4(load_sys(hp), load_sys(hp + 1), load_sys(hp + 2),
+                                             load_sys(hp + 3))
+                               : *(const float4*)hp;
           ssq[b] = fmaf(h.x, h.x, fmaf(h.y, h.y, fmaf(h.z, h.z, fmaf(h.w, h.w, ssq[b]))));
         }
     }
@@ -347,7 +429,7 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         xr[b][t] = b < a.batch ? make_uint4(o[0], o[1], o[2], o[3]) : make_uint4(0, 0, 0, 0);
         if (a.xn_out != nullptr && group == 0 && member == 0 && rb == 0 && t < ntw &&
             b < a.batch)
-          *(uint4*)(a.xn_out + b * a.x_stride + (kt0 + t) * kTileK + kx) = xr[b][t];
+          put4((uint4*)(a.xn_out + b * a.x_stride + (kt0 + t) * kTileK + kx), xr[b][t], sys);
       }
     }
   }
@@ -400,37 +482,55 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   for (int t = 0; t < TPW; ++t) {
     if (t >= ntw) continue;
     if (KIND == 4) {
+      // Both nibbles of a byte are moved to its top half (bits 4-7) before the byte
+      // permutes, so each code enters v_dot2 as the fp16 subnormal c * 2^-20. The dot2
+      // adder keeps fewer bits the more leading zeros a subnormal operand has (measured on
+      // gfx950: codes in bits 0-3 lose about 6 bits against the largest term), so the codes
+      // sit as high in the mantissa as the byte permutes allow.
+      float pv[B][16], X[B];   // pv[b][r]: row r of the lane's 16, over its 8 K
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        // pv[2i] = lo of row pair i (even row), pv[2i+1] = lo + 16*hi (both rows)
-        float pv[16], X = 0.f;
+        X[b] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) pv[i] = 0.f;
+        for (int i = 0; i < 16; ++i) pv[b][i] = 0.f;
+      }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint4 w = wq[t][c];
-          const uint32_t xpc = xp[b][t][c];
+      for (int c = 0; c < 4; ++c) {
+        const uint4 w = wq[t][c];
+        const uint32_t Lx = (w.x << 4) & 0xF0F0F0F0u, Ly = (w.y << 4) & 0xF0F0F0F0u;
+        const uint32_t Lz = (w.z << 4) & 0xF0F0F0F0u, Lw = (w.w << 4) & 0xF0F0F0F0u;
+        const uint32_t Hx = w.x & 0xF0F0F0F0u, Hy = w.y & 0xF0F0F0F0u;
+        const uint32_t Hz = w.z & 0xF0F0F0F0u, Hw = w.w & 0xF0F0F0F0u;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t T0 = perm(w.z, w.x, sel_byte(i));   // row pair i   (rows 0..7)
-            const uint32_t T1 = perm(w.w, w.y, sel_byte(i));   // row pair 4+i (rows 8..15)
-            pv[2 * i + 1] = dot2(T0, xpc, pv[2 * i + 1]);
-            pv[2 * i] = dot2(T0 & 0x000F000Fu, xpc, pv[2 * i]);
-            pv[2 * (4 + i) + 1] = dot2(T1, xpc, pv[2 * (4 + i) + 1]);
-            pv[2 * (4 + i)] = dot2(T1 & 0x000F000Fu, xpc, pv[2 * (4 + i)]);
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t o0 = perm(Lz, Lx, sel_byte(i));        // row 2i     (low nibbles)
+          const uint32_t o1 = perm(Hz, Hx, sel_byte(i));        // row 2i + 1 (high nibbles)
+          const uint32_t o2 = perm(Lw, Ly, sel_byte(i));        // rows 8..15
+          const uint32_t o3 = perm(Hw, Hy, sel_byte(i));
+#pragma unroll
+          for (int b = 0; b < B; ++b) {
+            const uint32_t xpc = xp[b][t][c];
+            pv[b][2 * i] = dot2(o0, xpc, pv[b][2 * i]);
+            pv[b][2 * i + 1] = dot2(o1, xpc, pv[b][2 * i + 1]);
+            pv[b][8 + 2 * i] = dot2(o2, xpc, pv[b][8 + 2 * i]);
+            pv[b][8 + 2 * i + 1] = dot2(o3, xpc, pv[b][8 + 2 * i + 1]);
           }
-          X = dot2(xpc, kOne2, X);
         }
-        float r4[4];   // lo(2q), full(2q), lo(2q+1), full(2q+1): rows 4q .. 4q+3
-        transpose_reduce4(pv, r4, lane);
-        X += dpp<kDppXor1>(X);
-        X += dpp<kDppXor2>(X);
-        const float se0 = r4[0] * 16777216.0f, so0 = (r4[1] - r4[0]) * 1048576.0f;
-        const float se1 = r4[2] * 16777216.0f, so1 = (r4[3] - r4[2]) * 1048576.0f;
-        acc[b][0] += fmaf(bf16lo(md[t].x), se0, bf16lo(mm[t].x) * X);
-        acc[b][1] += fmaf(bf16hi(md[t].x), so0, bf16hi(mm[t].x) * X);
-        acc[b][2] += fmaf(bf16lo(md[t].y), se1, bf16lo(mm[t].y) * X);
-        acc[b][3] += fmaf(bf16hi(md[t].y), so1, bf16hi(mm[t].y) * X);
+#pragma unroll
+        for (int b = 0; b < B; ++b) X[b] = dot2(xp[b][t][c], kOne2, X[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        float r4[4];   // rows 4q .. 4q+3, summed over the 32 K of the group
+        transpose_reduce4(pv[b], r4, lane);
+        float Xs = X[b];
+        Xs += dpp<kDppXor1>(Xs);
+        Xs += dpp<kDppXor2>(Xs);
+        constexpr float kC = 1048576.0f;   // undo the 2^-20 of the codes
+        acc[b][0] += fmaf(bf16lo(md[t].x), r4[0] * kC, bf16lo(mm[t].x) * Xs);
+        acc[b][1] += fmaf(bf16hi(md[t].x), r4[1] * kC, bf16hi(mm[t].x) * Xs);
+        acc[b][2] += fmaf(bf16lo(md[t].y), r4[2] * kC, bf16lo(mm[t].y) * Xs);
+        acc[b][3] += fmaf(bf16hi(md[t].y), r4[3] * kC, bf16hi(mm[t].y) * Xs);
       }
     } else {
 #pragma unroll
@@ -507,7 +607,7 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
     __syncthreads();
     if (tid == 0) s_last = atomicAdd(&a.counters[group], 1u) == (unsigned)(ks - 1) ? 1 : 0;
     __syncthreads();
-    if (!s_last) return;
+    if (!s_last) return false;
     const uint32_t rec0 = (uint32_t)(group * ks * nrec) * 4u;
     for (int e = tid; e < nrec / 4; e += blockDim.x) {
       uint4 v[8];
@@ -547,12 +647,12 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         const int64_t n = (int64_t)tr * 32 + r;
         v = sgrp[b][r];
         if (a.residual != nullptr) v += a.residual[b * a.y_stride + n];
-        if (a.y != nullptr) a.y[b * a.y_stride + n] = v;
+        if (a.y != nullptr) put(a.y + b * a.y_stride + n, v, sys);
         if (a.argmax_keys != nullptr) atomicMax(&skey[b], argmax_key(v, (uint32_t)n));
       }
       if (a.ssq_out != nullptr) {   // sum of squares of the tile-row's 32 outputs
         const float sq32 = group32_sum(v * v);
-        if (live && r == 0) a.ssq_out[(int64_t)b * a.n_tr[0] + tr] = sq32;
+        if (live && r == 0) put(a.ssq_out + (int64_t)b * a.n_tr[0] + tr, sq32, sys);
       }
     }
     if (a.argmax_keys != nullptr) {   // one slot per (batch row, tile-row): no contention
@@ -568,11 +668,11 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         const float g = bf16_to_f32(f32_to_bf16(gr));
         const float uu = bf16_to_f32(f32_to_bf16(ur));
         const float h = (g / (1.0f + expf(-g))) * uu;
-        a.h_out[b * a.h_stride + n] = f32_to_bf16(h);
+        put(a.h_out + b * a.h_stride + n, f32_to_bf16(h), sys);
         if (a.raw_out != nullptr) {
           const int64_t N = (int64_t)a.n_tr[0] * 32;
-          a.raw_out[b * 2 * N + n] = gr;
-          a.raw_out[b * 2 * N + N + n] = ur;
+          put(a.raw_out + b * 2 * N + n, gr, sys);
+          put(a.raw_out + b * 2 * N + N + n, ur, sys);
         }
       }
     }
@@ -591,8 +691,8 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         const float r0 = sgrp[b][d], r1 = sgrp[b][32 + d];
         if (a.raw_out != nullptr) {
           const int64_t Wd = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
-          a.raw_out[b * Wd + seg_off + hg * 64 + d] = r0;
-          a.raw_out[b * Wd + seg_off + hg * 64 + 32 + d] = r1;
+          put(a.raw_out + b * Wd + seg_off + hg * 64 + d, r0, sys);
+          put(a.raw_out + b * Wd + seg_off + hg * 64 + 32 + d, r1, sys);
         }
         const float x0 = bf16_to_f32(f32_to_bf16(r0));
         const float x1 = bf16_to_f32(f32_to_bf16(r1));
@@ -601,8 +701,8 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
         if (seg == 2) {
           if (pos_ok) {
             uint16_t* dst = a.v_cache + b * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
-            dst[d] = f32_to_bf16(x0);
-            dst[32 + d] = f32_to_bf16(x1);
+            put(dst + d, f32_to_bf16(x0), sys);
+            put(dst + 32 + d, f32_to_bf16(x1), sys);
           }
         } else if (pos_ok) {
           const float c = a.rope_tab[(int64_t)p * 64 + d];
@@ -612,12 +712,51 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
           uint16_t* dst = (seg == 0)
                               ? a.q_out + b * (int64_t)a.n_q_heads * 64 + hg * 64
                               : a.k_cache + b * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
-          dst[d] = f32_to_bf16(y0);
-          dst[32 + d] = f32_to_bf16(y1);
+          put(dst + d, f32_to_bf16(y0), sys);
+          put(dst + 32 + d, f32_to_bf16(y1), sys);
         }
       }
     }
   }
+  return true;
+}
+
+template <int KIND, int B, int TPW>
+__global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
+  (void)gemv_body<KIND, B, TPW>(a, blockIdx.x);
+}
+
+// A chain of GEMV stages in one launch: stage s owns workgroups [wg_begin[s], wg_begin[s+1])
+// and (after the first) waits until every item of stage s-1 is done before reading its
+// activations; its weights are already streaming by then. Workgroups are dispatched in
+// index order, so a waiting workgroup's producers were all dispatched before it and none
+// of them waits on a later stage: the chain always drains. The last item of the last
+// stage clears the stage counters for the next launch.
+constexpr int kMaxStages = 4;
+struct MultiGemvArgs {
+  GemvArgs st[kMaxStages];
+  int wg_begin[kMaxStages + 1];
+  int n_stages;
+  unsigned* done;      // one completion counter per stage
+  unsigned items[kMaxStages];
+};
+
+template <int KIND, int B, int TPW>
+__global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_multi_kernel(MultiGemvArgs m) {
+  __shared__ int s_final;
+  int s = 0;
+  while (s + 1 < m.n_stages && (int)blockIdx.x >= m.wg_begin[s + 1]) ++s;
+  const bool done_item = gemv_body<KIND, B, TPW>(m.st[s], blockIdx.x - m.wg_begin[s]);
+  if (!done_item) return;   // a split part that was not last: the last part signals
+  wait_vm();                // every output store of this item is acknowledged
+  __syncthreads();
+  if (threadIdx.x < (unsigned)kCounterReplicas) {
+    const unsigned prev = atomicAdd(&m.done[s * kCounterReplicas + threadIdx.x], 1u);
+    if (threadIdx.x == 0) s_final = (s == m.n_stages - 1 && prev == m.items[s] - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (s_final && threadIdx.x < (unsigned)(m.n_stages * kCounterReplicas))
+    __hip_atomic_store(&m.done[threadIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // ------------------------------------------------------------------ host side
@@ -715,6 +854,113 @@ static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char
     }
   }
   return check_launch(what);
+}
+
+// Counter region layout for multi-stage launches (inside the workspace's counter region):
+// split-K arrival counters of each stage from index 0, the stage completion counters and
+// the timeout flag at the end.
+constexpr int kStageDoneIdx = Q4NX_WS_COUNTER_BYTES / 4 - 32;   // kMaxStages x 8 replicas
+constexpr int kStageErrIdx = Q4NX_WS_COUNTER_BYTES / 4 - 33;
+// Waves per workgroup of a multi-stage launch (one K-tile per wave in every stage): 10
+// (640 threads) up to batch 2; the kernel's launch bound is 512 threads above that.
+static int multi_waves(int batch) { return round_batch(batch) <= 2 ? 10 : 8; }
+
+static int multi_ksplit(const GemvArgs& a, int n_groups) {
+  const int per_wg = multi_waves(a.batch) / a.G;   // K-tiles one workgroup covers per member
+  int ks = plan_ksplit(n_groups, a.G, a.k_t);
+  const int need = (a.k_t + per_wg - 1) / per_wg;
+  return ks > need ? ks : need;
+}
+
+static size_t multi_ws_bytes(const GemvArgs* st, const int* n_groups, int n) {
+  size_t part = 0;
+  int cnt = 0;
+  for (int i = 0; i < n; ++i) {
+    const int ks = multi_ksplit(st[i], n_groups[i]);
+    if (ks > 1) {
+      part += (size_t)n_groups[i] * ks * st[i].batch * st[i].G * 32 * 4;
+      cnt += n_groups[i];
+    }
+  }
+  if (cnt > kStageErrIdx) return 0;
+  return (size_t)Q4NX_WS_COUNTER_BYTES + part;
+}
+
+// Launches stages st[0..n) as one kernel (see gemv_multi_kernel). Every stage runs with
+// multi_waves(batch) waves and one K-tile per wave; K is split as far as that needs.
+static int launch_multi(int kind, GemvArgs* st, const int* n_groups, int n, void* ws,
+                        size_t ws_bytes, hipStream_t s, const char* what) {
+  Q4NX_REQUIRE(n >= 1 && n <= kMaxStages, Q4NX_ERR_ARG, "%s: %d stages", what, n);
+  const size_t need = multi_ws_bytes(st, n_groups, n);
+  Q4NX_REQUIRE(need > 0 && ws != nullptr && ws_bytes >= need && Q4NX_ALIGNED(ws, 256),
+               Q4NX_ERR_WS, "%s: workspace of %zu bytes (256-aligned) needed, %zu given", what,
+               need, ws_bytes);
+  MultiGemvArgs m{};
+  unsigned* counters = (unsigned*)ws;
+  uint8_t* part = (uint8_t*)ws + Q4NX_WS_COUNTER_BYTES;
+  int cnt = 0, blocks = 0, batch = st[0].batch;
+  for (int i = 0; i < n; ++i) {
+    GemvArgs& a = st[i];
+    Q4NX_REQUIRE(a.batch == batch, Q4NX_ERR_ARG, "%s: stages differ in batch", what);
+    const int ks = multi_ksplit(a, n_groups[i]);
+    Q4NX_REQUIRE(ks <= 8 && ks <= a.k_t, Q4NX_ERR_SHAPE, "%s: stage %d: K=%d too long", what, i,
+                 a.k_t * 256);
+    a.ksplit = ks;
+    if (ks > 1) {
+      const size_t pb = (size_t)n_groups[i] * ks * a.batch * a.G * 32 * 4;
+      a.counters = counters + cnt;
+      a.part = (float*)part;
+      a.part_bytes = (uint32_t)pb;
+      cnt += n_groups[i];
+      part += pb;
+    }
+    a.sys_io = 1;
+    a.err = counters + kStageErrIdx;
+    if (i > 0) {
+      a.wait_cnt = counters + kStageDoneIdx + (i - 1) * kCounterReplicas;
+      a.wait_target = (unsigned)n_groups[i - 1];
+    }
+    m.st[i] = a;
+    m.wg_begin[i] = blocks;
+    m.items[i] = (unsigned)n_groups[i];
+    blocks += n_groups[i] * ks;
+  }
+  m.wg_begin[n] = blocks;
+  m.n_stages = n;
+  m.done = counters + kStageDoneIdx;
+  const dim3 grid(blocks), block(multi_waves(batch) * 64);
+  const int B = round_batch(batch);
+  if (kind == 4) {
+    switch (B) {
+      case 1: hipLaunchKernelGGL((gemv_multi_kernel<4, 1, 1>), grid, block, 0, s, m); break;
+      case 2: hipLaunchKernelGGL((gemv_multi_kernel<4, 2, 1>), grid, block, 0, s, m); break;
+      case 4: hipLaunchKernelGGL((gemv_multi_kernel<4, 4, 1>), grid, block, 0, s, m); break;
+      default: hipLaunchKernelGGL((gemv_multi_kernel<4, 8, 1>), grid, block, 0, s, m); break;
+    }
+  } else {
+    return Q4NX_ERR_ARG;
+  }
+  return check_launch(what);
+}
+
+// The three GEMV stages after attention: o-proj (+ residual, sums of squares), the
+// RMSNorm + [gate, up, SwiGLU] group, and down (+ residual, sums of squares).
+static void tail_stages(GemvArgs* st, int* ng, const uint8_t* wo, const uint8_t* wg,
+                        const uint8_t* wu, const uint8_t* wd, int hidden, int q_dim, int inter,
+                        const uint16_t* attn, float* h, float* ssq, const uint16_t* norm_w,
+                        float eps, uint16_t* mlp, int batch) {
+  GemvArgs o{}, gu{}, dn{};
+  o.w[0] = wo; o.n_tr[0] = hidden / 32; o.op = OP_PLAIN; o.G = 1; o.k_t = q_dim / 256;
+  o.batch = batch; o.x = attn; o.x_stride = q_dim; o.y = h; o.y_stride = hidden;
+  o.residual = h; o.ssq_out = ssq;
+  gu.w[0] = wg; gu.w[1] = wu; gu.n_tr[0] = gu.n_tr[1] = inter / 32; gu.op = OP_GATEUP;
+  gu.G = 2; gu.k_t = hidden / 256; gu.batch = batch; gu.hres = h; gu.x_stride = hidden;
+  gu.norm_w = norm_w; gu.eps = eps; gu.ssq_in = ssq; gu.h_out = mlp; gu.h_stride = inter;
+  dn.w[0] = wd; dn.n_tr[0] = hidden / 32; dn.op = OP_PLAIN; dn.G = 1; dn.k_t = inter / 256;
+  dn.batch = batch; dn.x = mlp; dn.x_stride = inter; dn.y = h; dn.y_stride = hidden;
+  dn.residual = h; dn.ssq_out = ssq;
+  st[0] = o; st[1] = gu; st[2] = dn;
+  ng[0] = hidden / 32; ng[1] = inter / 32; ng[2] = hidden / 32;
 }
 
 static int check_common(const void* w, int n_tile_rows, int k_tiles, int batch, const char* what) {
@@ -964,6 +1210,58 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
   a.h_stride = h_stride;
   a.raw_out = raw_out;
   return launch(4, a, n_tile_rows, (hipStream_t)stream, what, ws, ws_bytes);
+}
+
+size_t q4nx_layer_tail_ws_bytes(int hidden, int q_dim, int inter, int batch) {
+  if (hidden < 256 || q_dim < 256 || inter < 256 || batch < 1 || batch > Q4NX_MAX_BATCH) return 0;
+  GemvArgs st[3];
+  int ng[3];
+  tail_stages(st, ng, nullptr, nullptr, nullptr, nullptr, hidden, q_dim, inter, nullptr, nullptr,
+              nullptr, nullptr, 0.f, nullptr, batch);
+  return multi_ws_bytes(st, ng, 3);
+}
+
+int q4nx_layer_tail(const uint8_t* wo, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                    int hidden, int q_dim, int inter, const uint16_t* attn, float* h, float* ssq,
+                    const uint16_t* norm_w, float eps, uint16_t* mlp, int batch, void* ws,
+                    size_t ws_bytes, void* stream) {
+  const char* what = "q4nx_layer_tail";
+  Q4NX_REQUIRE(hidden % 256 == 0 && q_dim % 256 == 0 && inter % 256 == 0 && hidden > 0 &&
+                   q_dim > 0 && inter > 0 && hidden <= 8192,
+               Q4NX_ERR_SHAPE, "%s: hidden=%d q_dim=%d inter=%d must be multiples of 256 "
+               "(hidden <= 8192)", what, hidden, q_dim, inter);
+  int rc = check_common(wo, hidden / 32, q_dim / 256, batch, what);
+  if (rc) return rc;
+  for (const void* p : {(const void*)wg, (const void*)wu})
+    if ((rc = check_common(p, inter / 32, hidden / 256, batch, what))) return rc;
+  if ((rc = check_common(wd, hidden / 32, inter / 256, batch, what))) return rc;
+  Q4NX_REQUIRE(attn && h && ssq && norm_w && mlp && Q4NX_ALIGNED(attn, 16) &&
+                   Q4NX_ALIGNED(h, 16) && Q4NX_ALIGNED(mlp, 16) && Q4NX_ALIGNED(norm_w, 16) &&
+                   Q4NX_ALIGNED(ssq, 4),
+               Q4NX_ERR_ARG, "%s: attn, h, ssq, norm_w and mlp are required (16-byte aligned)",
+               what);
+  GemvArgs st[3];
+  int ng[3];
+  tail_stages(st, ng, wo, wg, wu, wd, hidden, q_dim, inter, attn, h, ssq, norm_w, eps, mlp, batch);
+  return launch_multi(4, st, ng, 3, ws, ws_bytes, (hipStream_t)stream, what);
+}
+
+int q4nx_ws_check(void* ws, void* stream) {
+  Q4NX_REQUIRE(ws != nullptr, Q4NX_ERR_ARG, "q4nx_ws_check: ws is required");
+  unsigned flag = 0;
+  unsigned* dev = (unsigned*)ws + kStageErrIdx;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipMemcpyAsync(&flag, dev, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess) {
+    set_error("q4nx_ws_check: reading the flag failed");
+    return Q4NX_ERR_LAUNCH;
+  }
+  if (flag == 0) return Q4NX_OK;
+  // a stage gave up: counters may be left mid-count, so the whole region starts over
+  (void)hipMemsetAsync(ws, 0, Q4NX_WS_COUNTER_BYTES, s);
+  (void)hipStreamSynchronize(s);
+  set_error("a multi-stage launch timed out waiting for an earlier stage (results invalid)");
+  return Q4NX_ERR_TIMEOUT;
 }
 
 }  // extern "C"

@@ -172,9 +172,13 @@ class GraniteDecoder:
     greedy loop on the device from a HIP graph of one step."""
 
     def __init__(self, weights: GraniteWeights, max_batch: int = 1, max_len: int = 4096,
-                 device="cuda"):
+                 device="cuda", fused_tail: bool = False):
         c = weights.cfg
         self.cfg, self.w = c, weights
+        # o-proj + MLP of a layer as one three-stage launch (q4nx_layer_tail) instead of three.
+        # Off by default: measured slower on MI355X (the stages' cross-XCD hand-offs cost
+        # more than the weight streams they overlap).
+        self.fused_tail = fused_tail
         self.dev = torch.device(device)
         self.max_batch = max_batch
         self.max_len = (max_len + 63) // 64 * 64
@@ -217,6 +221,11 @@ class GraniteDecoder:
                          ssq_in=ssq)
             ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
                            max_len=self.max_len, out=attn, ws=self.ws)
+            if self.fused_tail:   # o-proj, norm + gate/up + SwiGLU, down: one launch
+                ops.layer_tail(L["o"], L["gate"], L["up"], L["down"], c.hidden, c.q_dim, c.inter,
+                               attn.view(b, c.q_dim), h, ssq, L["norm_post"], c.eps, mlp,
+                               ws=self.ws)
+                continue
             ops.gemv_ex(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q, residual=h,
                         out=h, ssq_out=ssq, ws=self.ws)
             ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
@@ -240,6 +249,7 @@ class GraniteDecoder:
         self.pos[:b].copy_(positions)
         self.lens[:b].copy_(positions + 1)
         self._launch_step(b)
+        ops.ws_check(self.ws)
         return self.logits[:b]
 
     # ------------------------------------------------------------ graph + greedy loop
@@ -291,6 +301,7 @@ class GraniteDecoder:
                 logs.append(self.logits[:b].clone())
         torch.cuda.synchronize()
         self.seconds += time.perf_counter() - t0
+        ops.ws_check(self.ws)   # raises if a multi-stage launch gave up waiting
         self.calls += n_new
         return self.history[:n_new, :b].t().contiguous().cpu().numpy(), logs
 

@@ -299,6 +299,36 @@ def gate_up_swiglu(wg, wu, n_tile_rows: int, k_tiles: int, x: torch.Tensor,
     return h_out
 
 
+def layer_tail(wo, wg, wu, wd, hidden: int, q_dim: int, inter: int, attn: torch.Tensor,
+               h: torch.Tensor, ssq: torch.Tensor, norm_w: torch.Tensor, eps: float,
+               mlp: torch.Tensor, ws: Workspace | None = None) -> None:
+    """o-proj + RMSNorm/[gate,up,SwiGLU] + down in one launch (three dependent stages):
+    h += Wo attn; mlp = SwiGLU(RMSNorm(h)); h += Wd mlp; ssq = per-32 sums of h^2."""
+    _tiles(wo, "q4", hidden // 32, q_dim // 256, "wo")
+    _tiles(wg, "q4", inter // 32, hidden // 256, "wg")
+    _tiles(wu, "q4", inter // 32, hidden // 256, "wu")
+    _tiles(wd, "q4", hidden // 32, inter // 256, "wd")
+    _dev(attn, "attn", torch.bfloat16)
+    _dev(h, "h", torch.float32)
+    _dev(mlp, "mlp", torch.bfloat16)
+    _dev(norm_w, "norm_w", torch.bfloat16)
+    b = h.shape[0]
+    _ssq(ssq, "ssq", b, hidden // 32)
+    if attn.numel() < b * q_dim or mlp.numel() < b * inter or h.numel() < b * hidden:
+        raise ValueError("attn, h or mlp too small for the batch")
+    ws = ws or default_workspace()
+    wp, wn = ws.get(_lib.lib().q4nx_layer_tail_ws_bytes(hidden, q_dim, inter, b))
+    _lib.call("q4nx_layer_tail", _ptr(wo), _ptr(wg), _ptr(wu), _ptr(wd), hidden, q_dim, inter,
+              _ptr(attn), _ptr(h), _ptr(ssq), _ptr(norm_w), float(eps), _ptr(mlp), b, wp, wn,
+              _stream())
+
+
+def ws_check(ws: Workspace | None = None) -> None:
+    """Synchronise and raise if a multi-stage launch on this workspace timed out."""
+    ws = ws or default_workspace()
+    _lib.call("q4nx_ws_check", ws.buf.data_ptr(), _stream())
+
+
 # ---------------------------------------------------------------- attention
 
 def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

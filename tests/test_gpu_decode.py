@@ -54,11 +54,13 @@ def check_step(got, ref, token):
     return rel, cos
 
 
-@pytest.mark.parametrize("n_layers,batch,ctx,n_new", [(2, 1, 256, 6), (1, 3, 100, 3)])
-def test_decode_steps_vs_oracle(dev, n_layers, batch, ctx, n_new):
+@pytest.mark.parametrize("n_layers,batch,ctx,n_new,fused", [(2, 1, 256, 6, False),
+                                                            (1, 3, 100, 3, False),
+                                                            (2, 1, 200, 3, True)])
+def test_decode_steps_vs_oracle(dev, n_layers, batch, ctx, n_new, fused):
     cfg = GraniteConfig(n_layers=n_layers)
     w = GraniteWeights.synthetic(cfg, seed=11, device=dev)
-    dec = GraniteDecoder(w, max_batch=batch, max_len=ctx + n_new, device=dev)
+    dec = GraniteDecoder(w, max_batch=batch, max_len=ctx + n_new, device=dev, fused_tail=fused)
     dec.seed_cache(ctx, seed=12)
     kc = [host_bits(t) for t in dec.k_cache]
     vc = [host_bits(t) for t in dec.v_cache]
@@ -76,11 +78,12 @@ def test_decode_steps_vs_oracle(dev, n_layers, batch, ctx, n_new):
         prev = toks[:, i]
 
 
-def test_graph_equals_eager(dev):
+@pytest.mark.parametrize("fused", [False, True])
+def test_graph_equals_eager(dev, fused):
     """A graph replay computes bit-identical logits to the eager step."""
     cfg = GraniteConfig(n_layers=2)
     w = GraniteWeights.synthetic(cfg, seed=21, device=dev)
-    dec = GraniteDecoder(w, max_batch=1, max_len=320, device=dev)
+    dec = GraniteDecoder(w, max_batch=1, max_len=320, device=dev, fused_tail=fused)
     dec.seed_cache(300, seed=22)
     snap_k = [t.clone() for t in dec.k_cache]
     snap_v = [t.clone() for t in dec.v_cache]

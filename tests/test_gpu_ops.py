@@ -350,3 +350,67 @@ def test_embed_and_argmax(dev):
     logits[1, 5000] = logits[1, 7000] = 99.0         # first maximum wins
     idx = ops.argmax(torch.from_numpy(logits).to(dev)).cpu().numpy()
     assert idx.tolist() == np.argmax(logits, axis=1).tolist()
+
+
+# ------------------------------------------------------------------ fused layer tail
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_layer_tail_equals_chain(dev, batch):
+    """o-proj -> RMSNorm/[gate,up,SwiGLU] -> down in one three-stage launch gives bit for bit
+    what the three separate launches give with the same K splits (1, 2 and 4 parts with
+    10-wave workgroups up to batch 2; 2, 3 and 4 with 8 waves above), and the chain
+    agrees with the float64 oracle run on the kernel's own intermediates."""
+    parts = (1, 2, 4) if batch <= 2 else (2, 3, 4)
+    rng = np.random.default_rng(31 + batch)
+    hid, qd, inter = 2560, 2560, 8192
+    wo = synth.q4_tiles(rng, hid, qd).reshape(-1)
+    wg = synth.q4_tiles(rng, inter, hid).reshape(-1)
+    wu = synth.q4_tiles(rng, inter, hid).reshape(-1)
+    wd = synth.q4_tiles(rng, hid, inter).reshape(-1)
+    attn = synth.random_bf16(rng, (batch, qd))
+    h0 = (rng.standard_normal((batch, hid)) * 3).astype(np.float32)
+    nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    W = [d(x) for x in (wo, wg, wu, wd)]
+    ad, nwd = bf16_dev(attn, dev), bf16_dev(nw, dev)
+    ws = ops.Workspace(16 << 20, device=dev)
+
+    h_f, ss_f = d(h0), torch.zeros((batch, hid // 32), dtype=torch.float32, device=dev)
+    mlp_f = torch.zeros((batch, inter), dtype=torch.bfloat16, device=dev)
+    ops.layer_tail(*W, hid, qd, inter, ad, h_f, ss_f, nwd, 1e-5, mlp_f, ws=ws)
+    ops.ws_check(ws)
+
+    h_c, ss_c = d(h0), torch.zeros((batch, hid // 32), dtype=torch.float32, device=dev)
+    try:
+        ops.set_gemv_ksplit(parts[0])
+        ops.gemv_ex(W[0], "q4", ad, hid // 32, qd // 256, residual=h_c, out=h_c, ssq_out=ss_c,
+                    ws=ws)
+        h1 = h_c.cpu().numpy().copy()
+        ops.set_gemv_ksplit(parts[1])
+        mlp_c = ops.gate_up_swiglu(W[1], W[2], inter // 32, hid // 256, h_c, norm_w=nwd,
+                                   eps=1e-5, ws=ws, ssq_in=ss_c)
+        ops.set_gemv_ksplit(parts[2])
+        ops.gemv_ex(W[3], "q4", mlp_c, hid // 32, inter // 256, residual=h_c, out=h_c,
+                    ssq_out=ss_c, ws=ws)
+    finally:
+        ops.set_gemv_ksplit(0)
+    assert np.array_equal(bits(mlp_f), bits(mlp_c))
+    assert np.array_equal(h_f.cpu().numpy().view(np.uint32), h_c.cpu().numpy().view(np.uint32))
+    assert np.array_equal(ss_f.cpu().numpy().view(np.uint32), ss_c.cpu().numpy().view(np.uint32))
+    # the chain itself, stage by stage, against the oracle on its own inputs
+    ref1 = h0 + qo.gemv(wo.reshape(-1, 5120), "q4", attn, hid // 32, qd // 256,
+                        acc=np.float64).reshape(batch, hid)
+    assert_close(h1, ref1)
+    mlp_bits = bits(mlp_f)
+    ref2 = qo.gemv(wd.reshape(-1, 5120), "q4", mlp_bits, hid // 32, inter // 256,
+                   acc=np.float64).reshape(batch, hid)
+    # the down GEMV's own output (the residual add is one more fp32 rounding of h)
+    assert_close(h_f.cpu().numpy().astype(np.float64) - h1, ref2)
+    xn = do.rmsnorm(h1, nw, 1e-5)
+    g = qo.gemv(wg.reshape(-1, 5120), "q4", qo.bf16_round(xn.astype(np.float32)), inter // 32,
+                hid // 256, acc=np.float64).reshape(batch, inter)
+    u = qo.gemv(wu.reshape(-1, 5120), "q4", qo.bf16_round(xn.astype(np.float32)), inter // 32,
+                hid // 256, acc=np.float64).reshape(batch, inter)
+    r = qo.bf16_to_f32(mlp_bits).astype(np.float64)
+    ref_m = do.swiglu_from_raw(g, u)
+    assert qo.metrics(r, ref_m)[1] > 0.9999      # xn may differ from the kernel's by 1 ulp
