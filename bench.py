@@ -140,6 +140,105 @@ def measured_traffic() -> int | None:
         return None
 
 
+def _graph_time(fn, reps: int, warm: int = 2) -> float:
+    """Seconds per call of fn (a sequence of launches) captured in one HIP graph."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def random_q8_tiles(n: int, k: int, gen: torch.Generator, dev) -> torch.Tensor:
+    """Device-generated q8 tiles: int8 codes in [-127, 127], s = bf16(|N|*0.01)."""
+    t = (n // 32) * (k // 256)
+    w = torch.randint(-127, 128, (t, 8704), dtype=torch.int8, device=dev, generator=gen)
+    s = (torch.randn((t, 256), device=dev, generator=gen).abs() * 0.01).to(torch.bfloat16)
+    w = w.view(torch.uint8)
+    w[:, 0:512] = s.view(torch.uint8).reshape(t, 512)
+    return w.reshape(-1)
+
+
+def secondary_bench(dev) -> dict:
+    """The other shapes of the hot path, each timed over a graph of launches with inputs
+    resident in HBM (weights rotated past the 256 MB Infinity Cache where they would fit):
+    the q8 lm_head GEMV, the [gate,up,SwiGLU] + down MLP at batch 1 and 8, RoPE, GQA decode
+    attention over the context lengths and batches of the parity tests, and a plain copy."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    out = {}
+    # q8 lm_head 248320 x 1024, two copies (540 MB)
+    n, k = 248320, 1024
+    ws = [random_q8_tiles(n, k, gen, dev) for _ in range(2)]
+    x = torch.randn(k, device=dev, generator=gen).to(torch.bfloat16)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    t = _graph_time(lambda: [ops.gemv(w, "q8", x, n // 32, k // 256, out=y) for w in ws], 10) / 2
+    b = ws[0].numel() + 2 * k + 4 * n
+    out["lm_head_q8_248320x1024"] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+    del ws
+    # MLP: [gate, up, SwiGLU] then down, 8 layers rotated (315 MB), batch 1 and 8
+    layers = [(random_q4_tiles(INTER, HIDDEN, gen, dev), random_q4_tiles(INTER, HIDDEN, gen, dev),
+               random_q4_tiles(HIDDEN, INTER, gen, dev)) for _ in range(8)]
+    wsp = ops.Workspace(8 << 20, device=dev)
+    for bb in (1, 8):
+        xb = torch.randn(bb, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
+        hb = torch.empty(bb, INTER, dtype=torch.bfloat16, device=dev)
+        yb = torch.empty(bb, HIDDEN, dtype=torch.float32, device=dev)
+
+        def mlp():
+            for g_, u_, d_ in layers:
+                ops.gate_up_swiglu(g_, u_, INTER // 32, HIDDEN // 256, xb, h_out=hb, ws=wsp)
+                ops.gemv(d_, "q4", hb, HIDDEN // 32, INTER // 256, out=yb, ws=wsp)
+        t = _graph_time(mlp, 10) / len(layers)
+        byt = 3 * q4_bytes(INTER, HIDDEN) + bb * (2 * HIDDEN + 2 * INTER * 2 + 4 * HIDDEN)
+        out[f"mlp_gate_up_swiglu_down_b{bb}"] = {"us": round(t * 1e6, 2),
+                                                 "GB/s": round(byt / t / 1e9, 1)}
+    del layers
+    # RoPE on q [B,40,64] and k [B,8,64]
+    tab = ops.rope_table(4096, 64, 10000.0, device=dev)
+    for bb in (1, 8):
+        q = torch.randn(bb, 40, 64, device=dev, generator=gen).to(torch.bfloat16)
+        kk = torch.randn(bb, 8, 64, device=dev, generator=gen).to(torch.bfloat16)
+        pos = torch.randint(0, 4096, (bb,), dtype=torch.int32, device=dev, generator=gen)
+        qo_, ko_ = torch.empty_like(q), torch.empty_like(kk)
+        t = _graph_time(lambda: (ops.rope(q, pos, tab, out=qo_), ops.rope(kk, pos, tab, out=ko_)),
+                        50)
+        out[f"rope_q40_k8_b{bb}"] = {"us": round(t * 1e6, 2)}
+    # GQA decode attention, 40 q / 8 kv heads, d 64
+    wsa = ops.Workspace(64 << 20, device=dev)
+    for bb in (1, 8):
+        for L in (512, 4096, 32768):
+            kv_bytes = bb * 8 * L * 64 * 2 * 2
+            copies = max(1, min(8, (600 << 20) // kv_bytes))
+            caches = [(torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16),
+                       torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16))
+                      for _ in range(copies)]
+            q = torch.randn(bb, 40, 64, device=dev, generator=gen).to(torch.bfloat16)
+            lens = torch.full((bb,), L, dtype=torch.int32, device=dev)
+            o = torch.empty_like(q)
+            t = _graph_time(lambda: [ops.gqa_decode(q, kc, vc, lens, 0.125, out=o, ws=wsa)
+                                     for kc, vc in caches], 10) / copies
+            out[f"gqa_decode_b{bb}_L{L}"] = {"us": round(t * 1e6, 2),
+                                             "GB/s": round(kv_bytes / t / 1e9, 1)}
+            del caches
+    # plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB): the achievable streaming rate
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    t = _graph_time(lambda: dst.copy_(src), 5)
+    out["copy_1GiB"] = {"us": round(t * 1e6, 1), "GB/s": round(2 * (1 << 30) / t / 1e9, 1)}
+    return out
+
+
 def decode_bytes_per_token(cfg: GraniteConfig, ctx: int, n_new: int) -> float:
     """Algorithmic HBM bytes of one decode step, averaged over the generated positions:
     every weight tile once, the K/V cache up to the current position (read) plus one
@@ -261,6 +360,8 @@ def main() -> int:
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-decode-tokens", type=int, default=2)
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other shapes (lm_head, MLP, RoPE, attention, copy)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     a = ap.parse_args()
@@ -283,6 +384,7 @@ def main() -> int:
     dec = None
     if not a.no_decode:
         dec = decode_bench(a.ctx, a.new_tokens, dev, 0 if a.no_cpu else a.cpu_decode_tokens)
+    sec = None if a.no_secondary else secondary_bench(dev)
     gbs = r["gbs"]
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) + decode tok/s, granite-3B shape, batch 1",
@@ -330,6 +432,8 @@ def main() -> int:
             "roofline_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
             "cpu_baseline": dec.get("cpu"),
         }
+    if sec is not None:
+        line["other_shapes"] = sec
     print(json.dumps(line), flush=True)
     return 0
 

@@ -212,7 +212,8 @@ def rope_table(max_pos: int, head_dim: int = 64, theta: float = 10000.0,
     return torch.from_numpy(tab).to(device)
 
 
-def rope(x: torch.Tensor, positions: torch.Tensor, table: torch.Tensor, want_f32: bool = False):
+def rope(x: torch.Tensor, positions: torch.Tensor, table: torch.Tensor, want_f32: bool = False,
+         out: torch.Tensor | None = None):
     """Half-split RoPE on bf16 x [B, H, D] with per-sequence positions [B]."""
     _dev(x, "x", torch.bfloat16)
     _dev(positions, "positions", torch.int32)
@@ -220,7 +221,8 @@ def rope(x: torch.Tensor, positions: torch.Tensor, table: torch.Tensor, want_f32
     b, h, d = x.shape
     if positions.numel() != b:
         raise ValueError("one position per sequence")
-    y = torch.empty_like(x)
+    y = torch.empty_like(x) if out is None else out
+    _dev(y, "out", torch.bfloat16)
     yf = torch.empty(x.shape, dtype=torch.float32, device=x.device) if want_f32 else None
     _lib.call("q4nx_rope", _ptr(x), _ptr(y), _ptr(yf), h, d, b, _ptr(positions), _ptr(table),
               table.shape[0], _stream())
