@@ -104,6 +104,22 @@ int q4nx_set_split_tiles(int tiles_per_wave);
  * Process-wide. No reference counterpart: on the NPU each core owned whole rows. */
 int q4nx_set_gemv_ksplit(int parts);
 
+/* ---------------------------------------------------------------- batched contraction (MFMA)
+ * y[m][n] = residual[m][n] + sum_k W[n][k] * x[m][k] for m < m_rows, any m_rows >= 1, on the
+ * matrix cores; fp32 out. Replaces the torch fallback reference/npu.py:118-122, 138-140
+ * takes for prefill (more than one row), and carries the batched design of
+ * designs/granite_gemv/granite_gemv.h:79-91 (tokens share one weight pass) past 8 rows.
+ *   w: q4 or q8 tiles (kind), 16-byte aligned; x: bf16 [m_rows][x_stride], x_stride % 8 == 0;
+ *   y, residual: fp32 [m_rows][y_stride], y_stride % 4 == 0, 16-byte aligned.
+ *   ws: workspace of q4nx_gemm_ws_bytes(...) bytes, zeroed once (K is split across
+ *   workgroups when the launch has few of them); NULL runs without the split. */
+size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows);
+int q4nx_gemm(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const uint16_t *x,
+              int64_t x_stride, int m_rows, float *y, int64_t y_stride, const float *residual,
+              void *ws, size_t ws_bytes, void *stream);
+/* Tuning knob: workgroups along K for q4nx_gemm (1..8), 0 = automatic. Process-wide. */
+int q4nx_set_gemm_ksplit(int parts);
+
 /* ---------------------------------------------------------------- elementwise
  * RMSNorm y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, bf16 out (+ optional fp32
  * pre-rounding copy). Replaces designs/granite_gemv/granite_rmsnorm.h:82-87

@@ -26,6 +26,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     # packed fp32 VALU forms are kept out of generated code on this target
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the epilogue reads them without v_accvgpr_read copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 

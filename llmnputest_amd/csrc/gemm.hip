@@ -1,0 +1,462 @@
+// q4nx batched contraction on the matrix cores (gfx950): Y[m][n] = R[m][n] + sum_k W[n][k] X[m][k]
+// for any number of rows m (batched decode, prefill), W read in the q4nx tile layout.
+//
+// Replaces the torch fallback that reference/npu.py:118-122, 138-140 takes for more than one
+// row (prefill), and extends the batched design of designs/granite_gemv/granite_gemv.h:79-91
+// (B tokens share one weight pass) from B <= 8 to any row count.
+//
+// Operands of v_mfma_f32_16x16x32_bf16 (verified layout: A[i][k] in lane i + 16(k/8), element
+// k%8; B[k][j] in lane j + 16(k/8), element k%8; D[i][j] in lane j + 16(i/4), element i%4):
+//   A = x rows (16 per m-tile), loaded straight from global memory: 16 contiguous bytes per
+//       lane and 32-K group.
+//   B = weight codes, 16 output rows per operand. A q4nx tile stores, per row-block of 16 rows
+//       and per k, 8 bytes whose low nibble is row 2p and high nibble row 2p+1 (tools/q4nx.py:
+//       46-56). The tile is copied to LDS as stored and read back with ds_read_b64_tr_b8,
+//       which hands lane (8h + p) of each 16-lane group the byte of pair p at 8 consecutive k
+//       of row-block h: one LDS read yields the codes of 32 rows x 8 k in two operands, the
+//       low nibbles (even rows) and the high nibbles (odd rows). For q8 (16 bytes per k and
+//       row-block) the same read yields one row-block's 16 rows.
+//   Codes become exact bf16 values without a table: a q4 code c in bits 3-6 of 0x4180 is
+//   16 + c; a q8 code q, biased to q + 128 in 0..255, converts with v_cvt_f32_ubyte.
+// Per 32-K group g each MFMA product P = sum_k (c_k + o) x_k is exact-input, fp32-accumulated,
+// and one more MFMA against ones gives S = sum_k x_k for every row; the Q4_1 identity
+// (granite_gemv.h:19-29) y += d P + (m - o d) S (q4: o = 16) or s P - 128 s S (q8) is
+// applied in fp32 per group. Waves along K combine through LDS in a fixed order; split-K
+// across workgroups publishes parts with system-scope stores and the last arriver adds them
+// in part order, as the GEMV does, so results are bit-reproducible.
+
+#include "common.h"
+
+namespace q4nx {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
+
+struct GemmArgs {
+  const uint8_t* w;
+  const uint16_t* x;
+  float* y;
+  const float* residual;
+  int64_t x_stride, y_stride;
+  int m_rows, n_tr, k_t;
+  int ksplit, kpp;       // workgroups along K, K-tiles per part
+  float* part;           // [group][part][m_block][RT*32] fp32
+  uint32_t part_bytes;
+  unsigned* counters;    // one arrival counter per (group, m-block)
+};
+
+template <int KIND>
+struct GemmFmt;
+template <>
+struct GemmFmt<4> {
+  static constexpr int kTile = kQ4TileBytes;
+  static constexpr int kCodes = 2 * kMetaBytes;   // codes start after d and m
+  static constexpr int kLoads = 5;                // 16-byte loads per lane per tile
+  static constexpr int kSlot = kQ4TileBytes;      // LDS bytes per staged tile
+};
+template <>
+struct GemmFmt<8> {
+  static constexpr int kTile = kQ8TileBytes;
+  static constexpr int kCodes = kMetaBytes;
+  static constexpr int kLoads = 9;                // 8704 B: the 9th load of lanes 32..63 is padding
+  static constexpr int kSlot = 9216;
+};
+
+__device__ __forceinline__ f32x4_t mfma_bf16(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// 8 transposed code bytes (k-slots 0..7 of one row pair) -> bf16 16 + c for the even row (low
+// nibbles) and the odd row (high nibbles).
+__device__ __forceinline__ void q4_operands(i32x2_t r, u32x4_t& ev, u32x4_t& od) {
+  const uint32_t w[2] = {(uint32_t)r.x, (uint32_t)r.y};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      // [b(2q), 0, b(2q+1), 0]
+      const uint32_t t = perm(0u, w[h], q ? 0x0C030C02u : 0x0C010C00u);
+      ev[2 * h + q] = ((t & 0x000F000Fu) << 3) | 0x41804180u;
+      od[2 * h + q] = ((t >> 1) & 0x00780078u) | 0x41804180u;
+    }
+  }
+}
+
+// 8 transposed int8 codes -> bf16 of q + 128 (exact: at most 8 significant bits); the byte
+// conversions compile to v_cvt_f32_ubyte0..3.
+__device__ __forceinline__ u32x4_t q8_operand(i32x2_t r) {
+  const uint32_t w[2] = {(uint32_t)r.x ^ 0x80808080u, (uint32_t)r.y ^ 0x80808080u};
+  u32x4_t o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t f0 = __float_as_uint((float)(w[h] & 0xFFu));
+    const uint32_t f1 = __float_as_uint((float)((w[h] >> 8) & 0xFFu));
+    const uint32_t f2 = __float_as_uint((float)((w[h] >> 16) & 0xFFu));
+    const uint32_t f3 = __float_as_uint((float)((w[h] >> 24) & 0xFFu));
+    o[2 * h] = perm(f1, f0, 0x07060302u);
+    o[2 * h + 1] = perm(f3, f2, 0x07060302u);
+  }
+  return o;
+}
+
+// One workgroup of 4 waves owns RT tile-rows x (16 MT WM) rows of X over the K-tiles of its
+// part; WK waves split those K-tiles round-robin and WM = 4 / WK waves take different m-tiles.
+// Each wave stages one tile per tile-row at a time in its own LDS slot while the next tile's
+// bytes are in flight to registers.
+template <int KIND, int RT, int MT, int WK>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+  constexpr int WM = 4 / WK;
+  constexpr int SLOT = GemmFmt<KIND>::kSlot;
+  constexpr int NLD = GemmFmt<KIND>::kLoads;
+  constexpr int TB = GemmFmt<KIND>::kTile;
+  constexpr int MB = 16 * MT * WM;          // rows of X per workgroup
+  constexpr int NW = RT * 32;               // outputs per row of X per workgroup
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+  const int wk = wave % WK, wm = wave / WK;
+  const int group = blockIdx.x / a.ksplit, kpart = blockIdx.x % a.ksplit;
+  const int tr0 = group * RT;
+  const int mblk = blockIdx.y;
+  const int m0 = mblk * MB + wm * 16 * MT;  // first row of this wave's m-tiles
+  const int kbeg = kpart * a.kpp;
+  const int kend = min(a.k_t, kbeg + a.kpp);
+  const int n_it = kend - kbeg > wk ? (kend - kbeg - wk + WK - 1) / WK : 0;
+  uint8_t* slot = lds + wave * RT * SLOT;
+
+  const int c = l & 15, s = l >> 4;         // operand column / k-slot group
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(m0 + 16 * mt + c, a.m_rows - 1);
+    xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
+  }
+  // ds_read_b64_tr_b8 row addresses: lane c of a 16-lane group addresses row (2j + h) with
+  // j = c/2, h = c%2 -> k = 8s + j of row-block h (q4) or row half h (q8)
+  const int tr_off = KIND == 4
+      ? GemmFmt<4>::kCodes + (c & 1) * 2048 + (8 * s + (c >> 1)) * 8
+      : GemmFmt<8>::kCodes + (8 * s + (c >> 1)) * 16 + (c & 1) * 8;
+  // this lane's output column within a tile-row, per operand: q4 even/odd row of pair p of
+  // row-block h (c = 8h + p); q8 row c of row-block 0 / 1
+  const int meta_off = KIND == 4 ? 2 * ((c >> 3) * 16 + 2 * (c & 7)) : 2 * c;
+
+  f32x4_t acc[RT][MT][2];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[r][mt][0] = acc[r][mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+  // this lane's 16-byte pieces of a tile: piece i at 16 (64 i + l); the last q8 piece of lanes
+  // 32..63 re-reads bytes inside the tile (its LDS copy lands in the slot's padding)
+  int ld_off[NLD];
+#pragma unroll
+  for (int i = 0; i < NLD; ++i)
+    ld_off[i] = 16 * (64 * i + l) - ((KIND == 8 && i == NLD - 1 && l >= 32) ? 512 : 0);
+  const uint8_t* wrow = a.w + (size_t)tr0 * a.k_t * TB;
+  const size_t tr_stride = (size_t)a.k_t * TB;
+
+  u32x4_t pf[RT][NLD];
+  if (n_it > 0) {
+    const uint8_t* t = wrow + (size_t)(kbeg + wk) * TB;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) pf[r][i] = *(const u32x4_t*)(t + r * tr_stride + ld_off[i]);
+  }
+
+  for (int it = 0; it < n_it; ++it) {
+    const int kt = kbeg + wk + it * WK;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) *(u32x4_t*)(slot + r * SLOT + 16 * (64 * i + l)) = pf[r][i];
+    // activations of this tile first, then the next tile's weights: the in-order load
+    // counter then lets the arithmetic start before the next tile arrives
+    u32x4_t xa[8][MT];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
+    asm volatile("" ::: "memory");
+    {  // the last iteration re-reads its own tile (an L2 hit) so the load count stays static
+      const uint8_t* t = wrow + (size_t)(it + 1 < n_it ? kt + WK : kt) * TB;
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) pf[r][i] = *(const u32x4_t*)(t + r * tr_stride + ld_off[i]);
+    }
+    asm volatile("" ::: "memory");
+
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+      f32x4_t sx[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) sx[mt] = mfma_bf16(xa[kb][mt], ones, zero);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const uint8_t* sl = slot + r * SLOT;
+        u32x4_t op[2];
+        float dd[2], mm[2];
+        if constexpr (KIND == 4) {
+          const i32x2_t cb = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (lds_i32x2_t*)(sl + tr_off + kb * 256));
+          q4_operands(cb, op[0], op[1]);
+          const uint32_t dv = *(const uint32_t*)(sl + kb * 64 + meta_off);
+          const uint32_t mv = *(const uint32_t*)(sl + kMetaBytes + kb * 64 + meta_off);
+          dd[0] = bf16lo(dv);
+          dd[1] = bf16hi(dv);
+          mm[0] = fmaf(-16.f, dd[0], bf16lo(mv));
+          mm[1] = fmaf(-16.f, dd[1], bf16hi(mv));
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const i32x2_t cb = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_i32x2_t*)(sl + tr_off + h * 4096 + kb * 512));
+            op[h] = q8_operand(cb);
+            dd[h] = bf16_to_f32(*(const uint16_t*)(sl + kb * 64 + h * 32 + meta_off));
+            mm[h] = -128.f * dd[h];
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const f32x4_t p = mfma_bf16(xa[kb][mt], op[h], zero);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[r][mt][h][e] = fmaf(mm[h], sx[mt][e], fmaf(dd[h], p[e], acc[r][mt][h][e]));
+          }
+      }
+    }
+  }
+
+  // ---- combine the waves: red[wave][m][n] (reuses the staging slots)
+  __syncthreads();
+  float* red = (float*)lds;
+  constexpr int RED = 16 * MT * NW;          // floats per wave
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = 16 * mt + 4 * s + e;
+          const int n = r * 32 + (KIND == 4 ? (c >> 3) * 16 + 2 * (c & 7) + h : h * 16 + c);
+          red[wave * RED + m * NW + n] = acc[r][mt][h][e];
+        }
+  __syncthreads();
+  // the block's row m lives in the record of wave (m / 16MT, wk = 0), row m % 16MT; the other
+  // K waves' records are added into it in wave order (each element has one owner thread)
+  auto outp = [&](int m, int n) -> float* {
+    return red + ((m / (16 * MT)) * WK) * RED + (m % (16 * MT)) * NW + n;
+  };
+  if constexpr (WK > 1) {
+    for (int e = tid; e < MB * NW / 4; e += 256) {
+      const int m = (4 * e) / NW, n = (4 * e) % NW;
+      float* dst = outp(m, n);
+      float4 v = *(const float4*)dst;
+#pragma unroll
+      for (int k = 1; k < WK; ++k) {
+        const float4 u = *(const float4*)(dst + k * RED);
+        v.x += u.x;
+        v.y += u.y;
+        v.z += u.z;
+        v.w += u.w;
+      }
+      *(float4*)dst = v;
+    }
+    __syncthreads();
+  }
+
+  if (a.ksplit > 1) {
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part, a.part_bytes);
+    const uint32_t nrec = MB * NW;           // floats per part record
+    const int cnt = group * gridDim.y + mblk;
+    const uint32_t rec0 = (uint32_t)(cnt * a.ksplit) * nrec * 4u;
+    for (int e = tid; e < (int)nrec / 4; e += 256)
+      st16_sys(pr, rec0 + (uint32_t)kpart * nrec * 4u + 16u * e,
+               *(const uint4*)outp((4 * e) / NW, (4 * e) % NW));
+    wait_vm();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&a.counters[cnt], 1u) == (unsigned)(a.ksplit - 1) ? 1 : 0;
+    __syncthreads();
+    if (!s_last) return;
+    for (int e = tid; e < (int)nrec / 4; e += 256) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int p = 0; p < a.ksplit; ++p) {
+        const uint4 u = ld16_sys(pr, rec0 + (uint32_t)p * nrec * 4u + 16u * e);
+        v.x += __uint_as_float(u.x);
+        v.y += __uint_as_float(u.y);
+        v.z += __uint_as_float(u.z);
+        v.w += __uint_as_float(u.w);
+      }
+      *(float4*)outp((4 * e) / NW, (4 * e) % NW) = v;
+    }
+    if (tid == 0)   // ready for the next launch
+      __hip_atomic_store(&a.counters[cnt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+  }
+
+  for (int e = tid; e < MB * NW / 4; e += 256) {
+    const int m = (4 * e) / NW, n = (4 * e) % NW;
+    const int gm = mblk * MB + m;
+    if (gm >= a.m_rows) continue;
+    float4 v = *(const float4*)outp(m, n);
+    const int64_t gn = (int64_t)tr0 * 32 + n;
+    if (a.residual != nullptr) {
+      const float4 rr = *(const float4*)(a.residual + gm * a.y_stride + gn);
+      v.x += rr.x;
+      v.y += rr.y;
+      v.z += rr.z;
+      v.w += rr.w;
+    }
+    *(float4*)(a.y + gm * a.y_stride + gn) = v;
+  }
+}
+
+// ---------------------------------------------------------------- host side
+
+struct GemmPlan {
+  int rt, mt, wk, ksplit, kpp, mb, m_blocks, groups;
+};
+
+static int g_gemm_ksplit = 0;   // 0: automatic
+
+static GemmPlan plan_gemm(int kind, int n_tr, int k_t, int m_rows) {
+  GemmPlan p{};
+  if (m_rows <= 16) {
+    p.rt = 1; p.mt = 1; p.wk = 4;
+  } else if (m_rows <= 32) {
+    p.rt = 1; p.mt = 2; p.wk = 4;
+  } else if (m_rows <= 64) {
+    p.rt = 1; p.mt = 2; p.wk = 2;
+  } else {
+    // two tile-rows per workgroup halve the x traffic; q8 keeps one (LDS stays under 64 KB)
+    p.rt = (kind == Q4NX_KIND_Q4 && n_tr % 2 == 0) ? 2 : 1; p.mt = 2; p.wk = 1;
+  }
+  p.mb = 16 * p.mt * (4 / p.wk);
+  p.m_blocks = (m_rows + p.mb - 1) / p.mb;
+  p.groups = n_tr / p.rt;
+  const int wgs = p.groups * p.m_blocks;
+  int ks = 1;
+  if (g_gemm_ksplit > 0) {
+    ks = g_gemm_ksplit;
+  } else if (wgs < 192 && k_t >= 8) {
+    ks = (240 + wgs - 1) / wgs;
+    const int cap = k_t / (2 * p.wk) > 0 ? k_t / (2 * p.wk) : 1;   // >= 2 tiles per wave
+    ks = ks < cap ? ks : cap;
+  }
+  ks = ks > 8 ? 8 : (ks < 1 ? 1 : ks);
+  ks = ks > k_t ? k_t : ks;
+  p.kpp = (k_t + ks - 1) / ks;
+  p.ksplit = (k_t + p.kpp - 1) / p.kpp;      // no empty parts
+  return p;
+}
+
+static size_t gemm_split_bytes(const GemmPlan& p) {
+  const size_t cnt = (size_t)p.groups * p.m_blocks;
+  if (p.ksplit <= 1 || cnt > Q4NX_WS_COUNTER_BYTES / 4) return 0;
+  return (size_t)Q4NX_WS_COUNTER_BYTES + cnt * p.ksplit * p.mb * p.rt * 32 * 4;
+}
+
+template <int KIND, int RT, int MT, int WK>
+static void gemm_launch_t(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
+  constexpr int lds = 4 * RT * GemmFmt<KIND>::kSlot;
+  static_assert(4 * 16 * MT * RT * 32 * 4 <= lds, "reduction does not fit the staging slots");
+  const dim3 grid((unsigned)(p.groups * p.ksplit), (unsigned)p.m_blocks);
+  hipLaunchKernelGGL((gemm_kernel<KIND, RT, MT, WK>), grid, dim3(256), lds, st, a);
+}
+
+template <int KIND>
+static void gemm_launch_k(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
+  if (p.wk == 4 && p.mt == 1) gemm_launch_t<KIND, 1, 1, 4>(a, p, st);
+  else if (p.wk == 4) gemm_launch_t<KIND, 1, 2, 4>(a, p, st);
+  else if (p.wk == 2) gemm_launch_t<KIND, 1, 2, 2>(a, p, st);
+  else if (p.rt == 2) gemm_launch_t<KIND, 2, 2, 1>(a, p, st);
+  else gemm_launch_t<KIND, 1, 2, 1>(a, p, st);
+}
+
+}  // namespace q4nx
+
+using namespace q4nx;
+
+extern "C" {
+
+int q4nx_set_gemm_ksplit(int parts) {
+  Q4NX_REQUIRE(parts >= 0 && parts <= 8, Q4NX_ERR_ARG,
+               "K parts per workgroup group must be 0 (automatic) or 1..8, got %d", parts);
+  g_gemm_ksplit = parts;
+  return Q4NX_OK;
+}
+
+size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows) {
+  if ((kind != Q4NX_KIND_Q4 && kind != Q4NX_KIND_Q8) || n_tile_rows < 1 || k_tiles < 1 ||
+      m_rows < 1)
+    return 0;
+  return gemm_split_bytes(plan_gemm(kind, n_tile_rows, k_tiles, m_rows));
+}
+
+int q4nx_gemm(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const uint16_t* x,
+              int64_t x_stride, int m_rows, float* y, int64_t y_stride, const float* residual,
+              void* ws, size_t ws_bytes, void* stream) {
+  const char* what = "q4nx_gemm";
+  Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
+               "%s: kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", what, kind);
+  Q4NX_REQUIRE(w != nullptr && Q4NX_ALIGNED(w, 16), Q4NX_ERR_ARG,
+               "%s: weights must be a non-null 16-byte aligned device pointer", what);
+  Q4NX_REQUIRE(n_tile_rows > 0 && k_tiles > 0, Q4NX_ERR_SHAPE,
+               "%s: n_tile_rows=%d k_tiles=%d must be positive (N %% 32 == 0, K %% 256 == 0)",
+               what, n_tile_rows, k_tiles);
+  Q4NX_REQUIRE(m_rows >= 1, Q4NX_ERR_SHAPE, "%s: m_rows=%d must be positive", what, m_rows);
+  Q4NX_REQUIRE(x != nullptr && Q4NX_ALIGNED(x, 16), Q4NX_ERR_ARG,
+               "%s: x must be a non-null 16-byte aligned device pointer", what);
+  Q4NX_REQUIRE(x_stride >= (int64_t)k_tiles * 256 && x_stride % 8 == 0, Q4NX_ERR_SHAPE,
+               "%s: x_stride=%lld must be a multiple of 8 and >= K=%d", what,
+               (long long)x_stride, k_tiles * 256);
+  Q4NX_REQUIRE(y != nullptr && Q4NX_ALIGNED(y, 16), Q4NX_ERR_ARG,
+               "%s: y must be a non-null 16-byte aligned device pointer", what);
+  Q4NX_REQUIRE(y_stride >= (int64_t)n_tile_rows * 32 && y_stride % 4 == 0, Q4NX_ERR_SHAPE,
+               "%s: y_stride=%lld must be a multiple of 4 and >= N=%d", what,
+               (long long)y_stride, n_tile_rows * 32);
+  Q4NX_REQUIRE(residual == nullptr || Q4NX_ALIGNED(residual, 16), Q4NX_ERR_ARG,
+               "%s: residual must be 16-byte aligned", what);
+  GemmPlan p = plan_gemm(kind, n_tile_rows, k_tiles, m_rows);
+  const size_t need = gemm_split_bytes(p);
+  if (p.ksplit > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256))) {
+    p.ksplit = 1;   // no (or too small a) workspace: whole K per workgroup
+    p.kpp = k_tiles;
+  }
+  GemmArgs a{};
+  a.w = w;
+  a.x = x;
+  a.y = y;
+  a.residual = residual;
+  a.x_stride = x_stride;
+  a.y_stride = y_stride;
+  a.m_rows = m_rows;
+  a.n_tr = n_tile_rows;
+  a.k_t = k_tiles;
+  a.ksplit = p.ksplit;
+  a.kpp = p.kpp;
+  if (p.ksplit > 1) {
+    a.counters = (unsigned*)ws;
+    a.part = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
+    a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (kind == Q4NX_KIND_Q4) gemm_launch_k<4>(a, p, st);
+  else gemm_launch_k<8>(a, p, st);
+  return check_launch(what);
+}
+
+}  // extern "C"

@@ -116,6 +116,43 @@ def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_ti
     return out.reshape(n) if squeeze else out
 
 
+def gemm(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
+         residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+         ws: Workspace | None = None) -> torch.Tensor:
+    """Y = residual + X @ W^T on the matrix cores, fp32, for any number of rows.
+    x: bf16 [M, K] (row stride a multiple of 8) or [K]. Returns [M, N] (or [N])."""
+    _tiles(tiles, kind, n_tile_rows, k_tiles)
+    if not (x.is_cuda and x.dtype == torch.bfloat16):
+        raise ValueError("x must be a bf16 tensor on the GPU")
+    squeeze = x.dim() == 1
+    x2 = x.reshape(1, -1) if squeeze else x
+    if x2.dim() != 2 or x2.stride(1) != 1:
+        raise ValueError("x must be [M, K] with unit stride along K")
+    m, k = x2.shape
+    if k != k_tiles * 256:
+        raise Q4NXFormatError(f"x has K={k}, tiles have K={k_tiles * 256}")
+    n = n_tile_rows * 32
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _dev(out, "out", torch.float32)
+    if out.numel() != m * n:
+        raise ValueError("out must hold [M, N] fp32")
+    if residual is not None:
+        _dev(residual, "residual", torch.float32)
+        if residual.numel() != m * n:
+            raise ValueError("residual must have the shape of the output")
+    ws = ws or default_workspace()
+    wp, wn = ws.get(_lib.lib().q4nx_gemm_ws_bytes(KIND[kind], n_tile_rows, k_tiles, m))
+    _lib.call("q4nx_gemm", KIND[kind], _ptr(tiles), n_tile_rows, k_tiles, _ptr(x2), x2.stride(0),
+              m, _ptr(out), n, _ptr(residual), wp, wn, _stream())
+    return out.reshape(n) if squeeze else out
+
+
+def set_gemm_ksplit(parts: int) -> None:
+    """Workgroups along K for `gemm` (0 = automatic)."""
+    _lib.call("q4nx_set_gemm_ksplit", int(parts))
+
+
 def _ssq(t, name, b, n):
     if t is not None:
         _dev(t, name, torch.float32)

@@ -80,6 +80,23 @@ def test_fused_and_attention_argument_errors():
     assert rc == ERR_ARG
 
 
+def test_gemm_argument_errors():
+    fake = C.c_void_p(0x10000)
+    rc, msg = rc_msg("q4nx_gemm", 3, fake, 8, 10, fake, 2560, 4, fake, 256, None, None, 0, None)
+    assert rc == ERR_ARG and "kind" in msg
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 0, fake, 256, None, None, 0, None)
+    assert rc == ERR_SHAPE and "m_rows" in msg
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2564, 4, fake, 256, None, None, 0, None)
+    assert rc == ERR_SHAPE and "x_stride" in msg            # not a multiple of 8
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 4, fake, 128, None, None, 0, None)
+    assert rc == ERR_SHAPE and "y_stride" in msg            # N = 256 does not fit
+    rc, msg = rc_msg("q4nx_gemm", 8, fake, 8, 10, fake, 2560, 4, C.c_void_p(0x10004), 256,
+                     None, None, 0, None)
+    assert rc == ERR_ARG and "y" in msg                     # misaligned output
+    rc, msg = rc_msg("q4nx_set_gemm_ksplit", 9)
+    assert rc == ERR_ARG
+
+
 def test_ws_queries():
     lib = _lib.lib()
     # 80 tile-rows do not fill the GPU: K is split 3 ways, partials [80][3][1][32] fp32
@@ -92,6 +109,12 @@ def test_ws_queries():
     assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64) == 0  # one split: no workspace
     big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768)    # 64 splits of (acc[64], m, l, pad)
     assert big == 65536 + 8 * 64 * 5 * 68 * 4
+    # batched contraction: 80 tile-rows x 1 block of 16 rows split 3 ways along K
+    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 8) == 65536 + 80 * 3 * 16 * 32 * 4
+    assert lib.q4nx_gemm_ws_bytes(4, 256, 10, 8) == 0      # 256 workgroups: no split
+    # 512 rows: 40 pairs of tile-rows x 4 blocks of 128 rows, split 2 ways
+    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 512) == 65536 + 160 * 2 * 128 * 64 * 4
+    assert lib.q4nx_gemm_ws_bytes(5, 80, 32, 8) == 0
 
 
 @pytest.mark.parametrize("max_pos,theta", [(4096, 10000.0), (64, 500000.0)])

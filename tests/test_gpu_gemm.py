@@ -1,0 +1,164 @@
+"""GPU parity of the batched q4/q8 contraction on the matrix cores (`q4nx_gemm`) against the
+oracle, for row counts from one (decode) to prefill lengths.
+
+Bars: max|Δ|/max|ref| < 1e-5 against the float64 oracle with cosine > 0.9999999 for every
+row (the reference's GEMV gate, designs/granite_gemv/granite_gemv.py:335, and its per-token
+check of the batched design, granite_gemv32.py:279-288); one-hot rows reproduce the
+float32 dequantised column bit-for-bit; split-K launches are bit-reproducible.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from llmnputest_amd import ops, synth
+from oracle import q4nx_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+COS = 0.9999999
+
+
+def _tiles(kind, n, k, seed):
+    rng = np.random.default_rng(seed)
+    t = synth.q4_tiles(rng, n, k) if kind == "q4" else synth.q8_tiles(rng, n, k)
+    return t.reshape(-1, t.shape[-1]), rng
+
+
+def _dev_u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).reshape(-1)).to(dev)
+
+
+def _dev_bf16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _check_rows(y, ref):
+    """Every row on its own, then the whole block."""
+    for i in range(ref.shape[0]):
+        rel, cos = qo.metrics(y[i], ref[i])
+        assert rel < REL and cos > COS, (i, rel, cos)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("m,n,k", [
+    (1, 128, 512),
+    (5, 128, 512),       # partial m-tile
+    (16, 256, 768),
+    (17, 256, 2560),     # two m-tiles, one of one row
+    (33, 128, 1024),     # K split over two waves, two m-tiles per wave
+    (64, 192, 768),
+    (65, 256, 1024),     # prefill blocks: 128 rows per workgroup
+    (200, 512, 2560),
+    (8, 2560, 8192),     # down_proj shape, batch 8: split K across workgroups
+])
+def test_gemm_parity(dev, kind, m, n, k):
+    raw, rng = _tiles(kind, n, k, 11 + m)
+    x = synth.random_bf16(rng, (m, k))
+    y = ops.gemm(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y, ref)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+def test_gemm_onehot_exact(dev, kind):
+    """Row i of x is the unit vector e_{k_i}: row i of y is column k_i of the float32
+    dequantised matrix, bit for bit (code * d + m rounds once, as tools/q4nx.py:127-137)."""
+    n, k = 96, 1024
+    raw, _ = _tiles(kind, n, k, 2)
+    cols = [0, 1, 7, 8, 31, 32, 255, 256, 511, 777, 1000, 1023, 5, 600, 64, 130, 900]
+    x = np.zeros((len(cols), k), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    y = ops.gemm(_dev_u8(raw, dev), kind, _dev_bf16(qo.bf16_round(x), dev), n // 32,
+                 k // 256).cpu().numpy()
+    wm = qo.dequant_matrix(raw, kind, n // 32, k // 256)
+    for i, kk in enumerate(cols):
+        assert np.array_equal(y[i].view(np.uint32), wm[:, kk].view(np.uint32)), kk
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 1e4, 1e30])
+def test_gemm_activation_range(dev, scale):
+    """bf16 x enters the matrix cores unchanged: any bf16 range is exact input."""
+    m, n, k = 24, 256, 2560
+    raw, rng = _tiles("q4", n, k, 8)
+    xf = rng.standard_normal((m, k)).astype(np.float32) * np.float32(scale)
+    xf[:, ::97] *= np.float32(1e-6)
+    x = qo.bf16_round(xf)
+    y = ops.gemm(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y, ref)
+
+
+def test_gemm_heavy_tailed(dev):
+    """Student-t(2) activations: a few entries dwarf the rest."""
+    m, n, k = 12, 512, 8192
+    raw, rng = _tiles("q4", n, k, 9)
+    x = qo.bf16_round(rng.standard_t(2.0, (m, k)).astype(np.float32))
+    y = ops.gemm(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y, ref)
+
+
+def test_gemm_residual_strided_x(dev):
+    """x rows with a stride longer than K, and a residual added once."""
+    m, n, k = 40, 256, 1536
+    raw, rng = _tiles("q4", n, k, 10)
+    xfull = synth.random_bf16(rng, (m, k + 64))
+    xd = _dev_bf16(xfull, dev)[:, :k]
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    y = ops.gemm(_dev_u8(raw, dev), "q4", xd, n // 32, k // 256,
+                 residual=torch.from_numpy(res).to(dev)).cpu().numpy()
+    ref = qo.gemv(raw, "q4", np.ascontiguousarray(xfull[:, :k]), n // 32, k // 256,
+                  acc=np.float64) + res
+    _check_rows(y, ref)
+
+
+@pytest.mark.parametrize("parts", [1, 2, 3, 5])
+@pytest.mark.parametrize("m", [3, 30, 100])
+def test_gemm_ksplit_deterministic(dev, parts, m):
+    """Any split of K gives the oracle's result, and the same bits on every call."""
+    n, k = 2560, 8192
+    raw, rng = _tiles("q4", n, k, 12)
+    w = _dev_u8(raw, dev)
+    x = synth.random_bf16(rng, (m, k))
+    xd = _dev_bf16(x, dev)
+    ops.set_gemm_ksplit(parts)
+    try:
+        y1 = ops.gemm(w, "q4", xd, n // 32, k // 256).cpu().numpy()
+        y2 = ops.gemm(w, "q4", xd, n // 32, k // 256).cpu().numpy()
+    finally:
+        ops.set_gemm_ksplit(0)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y1, ref)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+def test_gemm_matches_gemv_batch(dev, kind):
+    """For the batch sizes both paths take, the two agree to the oracle's bar."""
+    n, k, b = 1024, 2560, 8
+    raw, rng = _tiles(kind, n, k, 13)
+    w = _dev_u8(raw, dev)
+    x = synth.random_bf16(rng, (b, k))
+    xd = _dev_bf16(x, dev)
+    y_mma = ops.gemm(w, kind, xd, n // 32, k // 256).cpu().numpy()
+    y_vec = ops.gemv(w, kind, xd, n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y_mma, ref)
+    _check_rows(y_vec, ref)
+
+
+def test_gemm_q8_lm_head_prefill(dev):
+    """The tied lm_head shape of the granite-3B step (q8 2560 -> 100352) over 48 prompt rows,
+    checked against the oracle on a slice of the vocabulary."""
+    n, k, m = 100352, 2560, 48
+    rng = np.random.default_rng(14)
+    raw = synth.q8_tiles(rng, n, k).reshape(-1, qo.Q8_TILE_BYTES)
+    x = synth.random_bf16(rng, (m, k))
+    y = ops.gemm(_dev_u8(raw, dev), "q8", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    lo, hi = 96 * 32, 160 * 32   # tile-rows 96..159
+    k_t = k // 256
+    ref = qo.gemv(raw[lo // 32 * k_t: hi // 32 * k_t], "q8", x, (hi - lo) // 32, k_t,
+                  acc=np.float64)
+    _check_rows(y[:, lo:hi], ref)
