@@ -119,6 +119,13 @@ int q4nx_gemm(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const ui
               void *ws, size_t ws_bytes, void *stream);
 /* Tuning knob: workgroups along K for q4nx_gemm (1..8), 0 = automatic. Process-wide. */
 int q4nx_set_gemm_ksplit(int parts);
+/* Rows from which q4nx_gemv_q4/q8, q4nx_gemv_ex, q4nx_qkv_rope and q4nx_gate_up_swiglu run
+ * on the matrix-core kernels of q4nx_gemm (fused prologue and epilogues included) instead of
+ * the VALU GEMV, per kind; 0 = never. Defaults: q4 from 2 rows, q8 from 1 (measured faster
+ * there). On that path `batch` may exceed Q4NX_MAX_BATCH; an RMSNorm prologue there needs
+ * ssq_in (launches without it stay on the VALU kernel, batch <= 8).
+ * Process-wide. No reference counterpart. */
+int q4nx_set_mfma_rows(int kind, int min_rows);
 
 /* ---------------------------------------------------------------- elementwise
  * RMSNorm y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, bf16 out (+ optional fp32

@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_gemm_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
     "q4nx_gemm": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_i, c_p, c_i64, c_p, c_p, c_sz, c_p]),
     "q4nx_set_gemm_ksplit": (c_i, [c_i]),
+    "q4nx_set_mfma_rows": (c_i, [c_i, c_i]),
     "q4nx_rmsnorm": (c_i, [c_p, c_i, c_p, c_p, c_p, c_i, c_i, c_f, c_p]),
     "q4nx_rope": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_i, c_p]),
     "q4nx_rope_table_host": (c_i, [c_p, c_i, c_i, c_d]),

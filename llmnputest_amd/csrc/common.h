@@ -55,6 +55,16 @@ __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel)
   return __builtin_amdgcn_perm(s0, s1, sel);
 }
 
+// 64-bit key whose unsigned order is numpy's argmax order: larger value first, NaN above
+// everything, and on ties the smaller index (stored inverted in the low word).
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+  const uint32_t u = __float_as_uint(v);
+  uint32_t ord;
+  if ((u & 0x7fffffffu) > 0x7f800000u) ord = 0xffffffffu;
+  else ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - idx);
+}
+
 // Cross-workgroup publication without flushing the XCD L2s: partial results go out with
 // system-scope (L2-bypassing, write-through) stores, `wait_vm` waits until they are
 // acknowledged, and the workgroup that reads them back uses system-scope loads. An

@@ -298,7 +298,7 @@ int q4nx_decode_advance(const uint64_t* keys, int n_slots, int32_t* tokens, int3
                         int batch, void* stream) {
   Q4NX_REQUIRE(keys && tokens && pos && lens && step, Q4NX_ERR_ARG,
                "q4nx_decode_advance: keys, tokens, pos, lens and step are required");
-  Q4NX_REQUIRE(batch >= 1 && batch <= Q4NX_MAX_BATCH && n_slots >= 1, Q4NX_ERR_SHAPE,
+  Q4NX_REQUIRE(batch >= 1 && n_slots >= 1, Q4NX_ERR_SHAPE,
                "q4nx_decode_advance: batch=%d n_slots=%d", batch, n_slots);
   hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream,
                      (const unsigned long long*)keys, n_slots, tokens, pos, lens, history, step,

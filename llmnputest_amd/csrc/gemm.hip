@@ -26,6 +26,7 @@
 // in part order, as the GEMV does, so results are bit-reproducible.
 
 #include "common.h"
+#include "gemm.h"
 
 namespace q4nx {
 
@@ -34,19 +35,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
-
-struct GemmArgs {
-  const uint8_t* w;
-  const uint16_t* x;
-  float* y;
-  const float* residual;
-  int64_t x_stride, y_stride;
-  int m_rows, n_tr, k_t;
-  int ksplit, kpp;       // workgroups along K, K-tiles per part
-  float* part;           // [group][part][m_block][RT*32] fp32
-  uint32_t part_bytes;
-  unsigned* counters;    // one arrival counter per (group, m-block)
-};
 
 template <int KIND>
 struct GemmFmt;
@@ -103,11 +91,24 @@ __device__ __forceinline__ u32x4_t q8_operand(i32x2_t r) {
   return o;
 }
 
+// Row-wise 1/rms of the fp32 residual from its producer's sums of squares (one per 32
+// entries): lane (c, s) of a 16-lane column adds a quarter of row c's entries, the four
+// quarters meet through two lane exchanges.
+__device__ __forceinline__ float row_inv_rms(const float* ssq_row, int n_ss, int s, float K,
+                                             float eps) {
+  const int q = n_ss / 4;   // n_ss = K/32 = 8 k_tiles
+  float acc = 0.f;
+  for (int i = 0; i < q; ++i) acc += ssq_row[s * q + i];
+  acc += __shfl_xor(acc, 16);
+  acc += __shfl_xor(acc, 32);
+  return 1.0f / sqrtf(acc / K + eps);
+}
+
 // One workgroup of 4 waves owns RT tile-rows x (16 MT WM) rows of X over the K-tiles of its
 // part; WK waves split those K-tiles round-robin and WM = 4 / WK waves take different m-tiles.
 // Each wave stages one tile per tile-row at a time in its own LDS slot while the next tile's
 // bytes are in flight to registers.
-template <int KIND, int RT, int MT, int WK>
+template <int KIND, int OP, bool NORM, int RT, int MT, int WK>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   constexpr int WM = 4 / WK;
   constexpr int SLOT = GemmFmt<KIND>::kSlot;
@@ -115,13 +116,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   constexpr int TB = GemmFmt<KIND>::kTile;
   constexpr int MB = 16 * MT * WM;          // rows of X per workgroup
   constexpr int NW = RT * 32;               // outputs per row of X per workgroup
+  static_assert(OP == GOP_PLAIN || RT == 2, "fused epilogues pair two tile-rows");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ int s_last;
+  __shared__ unsigned long long skey[OP == GOP_PLAIN ? MB * RT : 1];
 
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int wk = wave % WK, wm = wave / WK;
   const int group = blockIdx.x / a.ksplit, kpart = blockIdx.x % a.ksplit;
-  const int tr0 = group * RT;
   const int mblk = blockIdx.y;
   const int m0 = mblk * MB + wm * 16 * MT;  // first row of this wave's m-tiles
   const int kbeg = kpart * a.kpp;
@@ -129,12 +131,41 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   const int n_it = kend - kbeg > wk ? (kend - kbeg - wk + WK - 1) / WK : 0;
   uint8_t* slot = lds + wave * RT * SLOT;
 
+  // weight tile-rows of this group
+  int seg = 0, hg = group;
+  const uint8_t* wr[RT];
+  if constexpr (OP == GOP_PLAIN) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) wr[r] = a.w[0] + (size_t)(group * RT + r) * a.k_t * TB;
+  } else if constexpr (OP == GOP_GATEUP) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) wr[r] = a.w[r] + (size_t)group * a.k_t * TB;
+  } else {
+    if (group >= a.grp_q + a.grp_k) {
+      seg = 2;
+      hg = group - a.grp_q - a.grp_k;
+    } else if (group >= a.grp_q) {
+      seg = 1;
+      hg = group - a.grp_q;
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) wr[r] = a.w[seg] + (size_t)(2 * hg + r) * a.k_t * TB;
+  }
+
   const int c = l & 15, s = l >> 4;         // operand column / k-slot group
+  const int K = a.k_t * kTileK;
   const uint16_t* xrow[MT];
+  const float* hrow[MT];
+  float inv_rms[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = min(m0 + 16 * mt + c, a.m_rows - 1);
-    xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
+    if constexpr (NORM) {
+      hrow[mt] = a.hres + (int64_t)m * a.x_stride + 8 * s;
+      inv_rms[mt] = row_inv_rms(a.ssq_in + (int64_t)m * (K / 32), K / 32, s, (float)K, a.eps);
+    } else {
+      xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
+    }
   }
   // ds_read_b64_tr_b8 row addresses: lane c of a 16-lane group addresses row (2j + h) with
   // j = c/2, h = c%2 -> k = 8s + j of row-block h (q4) or row half h (q8)
@@ -160,16 +191,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < NLD; ++i)
     ld_off[i] = 16 * (64 * i + l) - ((KIND == 8 && i == NLD - 1 && l >= 32) ? 512 : 0);
-  const uint8_t* wrow = a.w + (size_t)tr0 * a.k_t * TB;
-  const size_t tr_stride = (size_t)a.k_t * TB;
 
   u32x4_t pf[RT][NLD];
   if (n_it > 0) {
-    const uint8_t* t = wrow + (size_t)(kbeg + wk) * TB;
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) pf[r][i] = *(const u32x4_t*)(t + r * tr_stride + ld_off[i]);
+      for (int i = 0; i < NLD; ++i)
+        pf[r][i] = *(const u32x4_t*)(wr[r] + (size_t)(kbeg + wk) * TB + ld_off[i]);
   }
 
   for (int it = 0; it < n_it; ++it) {
@@ -181,22 +210,51 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     // activations of this tile first, then the next tile's weights: the in-order load
     // counter then lets the arithmetic start before the next tile arrives
     u32x4_t xa[8][MT];
+    float4 hx[NORM ? 8 : 1][MT][2];
+    u32x4_t nw[NORM ? 8 : 1];
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
+    for (int kb = 0; kb < 8; ++kb) {
+      if constexpr (NORM) {
+        nw[kb] = *(const u32x4_t*)(a.norm_w + kt * 256 + kb * 32 + 8 * s);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
+        for (int mt = 0; mt < MT; ++mt) {
+          hx[kb][mt][0] = *(const float4*)(hrow[mt] + kt * 256 + kb * 32);
+          hx[kb][mt][1] = *(const float4*)(hrow[mt] + kt * 256 + kb * 32 + 4);
+        }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
+      }
+    }
     asm volatile("" ::: "memory");
     {  // the last iteration re-reads its own tile (an L2 hit) so the load count stays static
-      const uint8_t* t = wrow + (size_t)(it + 1 < n_it ? kt + WK : kt) * TB;
+      const size_t off = (size_t)(it + 1 < n_it ? kt + WK : kt) * TB;
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) pf[r][i] = *(const u32x4_t*)(t + r * tr_stride + ld_off[i]);
+        for (int i = 0; i < NLD; ++i) pf[r][i] = *(const u32x4_t*)(wr[r] + off + ld_off[i]);
     }
     asm volatile("" ::: "memory");
 
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) {
+      if constexpr (NORM) {   // bf16((h * inv_rms) * w), as the GEMV prologue rounds it
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const float hv[8] = {hx[kb][mt][0].x, hx[kb][mt][0].y, hx[kb][mt][0].z, hx[kb][mt][0].w,
+                               hx[kb][mt][1].x, hx[kb][mt][1].y, hx[kb][mt][1].z, hx[kb][mt][1].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            xa[kb][mt][i] = pack_bf16x2((hv[2 * i] * inv_rms[mt]) * bf16lo(nw[kb][i]),
+                                        (hv[2 * i + 1] * inv_rms[mt]) * bf16hi(nw[kb][i]));
+          // the first output group's workgroups cover every (row, k) once
+          const int m = m0 + 16 * mt + c;
+          if (a.xn_out != nullptr && group == 0 && m < a.m_rows)
+            *(u32x4_t*)(a.xn_out + (int64_t)m * a.x_stride + kt * 256 + kb * 32 + 8 * s) =
+                xa[kb][mt];
+        }
+      }
       f32x4_t sx[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) sx[mt] = mfma_bf16(xa[kb][mt], ones, zero);
@@ -307,20 +365,90 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     __syncthreads();
   }
 
-  for (int e = tid; e < MB * NW / 4; e += 256) {
-    const int m = (4 * e) / NW, n = (4 * e) % NW;
-    const int gm = mblk * MB + m;
-    if (gm >= a.m_rows) continue;
-    float4 v = *(const float4*)outp(m, n);
-    const int64_t gn = (int64_t)tr0 * 32 + n;
-    if (a.residual != nullptr) {
-      const float4 rr = *(const float4*)(a.residual + gm * a.y_stride + gn);
-      v.x += rr.x;
-      v.y += rr.y;
-      v.z += rr.z;
-      v.w += rr.w;
+  // ---- epilogues, one thread per (row, output) with 32 consecutive threads on one tile-row
+  if constexpr (OP == GOP_PLAIN) {
+    const int n_tr = a.n_tr[0];
+    const int tr0 = group * RT;
+    if (a.argmax_keys != nullptr) {
+      for (int e = tid; e < MB * RT; e += 256) skey[e] = 0ull;
+      __syncthreads();
     }
-    *(float4*)(a.y + gm * a.y_stride + gn) = v;
+    for (int e0 = 0; e0 < MB * NW; e0 += 256) {   // MB * NW is a multiple of 256
+      const int e = e0 + tid;
+      const int m = e / NW, n = e % NW;
+      const int gm = mblk * MB + m;
+      const bool live = gm < a.m_rows;
+      const int64_t gn = (int64_t)tr0 * 32 + n;
+      float v = 0.f;
+      if (live) {
+        v = *outp(m, n);
+        if (a.residual != nullptr) v += a.residual[gm * a.y_stride + gn];
+        if (a.y != nullptr) a.y[gm * a.y_stride + gn] = v;
+        if (a.argmax_keys != nullptr) atomicMax(&skey[m * RT + n / 32], argmax_key(v, (uint32_t)gn));
+      }
+      if (a.ssq_out != nullptr) {
+        const float sq32 = group32_sum(v * v);
+        if (live && (n & 31) == 0) a.ssq_out[(int64_t)gm * n_tr + tr0 + n / 32] = sq32;
+      }
+    }
+    if (a.argmax_keys != nullptr) {
+      __syncthreads();
+      for (int e = tid; e < MB * RT; e += 256) {
+        const int gm = mblk * MB + e / RT;
+        if (gm < a.m_rows) a.argmax_keys[(int64_t)gm * n_tr + tr0 + e % RT] = skey[e];
+      }
+    }
+  } else if constexpr (OP == GOP_GATEUP) {
+    const int64_t N = (int64_t)a.n_tr[0] * 32;
+    for (int e = tid; e < MB * 32; e += 256) {
+      const int m = e >> 5, j = e & 31;
+      const int gm = mblk * MB + m;
+      if (gm >= a.m_rows) continue;
+      const int64_t n = (int64_t)group * 32 + j;
+      const float gr = *outp(m, j), ur = *outp(m, 32 + j);
+      const float g = bf16_to_f32(f32_to_bf16(gr));
+      const float uu = bf16_to_f32(f32_to_bf16(ur));
+      const float h = (g / (1.0f + expf(-g))) * uu;
+      a.h_out[gm * a.h_stride + n] = f32_to_bf16(h);
+      if (a.raw_out != nullptr) {
+        a.raw_out[gm * 2 * N + n] = gr;
+        a.raw_out[gm * 2 * N + N + n] = ur;
+      }
+    }
+  } else {   // QKV: one head of q, k or v (64 dims), RoPE pairs dim d with d + 32
+    int seg_off = 0;
+    if (seg == 1) seg_off = a.n_q_heads * 64;
+    else if (seg == 2) seg_off = (a.n_q_heads + a.n_kv_heads) * 64;
+    const int64_t Wd = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
+    for (int e = tid; e < MB * 32; e += 256) {
+      const int m = e >> 5, d = e & 31;
+      const int gm = mblk * MB + m;
+      if (gm >= a.m_rows) continue;
+      const float r0 = *outp(m, d), r1 = *outp(m, 32 + d);
+      if (a.raw_out != nullptr) {
+        a.raw_out[gm * Wd + seg_off + hg * 64 + d] = r0;
+        a.raw_out[gm * Wd + seg_off + hg * 64 + 32 + d] = r1;
+      }
+      const float x0 = bf16_to_f32(f32_to_bf16(r0));
+      const float x1 = bf16_to_f32(f32_to_bf16(r1));
+      const int p = a.pos[gm];
+      if (p < 0 || p >= a.max_pos) continue;
+      if (seg == 2) {
+        uint16_t* dst = a.v_cache + gm * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
+        dst[d] = f32_to_bf16(x0);
+        dst[32 + d] = f32_to_bf16(x1);
+      } else {
+        const float cs = a.rope_tab[(int64_t)p * 64 + d];
+        const float sn = a.rope_tab[(int64_t)p * 64 + 32 + d];
+        const float y0 = fmaf(x0, cs, -(x1 * sn));
+        const float y1 = fmaf(x1, cs, x0 * sn);
+        uint16_t* dst = seg == 0
+                            ? a.q_out + gm * (int64_t)a.n_q_heads * 64 + hg * 64
+                            : a.k_cache + gm * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
+        dst[d] = f32_to_bf16(y0);
+        dst[32 + d] = f32_to_bf16(y1);
+      }
+    }
   }
 }
 
@@ -332,21 +460,33 @@ struct GemmPlan {
 
 static int g_gemm_ksplit = 0;   // 0: automatic
 
-static GemmPlan plan_gemm(int kind, int n_tr, int k_t, int m_rows) {
+// Workgroup shape by row count: up to 16 rows the four waves split K; more rows go to more
+// waves and, past 64 (prefill), two m-tiles per wave. Fused epilogues and the RMSNorm
+// prologue keep one m-tile per wave (the prologue holds a tile of fp32 rows in registers).
+// n_units: tile-rows for PLAIN, output groups (of two tile-rows) for GATEUP and QKV.
+static GemmPlan plan_gemm(int kind, int op, bool norm, int n_units, int k_t, int m_rows) {
   GemmPlan p{};
+  const bool one_mt = norm || op != GOP_PLAIN;
   if (m_rows <= 16) {
-    p.rt = 1; p.mt = 1; p.wk = 4;
+    p.mt = 1; p.wk = 4;
   } else if (m_rows <= 32) {
-    p.rt = 1; p.mt = 2; p.wk = 4;
+    p.mt = one_mt ? 1 : 2; p.wk = one_mt ? 2 : 4;
   } else if (m_rows <= 64) {
-    p.rt = 1; p.mt = 2; p.wk = 2;
+    p.mt = one_mt ? 1 : 2; p.wk = one_mt ? 1 : 2;
   } else {
-    // two tile-rows per workgroup halve the x traffic; q8 keeps one (LDS stays under 64 KB)
-    p.rt = (kind == Q4NX_KIND_Q4 && n_tr % 2 == 0) ? 2 : 1; p.mt = 2; p.wk = 1;
+    p.mt = one_mt ? 1 : 2; p.wk = 1;
+  }
+  if (op != GOP_PLAIN) {
+    p.rt = 2;
+    p.groups = n_units;
+  } else {
+    // past 64 rows two tile-rows per workgroup halve the x traffic; q8 keeps one (LDS stays
+    // under 64 KB)
+    p.rt = (!one_mt && m_rows > 64 && kind == Q4NX_KIND_Q4 && n_units % 2 == 0) ? 2 : 1;
+    p.groups = n_units / p.rt;
   }
   p.mb = 16 * p.mt * (4 / p.wk);
   p.m_blocks = (m_rows + p.mb - 1) / p.mb;
-  p.groups = n_tr / p.rt;
   const int wgs = p.groups * p.m_blocks;
   int ks = 1;
   if (g_gemm_ksplit > 0) {
@@ -369,21 +509,82 @@ static size_t gemm_split_bytes(const GemmPlan& p) {
   return (size_t)Q4NX_WS_COUNTER_BYTES + cnt * p.ksplit * p.mb * p.rt * 32 * 4;
 }
 
-template <int KIND, int RT, int MT, int WK>
+template <int KIND, int OP, bool NORM, int RT, int MT, int WK>
 static void gemm_launch_t(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
   constexpr int lds = 4 * RT * GemmFmt<KIND>::kSlot;
   static_assert(4 * 16 * MT * RT * 32 * 4 <= lds, "reduction does not fit the staging slots");
   const dim3 grid((unsigned)(p.groups * p.ksplit), (unsigned)p.m_blocks);
-  hipLaunchKernelGGL((gemm_kernel<KIND, RT, MT, WK>), grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((gemm_kernel<KIND, OP, NORM, RT, MT, WK>), grid, dim3(256), lds, st, a);
+}
+
+// one m-tile per wave: WK = 4, 2 or 1
+template <int KIND, int OP, bool NORM, int RT>
+static void gemm_launch_mt1(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
+  if (p.wk == 4) gemm_launch_t<KIND, OP, NORM, RT, 1, 4>(a, p, st);
+  else if (p.wk == 2) gemm_launch_t<KIND, OP, NORM, RT, 1, 2>(a, p, st);
+  else gemm_launch_t<KIND, OP, NORM, RT, 1, 1>(a, p, st);
 }
 
 template <int KIND>
-static void gemm_launch_k(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
-  if (p.wk == 4 && p.mt == 1) gemm_launch_t<KIND, 1, 1, 4>(a, p, st);
-  else if (p.wk == 4) gemm_launch_t<KIND, 1, 2, 4>(a, p, st);
-  else if (p.wk == 2) gemm_launch_t<KIND, 1, 2, 2>(a, p, st);
-  else if (p.rt == 2) gemm_launch_t<KIND, 2, 2, 1>(a, p, st);
-  else gemm_launch_t<KIND, 1, 2, 1>(a, p, st);
+static void gemm_launch_plain(const GemmArgs& a, const GemmPlan& p, bool norm, hipStream_t st) {
+  if (norm) gemm_launch_mt1<KIND, GOP_PLAIN, true, 1>(a, p, st);
+  else if (p.mt == 1) gemm_launch_t<KIND, GOP_PLAIN, false, 1, 1, 4>(a, p, st);
+  else if (p.wk == 4) gemm_launch_t<KIND, GOP_PLAIN, false, 1, 2, 4>(a, p, st);
+  else if (p.wk == 2) gemm_launch_t<KIND, GOP_PLAIN, false, 1, 2, 2>(a, p, st);
+  else if (p.rt == 2) gemm_launch_t<KIND, GOP_PLAIN, false, 2, 2, 1>(a, p, st);
+  else gemm_launch_t<KIND, GOP_PLAIN, false, 1, 2, 1>(a, p, st);
+}
+
+// Rows from which the GEMV entry points run on the matrix cores, per kind (0: never).
+// Measured on MI355X: q4 from 2 rows (one row is as fast on the VALU kernel), q8 from one.
+static int g_mfma_rows[2] = {2, 1};
+
+bool mfma_use(int kind, int rows) {
+  const int t = g_mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0];
+  return t > 0 && rows >= t;
+}
+
+size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows) {
+  // the larger of the two prologue variants, so one query serves both
+  const size_t a = gemm_split_bytes(plan_gemm(kind, op, false, n_units, k_t, m_rows));
+  const size_t b = gemm_split_bytes(plan_gemm(kind, op, true, n_units, k_t, m_rows));
+  return a > b ? a : b;
+}
+
+// Launches the contraction described by `a` (weights, input, epilogue fields filled in);
+// sets the split-K fields from the plan and the workspace.
+int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
+                hipStream_t st, const char* what) {
+  const bool norm = a.norm_w != nullptr;
+  Q4NX_REQUIRE(!norm || a.ssq_in != nullptr, Q4NX_ERR_ARG,
+               "%s: with norm_w and %d rows the sums of squares ssq_in are required", what,
+               a.m_rows);
+  Q4NX_REQUIRE(op == GOP_PLAIN || kind == Q4NX_KIND_Q4, Q4NX_ERR_ARG,
+               "%s: fused epilogues take q4 tiles", what);
+  GemmPlan p = plan_gemm(kind, op, norm, n_units, a.k_t, a.m_rows);
+  const size_t need = gemm_split_bytes(p);
+  if (p.ksplit > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256))) {
+    p.ksplit = 1;   // no (or too small a) workspace: whole K per workgroup
+    p.kpp = a.k_t;
+  }
+  a.ksplit = p.ksplit;
+  a.kpp = p.kpp;
+  if (p.ksplit > 1) {
+    a.counters = (unsigned*)ws;
+    a.part = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
+    a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
+  }
+  if (op == GOP_PLAIN) {
+    if (kind == Q4NX_KIND_Q4) gemm_launch_plain<4>(a, p, norm, st);
+    else gemm_launch_plain<8>(a, p, norm, st);
+  } else if (op == GOP_GATEUP) {
+    if (norm) gemm_launch_mt1<4, GOP_GATEUP, true, 2>(a, p, st);
+    else gemm_launch_mt1<4, GOP_GATEUP, false, 2>(a, p, st);
+  } else {
+    if (norm) gemm_launch_mt1<4, GOP_QKV, true, 2>(a, p, st);
+    else gemm_launch_mt1<4, GOP_QKV, false, 2>(a, p, st);
+  }
+  return check_launch(what);
 }
 
 }  // namespace q4nx
@@ -403,7 +604,15 @@ size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows) {
   if ((kind != Q4NX_KIND_Q4 && kind != Q4NX_KIND_Q8) || n_tile_rows < 1 || k_tiles < 1 ||
       m_rows < 1)
     return 0;
-  return gemm_split_bytes(plan_gemm(kind, n_tile_rows, k_tiles, m_rows));
+  return gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, false, n_tile_rows, k_tiles, m_rows));
+}
+
+int q4nx_set_mfma_rows(int kind, int min_rows) {
+  Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
+               "kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", kind);
+  Q4NX_REQUIRE(min_rows >= 0, Q4NX_ERR_ARG, "min_rows must be >= 0, got %d", min_rows);
+  g_mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0] = min_rows;
+  return Q4NX_OK;
 }
 
 int q4nx_gemm(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const uint16_t* x,
@@ -430,33 +639,17 @@ int q4nx_gemm(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const ui
                (long long)y_stride, n_tile_rows * 32);
   Q4NX_REQUIRE(residual == nullptr || Q4NX_ALIGNED(residual, 16), Q4NX_ERR_ARG,
                "%s: residual must be 16-byte aligned", what);
-  GemmPlan p = plan_gemm(kind, n_tile_rows, k_tiles, m_rows);
-  const size_t need = gemm_split_bytes(p);
-  if (p.ksplit > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256))) {
-    p.ksplit = 1;   // no (or too small a) workspace: whole K per workgroup
-    p.kpp = k_tiles;
-  }
   GemmArgs a{};
-  a.w = w;
+  a.w[0] = w;
+  a.n_tr[0] = n_tile_rows;
   a.x = x;
   a.y = y;
   a.residual = residual;
   a.x_stride = x_stride;
   a.y_stride = y_stride;
   a.m_rows = m_rows;
-  a.n_tr = n_tile_rows;
   a.k_t = k_tiles;
-  a.ksplit = p.ksplit;
-  a.kpp = p.kpp;
-  if (p.ksplit > 1) {
-    a.counters = (unsigned*)ws;
-    a.part = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
-    a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
-  }
-  hipStream_t st = (hipStream_t)stream;
-  if (kind == Q4NX_KIND_Q4) gemm_launch_k<4>(a, p, st);
-  else gemm_launch_k<8>(a, p, st);
-  return check_launch(what);
+  return mfma_launch(kind, GOP_PLAIN, a, n_tile_rows, ws, ws_bytes, (hipStream_t)stream, what);
 }
 
 }  // extern "C"

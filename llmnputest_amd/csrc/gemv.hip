@@ -37,6 +37,9 @@
 //   y_r += d_r * sum(c x) + m_r * sum(x) per 32-K group.
 
 #include "common.h"
+#include "gemm.h"
+
+#include <climits>
 
 namespace q4nx {
 
@@ -129,16 +132,6 @@ __device__ __forceinline__ void stage_wait(const unsigned* cnt, unsigned target,
     }
   }
   __syncthreads();
-}
-
-// 64-bit key whose unsigned order is numpy's argmax order: larger value first, NaN above
-// everything, and on ties the smaller index (stored inverted in the low word).
-__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
-  const uint32_t u = __float_as_uint(v);
-  uint32_t ord;
-  if ((u & 0x7fffffffu) > 0x7f800000u) ord = 0xffffffffu;
-  else ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - idx);
 }
 
 constexpr int kMaxWaves = 16;
@@ -963,14 +956,16 @@ static void tail_stages(GemvArgs* st, int* ng, const uint8_t* wo, const uint8_t*
   ng[0] = hidden / 32; ng[1] = inter / 32; ng[2] = hidden / 32;
 }
 
-static int check_common(const void* w, int n_tile_rows, int k_tiles, int batch, const char* what) {
+static int check_common(const void* w, int n_tile_rows, int k_tiles, int batch, const char* what,
+                        int max_batch = Q4NX_MAX_BATCH) {
   Q4NX_REQUIRE(w != nullptr && Q4NX_ALIGNED(w, 16), Q4NX_ERR_ARG,
                "%s: weights must be a non-null 16-byte aligned device pointer", what);
   Q4NX_REQUIRE(n_tile_rows > 0 && k_tiles > 0, Q4NX_ERR_SHAPE,
                "%s: n_tile_rows=%d k_tiles=%d must be positive (N %% 32 == 0, K %% 256 == 0)",
                what, n_tile_rows, k_tiles);
-  Q4NX_REQUIRE(batch >= 1 && batch <= Q4NX_MAX_BATCH, Q4NX_ERR_SHAPE,
-               "%s: batch=%d outside 1..%d", what, batch, Q4NX_MAX_BATCH);
+  Q4NX_REQUIRE(batch >= 1 && batch <= max_batch, Q4NX_ERR_SHAPE,
+               "%s: batch=%d outside 1..%d (more rows need the matrix-core path)", what, batch,
+               max_batch);
   return Q4NX_OK;
 }
 
@@ -992,12 +987,21 @@ static int check_ssq_in(const float* ssq_in, const uint16_t* norm_w, int k_tiles
   return Q4NX_OK;
 }
 
+// Whether a launch of `batch` rows goes to the matrix-core kernels (gemm.hip): the policy
+// of q4nx_set_mfma_rows, and only for what they implement (the RMSNorm prologue there takes
+// the producer's sums of squares).
+static bool take_mfma(int kind, int batch, const uint16_t* norm_w, const float* ssq_in) {
+  if (!mfma_use(kind, batch)) return false;
+  return norm_w == nullptr || ssq_in != nullptr;
+}
+
 static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t* norm_w,
                       float eps, const float* ssq_in, float* y, int n_tile_rows, int k_tiles,
                       int batch, int64_t x_stride, int64_t y_stride, const float* residual,
                       float* ssq_out, unsigned long long* argmax_keys, void* stream,
                       const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
-  int rc = check_common(w, n_tile_rows, k_tiles, batch, what);
+  const bool mf = take_mfma(kind, batch, norm_w, ssq_in);
+  int rc = check_common(w, n_tile_rows, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
   if (rc) return rc;
   rc = check_x(x, x_stride, k_tiles, what);
   if (rc) return rc;
@@ -1015,6 +1019,28 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
                "%s: a residual needs an output", what);
   Q4NX_REQUIRE(argmax_keys == nullptr || Q4NX_ALIGNED(argmax_keys, 8), Q4NX_ERR_ARG,
                "%s: argmax keys must be 8-byte aligned", what);
+  if (mf) {
+    GemmArgs g{};
+    g.w[0] = w;
+    g.n_tr[0] = n_tile_rows;
+    g.k_t = k_tiles;
+    g.m_rows = batch;
+    if (norm_w) {
+      g.hres = (const float*)x;
+      g.norm_w = norm_w;
+      g.eps = eps;
+      g.ssq_in = ssq_in;
+    } else {
+      g.x = (const uint16_t*)x;
+    }
+    g.x_stride = x_stride;
+    g.y = y;
+    g.y_stride = y_stride;
+    g.residual = residual;
+    g.ssq_out = ssq_out;
+    g.argmax_keys = argmax_keys;
+    return mfma_launch(kind, GOP_PLAIN, g, n_tile_rows, ws, ws_bytes, (hipStream_t)stream, what);
+  }
   GemvArgs a{};
   a.w[0] = w;
   a.n_tr[0] = n_tile_rows;
@@ -1062,9 +1088,11 @@ int q4nx_set_split_tiles(int tiles) {
 // Workspace of a split-K launch (0 when the launch has enough groups to fill the GPU).
 // Without it the launches still run, one workgroup per group.
 size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch) {
-  (void)kind;
-  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1 || batch > Q4NX_MAX_BATCH) return 0;
-  return ws_need(n_tile_rows, 1, k_tiles, batch);
+  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1) return 0;
+  // either kernel may take the launch (the VALU one when the matrix-core one cannot)
+  const size_t v = batch <= Q4NX_MAX_BATCH ? ws_need(n_tile_rows, 1, k_tiles, batch) : 0;
+  const size_t m = mfma_use(kind, batch) ? mfma_ws_bytes(kind, GOP_PLAIN, n_tile_rows, k_tiles, batch) : 0;
+  return v > m ? v : m;
 }
 
 int q4nx_gemv_q4(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
@@ -1093,9 +1121,11 @@ int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const
 }
 
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {
-  if (n_q_heads < 1 || n_kv_heads < 1 || k_tiles < 1 || batch < 1 || batch > Q4NX_MAX_BATCH)
-    return 0;
-  return ws_need(n_q_heads + 2 * n_kv_heads, 2, k_tiles, batch);
+  if (n_q_heads < 1 || n_kv_heads < 1 || k_tiles < 1 || batch < 1) return 0;
+  const int g = n_q_heads + 2 * n_kv_heads;
+  const size_t v = batch <= Q4NX_MAX_BATCH ? ws_need(g, 2, k_tiles, batch) : 0;
+  const size_t m = mfma_use(Q4NX_KIND_Q4, batch) ? mfma_ws_bytes(Q4NX_KIND_Q4, GOP_QKV, g, k_tiles, batch) : 0;
+  return v > m ? v : m;
 }
 
 int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n_q_heads,
@@ -1106,8 +1136,9 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
                   uint16_t* v_cache, int64_t kv_b_stride, int64_t kv_h_stride, float* raw_out,
                   uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
   const char* what = "q4nx_qkv_rope";
+  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, norm_w, ssq_in);
   for (const void* p : {(const void*)wq, (const void*)wk, (const void*)wv}) {
-    int rc = check_common(p, 2, k_tiles, batch, what);
+    int rc = check_common(p, 2, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
     if (rc) return rc;
   }
   Q4NX_REQUIRE(n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0, Q4NX_ERR_SHAPE,
@@ -1126,6 +1157,42 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
   Q4NX_REQUIRE(max_pos > 0 && kv_h_stride >= (int64_t)max_pos * 64 &&
                    kv_b_stride >= (int64_t)n_kv_heads * kv_h_stride,
                Q4NX_ERR_SHAPE, "%s: cache strides do not hold [n_kv][max_pos][64]", what);
+  if (mf) {
+    GemmArgs g{};
+    g.w[0] = wq;
+    g.w[1] = wk;
+    g.w[2] = wv;
+    g.n_tr[0] = n_q_heads * 2;
+    g.n_tr[1] = n_kv_heads * 2;
+    g.n_tr[2] = n_kv_heads * 2;
+    g.grp_q = n_q_heads;
+    g.grp_k = n_kv_heads;
+    g.k_t = k_tiles;
+    g.m_rows = batch;
+    if (norm_w) {
+      g.hres = (const float*)x;
+      g.norm_w = norm_w;
+      g.eps = eps;
+      g.ssq_in = ssq_in;
+      g.xn_out = xn_out;
+    } else {
+      g.x = (const uint16_t*)x;
+    }
+    g.x_stride = x_stride;
+    g.q_out = q_out;
+    g.k_cache = k_cache;
+    g.v_cache = v_cache;
+    g.kv_b_stride = kv_b_stride;
+    g.kv_h_stride = kv_h_stride;
+    g.pos = positions;
+    g.rope_tab = rope_tab;
+    g.max_pos = max_pos;
+    g.n_q_heads = n_q_heads;
+    g.n_kv_heads = n_kv_heads;
+    g.raw_out = raw_out;
+    return mfma_launch(Q4NX_KIND_Q4, GOP_QKV, g, n_q_heads + 2 * n_kv_heads, ws, ws_bytes,
+                       (hipStream_t)stream, what);
+  }
   GemvArgs a{};
   a.w[0] = wq;
   a.w[1] = wk;
@@ -1164,8 +1231,10 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
 }
 
 size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch) {
-  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1 || batch > Q4NX_MAX_BATCH) return 0;
-  return ws_need(n_tile_rows, 2, k_tiles, batch);
+  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1) return 0;
+  const size_t v = batch <= Q4NX_MAX_BATCH ? ws_need(n_tile_rows, 2, k_tiles, batch) : 0;
+  const size_t m = mfma_use(Q4NX_KIND_Q4, batch) ? mfma_ws_bytes(Q4NX_KIND_Q4, GOP_GATEUP, n_tile_rows, k_tiles, batch) : 0;
+  return v > m ? v : m;
 }
 
 int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, int k_tiles,
@@ -1173,8 +1242,9 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
                         const float* ssq_in, int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
                         uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
   const char* what = "q4nx_gate_up_swiglu";
+  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, norm_w, ssq_in);
   for (const void* p : {(const void*)wg, (const void*)wu}) {
-    int rc = check_common(p, n_tile_rows, k_tiles, batch, what);
+    int rc = check_common(p, n_tile_rows, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
     if (rc) return rc;
   }
   int rc = check_x(x, x_stride, k_tiles, what);
@@ -1187,6 +1257,30 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
                "%s: xn_out must be 16-byte aligned", what);
   Q4NX_REQUIRE(h_out != nullptr, Q4NX_ERR_ARG, "%s: h_out is required", what);
   Q4NX_REQUIRE(h_stride >= (int64_t)n_tile_rows * 32, Q4NX_ERR_SHAPE, "%s: bad h_stride", what);
+  if (mf) {
+    GemmArgs g{};
+    g.w[0] = wg;
+    g.w[1] = wu;
+    g.n_tr[0] = n_tile_rows;
+    g.n_tr[1] = n_tile_rows;
+    g.k_t = k_tiles;
+    g.m_rows = batch;
+    if (norm_w) {
+      g.hres = (const float*)x;
+      g.norm_w = norm_w;
+      g.eps = eps;
+      g.ssq_in = ssq_in;
+      g.xn_out = xn_out;
+    } else {
+      g.x = (const uint16_t*)x;
+    }
+    g.x_stride = x_stride;
+    g.h_out = h_out;
+    g.h_stride = h_stride;
+    g.raw_out = raw_out;
+    return mfma_launch(Q4NX_KIND_Q4, GOP_GATEUP, g, n_tile_rows, ws, ws_bytes,
+                       (hipStream_t)stream, what);
+  }
   GemvArgs a{};
   a.w[0] = wg;
   a.w[1] = wu;

@@ -93,7 +93,8 @@ def dequant(tiles: torch.Tensor, kind: str, n_tile_rows: int, k_tiles: int,
 def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
          residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
          ws: Workspace | None = None) -> torch.Tensor:
-    """y = residual + W @ x, fp32. x: bf16 [K] or [B, K] (B <= 8). Returns [N] or [B, N]."""
+    """y = residual + W @ x, fp32. x: bf16 [K] or [B, K]; B <= 8 on the VALU kernel, any B on
+    the matrix-core one (`set_mfma_rows` chooses). Returns [N] or [B, N]."""
     _tiles(tiles, kind, n_tile_rows, k_tiles)
     _dev(x, "x", torch.bfloat16)
     squeeze = x.dim() == 1
@@ -151,6 +152,11 @@ def gemm(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_ti
 def set_gemm_ksplit(parts: int) -> None:
     """Workgroups along K for `gemm` (0 = automatic)."""
     _lib.call("q4nx_set_gemm_ksplit", int(parts))
+
+
+def set_mfma_rows(kind: str, min_rows: int) -> None:
+    """Rows from which the GEMV / fused ops of `kind` run on the matrix cores (0 = never)."""
+    _lib.call("q4nx_set_mfma_rows", KIND[kind], int(min_rows))
 
 
 def _ssq(t, name, b, n):

@@ -46,8 +46,15 @@ def test_gemv_argument_errors():
     assert rc == ERR_ARG                                   # misaligned tiles
     rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 0, 10, 1, 2560, 256, None, None, 0, None)
     assert rc == ERR_SHAPE and "n_tile_rows" in msg
-    rc, msg = rc_msg("q4nx_gemv_q8", fake, fake, fake, 8, 4, 9, 1024, 256, None, None, 0, None)
+    _lib.lib().q4nx_set_mfma_rows(8, 0)                   # VALU kernel only: batch <= 8
+    try:
+        rc, msg = rc_msg("q4nx_gemv_q8", fake, fake, fake, 8, 4, 9, 1024, 256, None, None, 0,
+                         None)
+    finally:
+        _lib.lib().q4nx_set_mfma_rows(8, 1)
     assert rc == ERR_SHAPE and "batch" in msg
+    rc, msg = rc_msg("q4nx_set_mfma_rows", 5, 1)
+    assert rc == ERR_ARG
     rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 8, 10, 1, 2000, 256, None, None, 0, None)
     assert rc == ERR_SHAPE and "x_stride" in msg           # K = 2560 does not fit a 2000 row
     rc, msg = rc_msg("q4nx_gemv_ex", 5, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), None, 1,

@@ -57,7 +57,7 @@ def check_step(got, ref, token):
 @pytest.mark.parametrize("n_layers,batch,ctx,n_new,fused", [(2, 1, 256, 6, False),
                                                             (1, 3, 100, 3, False),
                                                             (2, 1, 200, 3, True)])
-def test_decode_steps_vs_oracle(dev, n_layers, batch, ctx, n_new, fused):
+def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new, fused):
     cfg = GraniteConfig(n_layers=n_layers)
     w = GraniteWeights.synthetic(cfg, seed=11, device=dev)
     dec = GraniteDecoder(w, max_batch=batch, max_len=ctx + n_new, device=dev, fused_tail=fused)
@@ -79,7 +79,7 @@ def test_decode_steps_vs_oracle(dev, n_layers, batch, ctx, n_new, fused):
 
 
 @pytest.mark.parametrize("fused", [False, True])
-def test_graph_equals_eager(dev, fused):
+def test_graph_equals_eager(dev, kpath, fused):
     """A graph replay computes bit-identical logits to the eager step."""
     cfg = GraniteConfig(n_layers=2)
     w = GraniteWeights.synthetic(cfg, seed=21, device=dev)

@@ -53,7 +53,7 @@ def test_dequant_bitexact(dev, kind, untile):
 
 
 @pytest.mark.parametrize("kind", ["q4", "q8"])
-def test_onehot_exact(dev, kind):
+def test_onehot_exact(dev, kpath, kind):
     n, k = 64, 1024
     raw, _ = _tiles(kind, n, k, 2)
     w = _dev_u8(raw, dev)
@@ -73,7 +73,7 @@ def test_onehot_exact(dev, kind):
     ("q8", 4096, 1024),
     ("q8", 2048, 2560),
 ])
-def test_gemv_parity(dev, kind, n, k):
+def test_gemv_parity(dev, kpath, kind, n, k):
     raw, rng = _tiles(kind, n, k, 3)
     x = synth.random_bf16(rng, k)
     y = ops.gemv(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
@@ -82,7 +82,7 @@ def test_gemv_parity(dev, kind, n, k):
     assert rel < REL and cos > COS, (rel, cos)
 
 
-def test_gemv_q8_lm_head_full(dev):
+def test_gemv_q8_lm_head_full(dev, kpath):
     """Config: y[248320] = W[248320, 1024] @ x, q8 tiles."""
     n, k = 248320, 1024
     raw, rng = _tiles("q8", n, k, 4)
@@ -95,7 +95,7 @@ def test_gemv_q8_lm_head_full(dev):
 
 @pytest.mark.parametrize("kind", ["q4", "q8"])
 @pytest.mark.parametrize("batch", [2, 3, 5, 8])
-def test_gemv_batch(dev, kind, batch):
+def test_gemv_batch(dev, kpath, kind, batch):
     n, k = 1024, 2560
     raw, rng = _tiles(kind, n, k, 5)
     x = synth.random_bf16(rng, (batch, k))
@@ -108,7 +108,7 @@ def test_gemv_batch(dev, kind, batch):
 
 @pytest.mark.parametrize("k,tiles_per_wave", [(2560, 1), (2560, 2), (2560, 4), (8192, 2), (8192, 4),
                                                 (1024, 4)])
-def test_gemv_tiles_per_wave(dev, k, tiles_per_wave):
+def test_gemv_tiles_per_wave(dev, valu, k, tiles_per_wave):
     """Every wave/tile decomposition gives the same answer, run after run."""
     n = 512
     raw, rng = _tiles("q4", n, k, 6)
@@ -130,7 +130,7 @@ def test_gemv_tiles_per_wave(dev, k, tiles_per_wave):
 @pytest.mark.parametrize("parts,batch,n,k", [(2, 1, 2560, 2560), (3, 3, 2560, 8192),
                                              (5, 1, 1024, 2560), (8, 8, 512, 8192),
                                              (0, 1, 2560, 8192), (0, 2, 2560, 2560)])
-def test_gemv_ksplit(dev, kind, parts, batch, n, k):
+def test_gemv_ksplit(dev, valu, kind, parts, batch, n, k):
     """K split over several workgroups per tile-row (last one adds the parts in order):
     same answer as the oracle, with a residual, bit-identical run after run."""
     raw, rng = _tiles(kind, n, k, 11)
@@ -152,7 +152,7 @@ def test_gemv_ksplit(dev, kind, parts, batch, n, k):
 
 
 @pytest.mark.parametrize("parts", [0, 1])
-def test_gemv_ex_norm_ssq_and_keys(dev, parts):
+def test_gemv_ex_norm_ssq_and_keys(dev, kpath, parts):
     """gemv_ex: RMSNorm prologue from an fp32 residual (with and without the producer's
     per-32 sums of squares), the sums of squares of its own output per tile-row, and
     argmax keys that decode_advance turns into the first maximal row."""
@@ -196,7 +196,7 @@ def test_gemv_ex_norm_ssq_and_keys(dev, parts):
     assert tok.cpu().numpy().tolist() == np.argmax(y, axis=1).tolist()
 
 
-def test_gemv_residual_and_ones(dev):
+def test_gemv_residual_and_ones(dev, kpath):
     n, k = 2560, 2560
     raw, rng = _tiles("q4", n, k, 7)
     w = _dev_u8(raw, dev)
@@ -210,7 +210,7 @@ def test_gemv_residual_and_ones(dev):
 
 
 @pytest.mark.parametrize("scale", [1e-30, 1e-3, 1e4, 1e30])
-def test_gemv_activation_range(dev, scale):
+def test_gemv_activation_range(dev, kpath, scale):
     """The per-workgroup power-of-two fp16 scaling keeps any bf16 range exact."""
     n, k = 256, 2560
     raw, rng = _tiles("q4", n, k, 8)

@@ -140,7 +140,7 @@ def ksplit(request):
 @pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (1, True, 0), (3, True, 0),
                                                (3, True, 1), (2, True, 8)],
                          indirect=["ksplit"])
-def test_qkv_rope(dev, batch, norm, ksplit):
+def test_qkv_rope(dev, valu, batch, norm, ksplit):
     rng = np.random.default_rng(13)
     hq, hkv, hid, lmax = 40, 8, 2560, 512
     kt = hid // 256
@@ -193,7 +193,7 @@ def test_qkv_rope(dev, batch, norm, ksplit):
 
 
 @pytest.mark.parametrize("batch,ksplit", [(1, 0), (3, 0), (2, 1)], indirect=["ksplit"])
-def test_qkv_rope_ssq_in(dev, batch, ksplit):
+def test_qkv_rope_ssq_in(dev, valu, batch, ksplit):
     """The norm fed the producer's per-32 sums of squares gives the same normalised input
     (to bf16 rounding) and GEMV outputs as the oracle on that input."""
     rng = np.random.default_rng(23)
@@ -226,7 +226,7 @@ def test_qkv_rope_ssq_in(dev, batch, ksplit):
 
 @pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (2, True, 0), (1, True, 2),
                                                (3, True, 5)], indirect=["ksplit"])
-def test_gate_up_swiglu(dev, batch, norm, ksplit):
+def test_gate_up_swiglu(dev, valu, batch, norm, ksplit):
     rng = np.random.default_rng(14)
     hid, inter = 2560, 8192
     kt = hid // 256
@@ -355,7 +355,7 @@ def test_embed_and_argmax(dev):
 # ------------------------------------------------------------------ fused layer tail
 
 @pytest.mark.parametrize("batch", [1, 3])
-def test_layer_tail_equals_chain(dev, batch):
+def test_layer_tail_equals_chain(dev, valu, batch):
     """o-proj -> RMSNorm/[gate,up,SwiGLU] -> down in one three-stage launch gives bit for bit
     what the three separate launches give with the same K splits (1, 2 and 4 parts with
     10-wave workgroups up to batch 2; 2, 3 and 4 with 8 waves above), and the chain
