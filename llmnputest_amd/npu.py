@@ -5,7 +5,7 @@ bytes), x (bf16) and y (fp32); `upload(i, ndarray)`, `run()`, `download(i, dtype
 `close()`, `meta`, and the `calls`/`seconds` counters -- but a "design" is a GEMV of the
 HIP library instead of an xclbin: the weights stay resident in HBM, `run()` launches the
 q4 or q8 GEMV and waits for it. `NpuLmHead` and `attach_lm_head` swap a torch lm_head for
-the GPU one with the same prefill fallback and counters (npu.py:117-163).
+the GPU one with the same counters (npu.py:117-163); prefill runs on the GPU too.
 """
 
 from __future__ import annotations
@@ -114,10 +114,12 @@ class NpuDesign:
 class NpuLmHead(torch.nn.Module):
     """The tied lm_head on the GPU (reference/npu.py:117-150).
 
-    Up to 8 rows (decode, or a small batch) run on the GPU GEMV; longer inputs (prefill)
-    use the torch fallback, as the reference does for anything but one row."""
-
-    MAX_ROWS = 8
+    The reference runs one row (decode) on the NPU and hands anything longer (prefill) to the
+    torch fallback (npu.py:136-139). Here every row count runs on the GPU: one row on the q8
+    contraction the design names, several rows (prefill) on the batched matrix-core
+    contraction over the same resident tile bytes. `npu_calls` counts GPU calls,
+    `prefill_calls` those with more than one row; `cpu_calls` counts fallback calls, which
+    happen only for an input with no rows. The fallback module is kept, as in the reference."""
 
     def __init__(self, fallback: torch.nn.Module, meta: dict | None = None, device=None):
         super().__init__()
@@ -126,6 +128,7 @@ class NpuLmHead(torch.nn.Module):
         self.n_rows = self.design.meta["n_rows"]
         self.k = self.design.meta["k"]
         self.npu_calls = 0
+        self.prefill_calls = 0
         self.cpu_calls = 0
 
     def load_weights(self, raw: bytes) -> None:
@@ -133,19 +136,20 @@ class NpuLmHead(torch.nn.Module):
 
     def forward(self, h: torch.Tensor) -> torch.Tensor:
         rows = h.shape[:-1].numel()
-        if rows > self.MAX_ROWS or rows == 0:
+        if rows == 0:
             self.cpu_calls += 1
             return self.fallback(h)
         t = time.perf_counter()
         d = self.design
         x = h.detach().to(torch.float32).reshape(rows, -1).to(torch.bfloat16).to(d.device)
-        y = ops.gemv(d.bos[0], d.meta["kind"], x, d.meta["tile_rows"], self.k // TILE_K)
+        y = ops.gemm(d.bos[0], d.meta["kind"], x, d.meta["tile_rows"], self.k // TILE_K)
         out = y.reshape(*h.shape[:-1], -1).to(h.device).to(h.dtype)
         if out.is_cuda:
             torch.cuda.current_stream(out.device).synchronize()
         d.seconds += time.perf_counter() - t
         d.calls += 1
         self.npu_calls += 1
+        self.prefill_calls += rows > 1
         return out
 
 
