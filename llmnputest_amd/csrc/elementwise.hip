@@ -187,12 +187,12 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
     const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
     int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
     int32_t* __restrict__ step, int history_len, int batch) {
-  __shared__ unsigned long long sk[16];
-  const int tid = threadIdx.x;
+  // wave w reduces rows w, w + 16, ...: a row's slots in lane-strided order, then the lanes
+  const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int s = step[0];
-  for (int b = 0; b < batch; ++b) {
+  for (int b = wave; b < batch; b += (int)(blockDim.x >> 6)) {
     unsigned long long k = 0ull;
-    for (int i = tid; i < n_slots; i += blockDim.x) {
+    for (int i = l; i < n_slots; i += 64) {
       const unsigned long long v = keys[(int64_t)b * n_slots + i];
       k = v > k ? v : k;
     }
@@ -201,10 +201,7 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
       const unsigned long long v = __shfl_xor(k, o);
       k = v > k ? v : k;
     }
-    if ((tid & 63) == 0) sk[tid >> 6] = k;
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < (int)(blockDim.x >> 6); ++w) k = sk[w] > k ? sk[w] : k;
+    if (l == 0) {
       const int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
       tokens[b] = tok;
       const int32_t p = pos[b] + 1;
@@ -212,8 +209,8 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
       lens[b] = p + 1;
       if (history != nullptr && s < history_len) history[(int64_t)s * batch + b] = tok;
     }
-    __syncthreads();
   }
+  __syncthreads();   // every wave has read step[0]
   if (tid == 0) step[0] = s + 1;
 }
 

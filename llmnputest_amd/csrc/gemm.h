@@ -20,7 +20,7 @@ struct GemmArgs {
   const float* hres;
   const uint16_t* norm_w;
   const float* ssq_in;
-  uint16_t* xn_out;      // optional [m][x_stride] copy of the normalised bf16 input
+  uint16_t* xn_out;      // optional [m][x_stride] normalised bf16 input (else in the workspace)
   float eps;
   int64_t x_stride;
   int m_rows, k_t;
@@ -52,6 +52,8 @@ struct GemmArgs {
 bool mfma_use(int kind, int rows);
 // workspace bytes of a launch of `n_units` tile-rows (PLAIN) or output groups (fused)
 size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows);
+// whether ws_bytes holds the normalised rows an RMSNorm prologue needs on this path
+bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes);
 // launches `a` (all but the split-K fields filled in); returns Q4NX_OK or an error code
 int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
                 hipStream_t st, const char* what);

@@ -91,24 +91,11 @@ __device__ __forceinline__ u32x4_t q8_operand(i32x2_t r) {
   return o;
 }
 
-// Row-wise 1/rms of the fp32 residual from its producer's sums of squares (one per 32
-// entries): lane (c, s) of a 16-lane column adds a quarter of row c's entries, the four
-// quarters meet through two lane exchanges.
-__device__ __forceinline__ float row_inv_rms(const float* ssq_row, int n_ss, int s, float K,
-                                             float eps) {
-  const int q = n_ss / 4;   // n_ss = K/32 = 8 k_tiles
-  float acc = 0.f;
-  for (int i = 0; i < q; ++i) acc += ssq_row[s * q + i];
-  acc += __shfl_xor(acc, 16);
-  acc += __shfl_xor(acc, 32);
-  return 1.0f / sqrtf(acc / K + eps);
-}
-
 // One workgroup of 4 waves owns RT tile-rows x (16 MT WM) rows of X over the K-tiles of its
 // part; WK waves split those K-tiles round-robin and WM = 4 / WK waves take different m-tiles.
 // Each wave stages one tile per tile-row at a time in its own LDS slot while the next tile's
 // bytes are in flight to registers.
-template <int KIND, int OP, bool NORM, int RT, int MT, int WK>
+template <int KIND, int OP, int RT, int MT, int WK>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   constexpr int WM = 4 / WK;
   constexpr int SLOT = GemmFmt<KIND>::kSlot;
@@ -153,20 +140,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   }
 
   const int c = l & 15, s = l >> 4;         // operand column / k-slot group
-  const int K = a.k_t * kTileK;
-  const uint16_t* xrow[MT];
-  const float* hrow[MT];
-  float inv_rms[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = min(m0 + 16 * mt + c, a.m_rows - 1);
-    if constexpr (NORM) {
-      hrow[mt] = a.hres + (int64_t)m * a.x_stride + 8 * s;
-      inv_rms[mt] = row_inv_rms(a.ssq_in + (int64_t)m * (K / 32), K / 32, s, (float)K, a.eps);
-    } else {
-      xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
-    }
-  }
   // ds_read_b64_tr_b8 row addresses: lane c of a 16-lane group addresses row (2j + h) with
   // j = c/2, h = c%2 -> k = 8s + j of row-block h (q4) or row half h (q8)
   const int tr_off = KIND == 4
@@ -201,6 +174,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         pf[r][i] = *(const u32x4_t*)(wr[r] + (size_t)(kbeg + wk) * TB + ld_off[i]);
   }
 
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(m0 + 16 * mt + c, a.m_rows - 1);
+    xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
+  }
   for (int it = 0; it < n_it; ++it) {
     const int kt = kbeg + wk + it * WK;
 #pragma unroll
@@ -210,23 +189,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     // activations of this tile first, then the next tile's weights: the in-order load
     // counter then lets the arithmetic start before the next tile arrives
     u32x4_t xa[8][MT];
-    float4 hx[NORM ? 8 : 1][MT][2];
-    u32x4_t nw[NORM ? 8 : 1];
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-      if constexpr (NORM) {
-        nw[kb] = *(const u32x4_t*)(a.norm_w + kt * 256 + kb * 32 + 8 * s);
+    for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          hx[kb][mt][0] = *(const float4*)(hrow[mt] + kt * 256 + kb * 32);
-          hx[kb][mt][1] = *(const float4*)(hrow[mt] + kt * 256 + kb * 32 + 4);
-        }
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
-      }
-    }
+      for (int mt = 0; mt < MT; ++mt) xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
     asm volatile("" ::: "memory");
     {  // the last iteration re-reads its own tile (an L2 hit) so the load count stays static
       const size_t off = (size_t)(it + 1 < n_it ? kt + WK : kt) * TB;
@@ -239,22 +205,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) {
-      if constexpr (NORM) {   // bf16((h * inv_rms) * w), as the GEMV prologue rounds it
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const float hv[8] = {hx[kb][mt][0].x, hx[kb][mt][0].y, hx[kb][mt][0].z, hx[kb][mt][0].w,
-                               hx[kb][mt][1].x, hx[kb][mt][1].y, hx[kb][mt][1].z, hx[kb][mt][1].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            xa[kb][mt][i] = pack_bf16x2((hv[2 * i] * inv_rms[mt]) * bf16lo(nw[kb][i]),
-                                        (hv[2 * i + 1] * inv_rms[mt]) * bf16hi(nw[kb][i]));
-          // the first output group's workgroups cover every (row, k) once
-          const int m = m0 + 16 * mt + c;
-          if (a.xn_out != nullptr && group == 0 && m < a.m_rows)
-            *(u32x4_t*)(a.xn_out + (int64_t)m * a.x_stride + kt * 256 + kb * 32 + 8 * s) =
-                xa[kb][mt];
-        }
-      }
       f32x4_t sx[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) sx[mt] = mfma_bf16(xa[kb][mt], ones, zero);
@@ -452,6 +402,54 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   }
 }
 
+// RMSNorm of the input rows into bf16, once per launch, before a contraction that needs it:
+// xn[m][k] = bf16((h[m][k] * r_m) * w[k]), r_m = 1/sqrt(sum(ssq[m]) / K + eps) with the sums
+// of squares added in the order of the VALU GEMV's prologue (lane l takes entries l, l+64,
+// l+128, l+192; the wave sums the lanes), so both kernel families see the same input.
+// granite_rmsnorm.h:45-80. One workgroup per row; K % 256 == 0, K / 32 <= 256.
+__global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h, int64_t h_stride,
+                                                    const float* __restrict__ ssq,
+                                                    const uint16_t* __restrict__ w, float eps,
+                                                    int K, uint16_t* __restrict__ xn,
+                                                    int64_t xn_stride) {
+  constexpr int kMaxChunks = 4;   // 8-entry chunks per thread: K <= 8192
+  const int m = blockIdx.x, tid = threadIdx.x, l = tid & 63;
+  const int n_ss = K / 32, n_ch = K / 8;
+  const float* hr = h + (int64_t)m * h_stride;
+  // the row and the weights are requested before the sums of squares are added up, so the
+  // kernel waits on memory once
+  float4 a0[kMaxChunks], a1[kMaxChunks];
+  uint4 wv[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int e = tid + 256 * i;
+    if (e < n_ch) {
+      a0[i] = *(const float4*)(hr + 8 * e);
+      a1[i] = *(const float4*)(hr + 8 * e + 4);
+      wv[i] = *(const uint4*)(w + 8 * e);
+    }
+  }
+  const float* srow = ssq + (int64_t)m * n_ss;
+  float part = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (l + 64 * j < n_ss) part += srow[l + 64 * j];
+  const float inv = 1.0f / sqrtf(wave_sum(part) / (float)K + eps);
+  uint16_t* xr = xn + (int64_t)m * xn_stride;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int e = tid + 256 * i;
+    if (e < n_ch) {
+      uint4 o;
+      o.x = pack_bf16x2((a0[i].x * inv) * bf16lo(wv[i].x), (a0[i].y * inv) * bf16hi(wv[i].x));
+      o.y = pack_bf16x2((a0[i].z * inv) * bf16lo(wv[i].y), (a0[i].w * inv) * bf16hi(wv[i].y));
+      o.z = pack_bf16x2((a1[i].x * inv) * bf16lo(wv[i].z), (a1[i].y * inv) * bf16hi(wv[i].z));
+      o.w = pack_bf16x2((a1[i].z * inv) * bf16lo(wv[i].w), (a1[i].w * inv) * bf16hi(wv[i].w));
+      *(uint4*)(xr + 8 * e) = o;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- host side
 
 struct GemmPlan {
@@ -461,28 +459,26 @@ struct GemmPlan {
 static int g_gemm_ksplit = 0;   // 0: automatic
 
 // Workgroup shape by row count: up to 16 rows the four waves split K; more rows go to more
-// waves and, past 64 (prefill), two m-tiles per wave. Fused epilogues and the RMSNorm
-// prologue keep one m-tile per wave (the prologue holds a tile of fp32 rows in registers).
+// waves and, past 32, two m-tiles per wave. Past 64 rows (prefill) a workgroup takes two
+// tile-rows, halving the x traffic (the fused epilogues always pair two tile-rows); q8 keeps
+// one so the staging stays under 64 KB of LDS.
 // n_units: tile-rows for PLAIN, output groups (of two tile-rows) for GATEUP and QKV.
-static GemmPlan plan_gemm(int kind, int op, bool norm, int n_units, int k_t, int m_rows) {
+static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows) {
   GemmPlan p{};
-  const bool one_mt = norm || op != GOP_PLAIN;
   if (m_rows <= 16) {
     p.mt = 1; p.wk = 4;
   } else if (m_rows <= 32) {
-    p.mt = one_mt ? 1 : 2; p.wk = one_mt ? 2 : 4;
+    p.mt = 2; p.wk = 4;
   } else if (m_rows <= 64) {
-    p.mt = one_mt ? 1 : 2; p.wk = one_mt ? 1 : 2;
+    p.mt = 2; p.wk = 2;
   } else {
-    p.mt = one_mt ? 1 : 2; p.wk = 1;
+    p.mt = 2; p.wk = 1;
   }
   if (op != GOP_PLAIN) {
     p.rt = 2;
     p.groups = n_units;
   } else {
-    // past 64 rows two tile-rows per workgroup halve the x traffic; q8 keeps one (LDS stays
-    // under 64 KB)
-    p.rt = (!one_mt && m_rows > 64 && kind == Q4NX_KIND_Q4 && n_units % 2 == 0) ? 2 : 1;
+    p.rt = (m_rows > 64 && kind == Q4NX_KIND_Q4 && n_units % 2 == 0) ? 2 : 1;
     p.groups = n_units / p.rt;
   }
   p.mb = 16 * p.mt * (4 / p.wk);
@@ -491,9 +487,9 @@ static GemmPlan plan_gemm(int kind, int op, bool norm, int n_units, int k_t, int
   int ks = 1;
   if (g_gemm_ksplit > 0) {
     ks = g_gemm_ksplit;
-  } else if (wgs < 192 && k_t >= 8) {
+  } else if (wgs < 192 && k_t >= 4) {
     ks = (240 + wgs - 1) / wgs;
-    const int cap = k_t / (2 * p.wk) > 0 ? k_t / (2 * p.wk) : 1;   // >= 2 tiles per wave
+    const int cap = k_t / 2;                 // >= 2 K-tiles per workgroup
     ks = ks < cap ? ks : cap;
   }
   ks = ks > 8 ? 8 : (ks < 1 ? 1 : ks);
@@ -503,36 +499,37 @@ static GemmPlan plan_gemm(int kind, int op, bool norm, int n_units, int k_t, int
   return p;
 }
 
-static size_t gemm_split_bytes(const GemmPlan& p) {
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// fp32 part records of a split-K launch (0 without a split or with too many counters)
+static size_t split_part_bytes(const GemmPlan& p) {
   const size_t cnt = (size_t)p.groups * p.m_blocks;
   if (p.ksplit <= 1 || cnt > Q4NX_WS_COUNTER_BYTES / 4) return 0;
-  return (size_t)Q4NX_WS_COUNTER_BYTES + cnt * p.ksplit * p.mb * p.rt * 32 * 4;
+  return cnt * p.ksplit * p.mb * p.rt * 32 * 4;
 }
 
-template <int KIND, int OP, bool NORM, int RT, int MT, int WK>
+// Workspace layout: arrival counters, the split-K part records, then (for an RMSNorm
+// prologue) the normalised bf16 rows.
+static size_t gemm_split_bytes(const GemmPlan& p) {
+  const size_t part = split_part_bytes(p);
+  return part ? Q4NX_WS_COUNTER_BYTES + align256(part) : 0;
+}
+
+template <int KIND, int OP, int RT, int MT, int WK>
 static void gemm_launch_t(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
   constexpr int lds = 4 * RT * GemmFmt<KIND>::kSlot;
   static_assert(4 * 16 * MT * RT * 32 * 4 <= lds, "reduction does not fit the staging slots");
   const dim3 grid((unsigned)(p.groups * p.ksplit), (unsigned)p.m_blocks);
-  hipLaunchKernelGGL((gemm_kernel<KIND, OP, NORM, RT, MT, WK>), grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((gemm_kernel<KIND, OP, RT, MT, WK>), grid, dim3(256), lds, st, a);
 }
 
-// one m-tile per wave: WK = 4, 2 or 1
-template <int KIND, int OP, bool NORM, int RT>
-static void gemm_launch_mt1(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
-  if (p.wk == 4) gemm_launch_t<KIND, OP, NORM, RT, 1, 4>(a, p, st);
-  else if (p.wk == 2) gemm_launch_t<KIND, OP, NORM, RT, 1, 2>(a, p, st);
-  else gemm_launch_t<KIND, OP, NORM, RT, 1, 1>(a, p, st);
-}
-
-template <int KIND>
-static void gemm_launch_plain(const GemmArgs& a, const GemmPlan& p, bool norm, hipStream_t st) {
-  if (norm) gemm_launch_mt1<KIND, GOP_PLAIN, true, 1>(a, p, st);
-  else if (p.mt == 1) gemm_launch_t<KIND, GOP_PLAIN, false, 1, 1, 4>(a, p, st);
-  else if (p.wk == 4) gemm_launch_t<KIND, GOP_PLAIN, false, 1, 2, 4>(a, p, st);
-  else if (p.wk == 2) gemm_launch_t<KIND, GOP_PLAIN, false, 1, 2, 2>(a, p, st);
-  else if (p.rt == 2) gemm_launch_t<KIND, GOP_PLAIN, false, 2, 2, 1>(a, p, st);
-  else gemm_launch_t<KIND, GOP_PLAIN, false, 1, 2, 1>(a, p, st);
+template <int KIND, int OP>
+static void gemm_launch_op(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
+  if (p.mt == 1) gemm_launch_t<KIND, OP, (OP == GOP_PLAIN ? 1 : 2), 1, 4>(a, p, st);
+  else if (p.wk == 4) gemm_launch_t<KIND, OP, (OP == GOP_PLAIN ? 1 : 2), 2, 4>(a, p, st);
+  else if (p.wk == 2) gemm_launch_t<KIND, OP, (OP == GOP_PLAIN ? 1 : 2), 2, 2>(a, p, st);
+  else if (OP != GOP_PLAIN || p.rt == 2) gemm_launch_t<KIND, OP, 2, 2, 1>(a, p, st);
+  else if constexpr (OP == GOP_PLAIN) gemm_launch_t<KIND, OP, 1, 2, 1>(a, p, st);
 }
 
 // Rows from which the GEMV entry points run on the matrix cores, per kind (0: never).
@@ -545,44 +542,65 @@ bool mfma_use(int kind, int rows) {
 }
 
 size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows) {
-  // the larger of the two prologue variants, so one query serves both
-  const size_t a = gemm_split_bytes(plan_gemm(kind, op, false, n_units, k_t, m_rows));
-  const size_t b = gemm_split_bytes(plan_gemm(kind, op, true, n_units, k_t, m_rows));
-  return a > b ? a : b;
+  // room for the split-K records and for the normalised rows of an RMSNorm prologue
+  const size_t split = split_part_bytes(plan_gemm(kind, op, n_units, k_t, m_rows));
+  return Q4NX_WS_COUNTER_BYTES + align256(split) + align256((size_t)m_rows * k_t * kTileK * 2);
+}
+
+bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes) {
+  return ws_bytes >= Q4NX_WS_COUNTER_BYTES + align256((size_t)m_rows * k_t * kTileK * 2);
 }
 
 // Launches the contraction described by `a` (weights, input, epilogue fields filled in);
-// sets the split-K fields from the plan and the workspace.
+// sets the split-K fields from the plan and the workspace. With norm_w set, the rows are
+// normalised once into xn_out (when given) or the workspace, then contracted as bf16.
 int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
                 hipStream_t st, const char* what) {
-  const bool norm = a.norm_w != nullptr;
-  Q4NX_REQUIRE(!norm || a.ssq_in != nullptr, Q4NX_ERR_ARG,
-               "%s: with norm_w and %d rows the sums of squares ssq_in are required", what,
-               a.m_rows);
   Q4NX_REQUIRE(op == GOP_PLAIN || kind == Q4NX_KIND_Q4, Q4NX_ERR_ARG,
                "%s: fused epilogues take q4 tiles", what);
-  GemmPlan p = plan_gemm(kind, op, norm, n_units, a.k_t, a.m_rows);
-  const size_t need = gemm_split_bytes(p);
-  if (p.ksplit > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256))) {
-    p.ksplit = 1;   // no (or too small a) workspace: whole K per workgroup
+  const int K = a.k_t * kTileK;
+  GemmPlan p = plan_gemm(kind, op, n_units, a.k_t, a.m_rows);
+  size_t split = split_part_bytes(p);
+  const size_t xn_b = a.norm_w != nullptr && a.xn_out == nullptr
+                          ? align256((size_t)a.m_rows * K * 2) : 0;
+  const bool ws_ok = ws != nullptr && Q4NX_ALIGNED(ws, 256);
+  if (split && (!ws_ok || ws_bytes < Q4NX_WS_COUNTER_BYTES + align256(split) + xn_b)) {
+    split = 0;   // no (or too small a) workspace: whole K per workgroup
+    p.ksplit = 1;
     p.kpp = a.k_t;
+  }
+  if (a.norm_w != nullptr) {
+    Q4NX_REQUIRE(a.ssq_in != nullptr, Q4NX_ERR_ARG,
+                 "%s: the matrix-core RMSNorm prologue needs the sums of squares ssq_in", what);
+    Q4NX_REQUIRE(K / 32 <= 256, Q4NX_ERR_SHAPE, "%s: RMSNorm prologue supports K <= 8192", what);
+    uint16_t* xn = a.xn_out;
+    int64_t xs = a.x_stride;
+    if (xn == nullptr) {
+      Q4NX_REQUIRE(ws_ok && ws_bytes >= Q4NX_WS_COUNTER_BYTES + align256(split) + xn_b,
+                   Q4NX_ERR_WS, "%s: workspace of %zu bytes needed for the normalised rows",
+                   what, (size_t)(Q4NX_WS_COUNTER_BYTES + align256(split) + xn_b));
+      xn = (uint16_t*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES + align256(split));
+      xs = K;
+    }
+    hipLaunchKernelGGL(xnorm_kernel, dim3(a.m_rows), dim3(256), 0, st, a.hres, a.x_stride,
+                       a.ssq_in, a.norm_w, a.eps, K, xn, xs);
+    a.x = xn;
+    a.x_stride = xs;
   }
   a.ksplit = p.ksplit;
   a.kpp = p.kpp;
   if (p.ksplit > 1) {
     a.counters = (unsigned*)ws;
     a.part = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
-    a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
+    a.part_bytes = (uint32_t)split;
   }
   if (op == GOP_PLAIN) {
-    if (kind == Q4NX_KIND_Q4) gemm_launch_plain<4>(a, p, norm, st);
-    else gemm_launch_plain<8>(a, p, norm, st);
+    if (kind == Q4NX_KIND_Q4) gemm_launch_op<4, GOP_PLAIN>(a, p, st);
+    else gemm_launch_op<8, GOP_PLAIN>(a, p, st);
   } else if (op == GOP_GATEUP) {
-    if (norm) gemm_launch_mt1<4, GOP_GATEUP, true, 2>(a, p, st);
-    else gemm_launch_mt1<4, GOP_GATEUP, false, 2>(a, p, st);
+    gemm_launch_op<4, GOP_GATEUP>(a, p, st);
   } else {
-    if (norm) gemm_launch_mt1<4, GOP_QKV, true, 2>(a, p, st);
-    else gemm_launch_mt1<4, GOP_QKV, false, 2>(a, p, st);
+    gemm_launch_op<4, GOP_QKV>(a, p, st);
   }
   return check_launch(what);
 }
@@ -604,7 +622,7 @@ size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows) {
   if ((kind != Q4NX_KIND_Q4 && kind != Q4NX_KIND_Q8) || n_tile_rows < 1 || k_tiles < 1 ||
       m_rows < 1)
     return 0;
-  return gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, false, n_tile_rows, k_tiles, m_rows));
+  return gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, n_tile_rows, k_tiles, m_rows));
 }
 
 int q4nx_set_mfma_rows(int kind, int min_rows) {

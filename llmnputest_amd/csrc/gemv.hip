@@ -988,11 +988,14 @@ static int check_ssq_in(const float* ssq_in, const uint16_t* norm_w, int k_tiles
 }
 
 // Whether a launch of `batch` rows goes to the matrix-core kernels (gemm.hip): the policy
-// of q4nx_set_mfma_rows, and only for what they implement (the RMSNorm prologue there takes
-// the producer's sums of squares).
-static bool take_mfma(int kind, int batch, const uint16_t* norm_w, const float* ssq_in) {
+// of q4nx_set_mfma_rows, and only for what they implement (an RMSNorm prologue there takes
+// the producer's sums of squares, and room for the normalised rows in xn_out or the
+// workspace).
+static bool take_mfma(int kind, int batch, int k_tiles, const uint16_t* norm_w,
+                      const float* ssq_in, const void* xn_out, size_t ws_bytes) {
   if (!mfma_use(kind, batch)) return false;
-  return norm_w == nullptr || ssq_in != nullptr;
+  if (norm_w == nullptr) return true;
+  return ssq_in != nullptr && (xn_out != nullptr || mfma_norm_fits(k_tiles, batch, ws_bytes));
 }
 
 static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t* norm_w,
@@ -1000,7 +1003,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
                       int batch, int64_t x_stride, int64_t y_stride, const float* residual,
                       float* ssq_out, unsigned long long* argmax_keys, void* stream,
                       const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
-  const bool mf = take_mfma(kind, batch, norm_w, ssq_in);
+  const bool mf = take_mfma(kind, batch, k_tiles, norm_w, ssq_in, nullptr, ws ? ws_bytes : 0);
   int rc = check_common(w, n_tile_rows, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
   if (rc) return rc;
   rc = check_x(x, x_stride, k_tiles, what);
@@ -1136,7 +1139,7 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
                   uint16_t* v_cache, int64_t kv_b_stride, int64_t kv_h_stride, float* raw_out,
                   uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
   const char* what = "q4nx_qkv_rope";
-  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, norm_w, ssq_in);
+  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, k_tiles, norm_w, ssq_in, xn_out, ws ? ws_bytes : 0);
   for (const void* p : {(const void*)wq, (const void*)wk, (const void*)wv}) {
     int rc = check_common(p, 2, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
     if (rc) return rc;
@@ -1242,7 +1245,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
                         const float* ssq_in, int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
                         uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
   const char* what = "q4nx_gate_up_swiglu";
-  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, norm_w, ssq_in);
+  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, k_tiles, norm_w, ssq_in, xn_out, ws ? ws_bytes : 0);
   for (const void* p : {(const void*)wg, (const void*)wu}) {
     int rc = check_common(p, n_tile_rows, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
     if (rc) return rc;

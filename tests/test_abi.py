@@ -109,9 +109,19 @@ def test_ws_queries():
     # 80 tile-rows do not fill the GPU: K is split 3 ways, partials [80][3][1][32] fp32
     assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1) == 65536 + 80 * 3 * 32 * 4
     assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 1) == 0      # enough tile-rows: no split
-    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9) == 0      # batch out of range
-    # 56 heads of 2 tile-rows: 5 parts of 2 K-tiles, [56][5][batch 2][64]
-    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2) == 65536 + 56 * 5 * 2 * 64 * 4
+    # batch 9 runs on the matrix cores: no split, room for 9 normalised rows
+    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9) == 65536 + 9 * 2560 * 2
+    # 56 heads of 2 tile-rows, batch 2 on the VALU kernel: 5 parts of 2 K-tiles,
+    # [56][5][batch 2][64]; on the matrix cores (the default from 2 rows): 5 parts of
+    # [16 rows][64] per head, then room for 2 normalised rows of 2560 bf16
+    lib.q4nx_set_mfma_rows(4, 0)
+    try:
+        assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2) == 65536 + 56 * 5 * 2 * 64 * 4
+    finally:
+        lib.q4nx_set_mfma_rows(4, 2)
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2) == 65536 + 56 * 5 * 16 * 64 * 4 + 2 * 2560 * 2
+    # q8 lm_head at one row (matrix cores): 3136 workgroups, no split, one normalised row
+    assert lib.q4nx_gemv_ws_bytes(8, 3136, 10, 1) == 65536 + 2560 * 2
     assert lib.q4nx_gate_up_ws_bytes(256, 10, 1) == 0
     assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64) == 0  # one split: no workspace
     big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768)    # 64 splits of (acc[64], m, l, pad)
