@@ -187,21 +187,37 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
     const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
     int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
     int32_t* __restrict__ step, int history_len, int batch) {
-  // wave w reduces rows w, w + 16, ...: a row's slots in lane-strided order, then the lanes
+  // Rows are taken `groups` at a time, `wpr` waves per row; each lane keeps eight key loads
+  // in flight, then the lanes and the row's waves combine (max is order-independent).
+  __shared__ unsigned long long sk[16];
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+  const int n_waves = (int)(blockDim.x >> 6);
+  const int wpr = batch >= n_waves ? 1 : n_waves / batch;
+  const int groups = n_waves / wpr;
   const int s = step[0];
-  for (int b = wave; b < batch; b += (int)(blockDim.x >> 6)) {
+  for (int b0 = 0; b0 < batch; b0 += groups) {
+    const int b = b0 + wave / wpr, sub = wave % wpr;
     unsigned long long k = 0ull;
-    for (int i = l; i < n_slots; i += 64) {
-      const unsigned long long v = keys[(int64_t)b * n_slots + i];
-      k = v > k ? v : k;
-    }
+    if (wave < groups * wpr && b < batch) {
+      const int T = wpr * 64;
+      const unsigned long long* row = keys + (int64_t)b * n_slots;
+      for (int i = sub * 64 + l; i < n_slots; i += 8 * T) {
+        unsigned long long v[8];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const unsigned long long v = __shfl_xor(k, o);
-      k = v > k ? v : k;
+        for (int j = 0; j < 8; ++j) v[j] = i + j * T < n_slots ? row[i + j * T] : 0ull;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) k = v[j] > k ? v[j] : k;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long v = __shfl_xor(k, o);
+        k = v > k ? v : k;
+      }
     }
-    if (l == 0) {
+    if (l == 0) sk[wave] = k;
+    __syncthreads();
+    if (l == 0 && sub == 0 && wave < groups * wpr && b < batch) {
+      for (int w = 1; w < wpr; ++w) k = sk[wave + w] > k ? sk[wave + w] : k;
       const int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
       tokens[b] = tok;
       const int32_t p = pos[b] + 1;
@@ -209,8 +225,8 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
       lens[b] = p + 1;
       if (history != nullptr && s < history_len) history[(int64_t)s * batch + b] = tok;
     }
+    __syncthreads();
   }
-  __syncthreads();   // every wave has read step[0]
   if (tid == 0) step[0] = s + 1;
 }
 
