@@ -50,14 +50,13 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ 
                                                    const int32_t* __restrict__ pos,
                                                    const float* __restrict__ tab, int max_pos) {
   const int half = hd >> 1;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, h, d<half)
-  const int64_t total = (int64_t)batch * n_heads * half;
-  if (i >= total) return;
-  const int d = (int)(i % half);
-  const int64_t bh = i / half;
-  const int b = (int)(bh / n_heads);
+  const int i = blockIdx.x * 256 + threadIdx.x;  // (b, h, d < half); the host keeps it < 2^31
+  if (i >= batch * n_heads * half) return;
+  const int bh = i / half;
+  const int d = i - bh * half;
+  const int b = bh / n_heads;
   const int p = pos[b];
-  const int64_t base = bh * hd;
+  const int64_t base = (int64_t)bh * hd;
   const float x0 = bf16_to_f32(x[base + d]);
   const float x1 = bf16_to_f32(x[base + half + d]);
   float y0, y1;
@@ -257,6 +256,8 @@ int q4nx_rope(const uint16_t* x, uint16_t* y, float* y_f32, int n_heads, int hea
                Q4NX_ERR_SHAPE, "q4nx_rope: n_heads=%d head_dim=%d batch=%d max_pos=%d", n_heads,
                head_dim, batch, max_pos);
   const int64_t total = (int64_t)batch * n_heads * (head_dim / 2);
+  Q4NX_REQUIRE(total < ((int64_t)1 << 31) - 256, Q4NX_ERR_SHAPE,
+               "q4nx_rope: %lld rotation pairs exceed one launch", (long long)total);
   hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, x, y, y_f32, n_heads, head_dim, batch, positions, tab,
                      max_pos);
