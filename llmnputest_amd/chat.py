@@ -8,6 +8,13 @@ decoded on the device and the reference's report line is printed.
 
     python -m llmnputest_amd.chat [--layers 40] [--ctx 2048] [--new 128] [--batch 1]
     python -m llmnputest_amd.chat --q4nx model.q4nx ...     # a real granite q4nx file
+    python -m llmnputest_amd.chat --hf-tiny                 # chat.py's own flow (below)
+
+`--hf-tiny` runs chat.py's flow itself (chat.py:36-42, 80-94): a transformers causal LM whose
+lm_head is swapped for the GPU one with `attach_lm_head` and a .q4nx file, greedy `generate`
+with the rest of the model in torch on the CPU, and the report line with the head's share
+of the wall time. Without model files the model is a small random Qwen3 and its lm_head is
+written as q8 tiles by `synth.quantize_q8`.
 """
 
 from __future__ import annotations
@@ -22,6 +29,42 @@ import torch
 MAX_NEW = 128   # chat.py:22
 
 
+def hf_tiny(new_tokens: int, seed: int) -> int:
+    import tempfile
+
+    import transformers
+
+    from . import npu, q4nx, synth
+
+    t0 = time.time()
+    cfg = transformers.Qwen3Config(vocab_size=32768, hidden_size=1024, intermediate_size=3072,
+                                   num_hidden_layers=4, num_attention_heads=16,
+                                   num_key_value_heads=8, head_dim=64, tie_word_embeddings=True,
+                                   max_position_embeddings=1024)
+    torch.manual_seed(seed)
+    model = transformers.Qwen3ForCausalLM(cfg).eval()
+    with tempfile.TemporaryDirectory() as d:
+        path = f"{d}/model.q4nx"
+        q4nx.write_q4nx(path, {"lm_head.weight": (
+            "q8", synth.quantize_q8(model.lm_head.weight.detach().float().numpy()))})
+        head = npu.attach_lm_head(model, q4nx.Q4NX(path))
+    print(f"gpu      lm_head on the gpu, {head.n_rows} x {head.k}, q8 tiles "
+          f"(random Qwen3, {cfg.num_hidden_layers} layers, in torch on the cpu)")
+    print(f"ready    {time.time() - t0:.1f}s\n")
+    ids = torch.from_numpy(np.random.default_rng(seed).integers(0, cfg.vocab_size, (1, 16)))
+    head.design.seconds = head.design.calls = head.npu_calls = 0
+    t = time.time()
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=new_tokens, do_sample=False, pad_token_id=0)
+    dt = time.time() - t
+    new = out[0, ids.shape[-1]:]
+    print(" ".join(str(int(x)) for x in new))
+    per = head.design.seconds / max(head.design.calls, 1) * 1e3
+    print(f"\n[{len(new)} tokens, {dt:.1f}s, {len(new) / dt:.2f} tok/s; lm_head on gpu "
+          f"{head.npu_calls}x at {per:.1f} ms, {100 * head.design.seconds / dt:.0f}% of wall]\n")
+    return 0
+
+
 def main(argv: list[str]) -> int:
     from .granite import GraniteConfig, GraniteDecoder, GraniteWeights
 
@@ -32,8 +75,12 @@ def main(argv: list[str]) -> int:
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--q4nx", default=None, help="load weights from a granite .q4nx file")
+    ap.add_argument("--hf-tiny", action="store_true",
+                    help="transformers generate with the GPU lm_head (chat.py's flow)")
     ap.add_argument("prompt_ids", nargs="*", type=int)
     a = ap.parse_args(argv[1:])
+    if a.hf_tiny:
+        return hf_tiny(a.new, a.seed)
 
     t0 = time.time()
     cfg = GraniteConfig(n_layers=a.layers)

@@ -98,3 +98,27 @@ def pack_q4_tile(codes_rk: np.ndarray, d_rk: np.ndarray, m_rk: np.ndarray) -> np
                 nib[i >> 1] |= c
     tile[1024:] = nib
     return tile
+
+
+def quantize_q8(w: np.ndarray) -> np.ndarray:
+    """q8 tiles of a float matrix [N, K]: per row and 32-K group s = bf16(max|w| / 127) and
+    code = clip(round(w / s), -127, 127), so that code * s -- the q8 dequantisation of
+    tools/q4nx.py:140-143 -- is within s/2 of w. FastFlowLM wrote the reference's files; this
+    writes the same layout from any weights (a small transformers model's lm_head in the
+    tests). Returns uint8[N/32, K/256, 8704]."""
+    w = np.asarray(w, np.float32)
+    n, k = w.shape
+    tr, kt = tiled_shape(n, k)
+    grp = w.reshape(n, k // 32, 32)
+    s_bits = f32_to_bf16_bits(np.abs(grp).max(-1) / np.float32(127.0))      # [n, k/32]
+    s = bf16_bits_to_f32(s_bits)
+    safe = np.where(s > 0, s, np.float32(1.0))[..., None]
+    codes = np.clip(np.rint(grp / safe), -127, 127).astype(np.int8).reshape(n, k)
+    # weight index i = rb*4096 + kk*16 + r of tile (tr, kt): order [tr, kt, rb, kk, r]
+    cod = codes.reshape(tr, 2, 16, kt, 256).transpose(0, 3, 1, 4, 2).reshape(tr, kt, 8192)
+    # metadata index g = kb*32 + rb*16 + r: order [tr, kt, kb, rb, r]
+    meta = s_bits.reshape(tr, 2, 16, kt, 8).transpose(0, 3, 4, 1, 2).reshape(tr, kt, 256)
+    out = np.empty((tr, kt, Q8_TILE_BYTES), np.uint8)
+    out[..., :512] = np.ascontiguousarray(meta).view(np.uint8)
+    out[..., 512:] = np.ascontiguousarray(cod).view(np.uint8)
+    return out

@@ -64,3 +64,24 @@ def test_design_meta():
         npu._meta_for("no_such_design", None)
     with pytest.raises(ValueError):
         npu._meta_for("x", {"kind": "q4", "n_rows": 100, "k": 256})
+
+
+def test_quantize_q8_roundtrip():
+    """quantize_q8 writes the q8 tile layout: the oracle's dequantisation of its tiles is the
+    input to within half a scale step, element by element, and a tile's brute-force natural
+    view agrees."""
+    from oracle import q4nx_oracle as qo
+    rng = np.random.default_rng(5)
+    n, k = 96, 512
+    w = (rng.standard_normal((n, k)) * rng.uniform(0.01, 2.0, (n, 1))).astype(np.float32)
+    w[3, 40:72] = 0.0                                   # an all-zero group
+    t = synth.quantize_q8(w)
+    assert t.shape == (n // 32, k // 256, 8704)
+    deq = qo.dequant_matrix(t.reshape(-1, 8704), "q8", n // 32, k // 256)
+    s = qo.bf16_to_f32(synth.f32_to_bf16_bits(
+        np.abs(w.reshape(n, -1, 32)).max(-1) / np.float32(127.0)))
+    step = np.repeat(s, 32, axis=1)
+    assert (np.abs(deq - w) <= step * 0.5 + 1e-7 + step * 0.01).all()
+    assert (deq[3, 40:72] == 0).all()
+    nat = qo.dequant_tile_bruteforce(t[1, 1], "q8")
+    assert np.array_equal(nat, deq[32:64, 256:512])
