@@ -185,12 +185,21 @@ def secondary_bench(dev) -> dict:
     t = _graph_time(lambda: [ops.gemv(w, "q8", x, n // 32, k // 256, out=y) for w in ws], 10) / 2
     b = ws[0].numel() + 2 * k + 4 * n
     out["lm_head_q8_248320x1024"] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
-    del ws
+    # the same lm_head over a 512-row prefill block (the rows the reference hands to torch)
+    xp = torch.randn(512, k, device=dev, generator=gen).to(torch.bfloat16)
+    yp = torch.empty(512, n, dtype=torch.float32, device=dev)
+    wsg = ops.Workspace(1 << 20, device=dev)
+    t = _graph_time(lambda: ops.gemm(ws[0], "q8", xp, n // 32, k // 256, out=yp, ws=wsg), 5)
+    fl = 2.0 * 512 * n * k
+    out["lm_head_q8_248320x1024_prefill_m512"] = {"us": round(t * 1e6, 1),
+                                                  "TFLOP/s": round(fl / t / 1e12, 1)}
+    del ws, xp, yp
     # MLP: [gate, up, SwiGLU] then down, 8 layers rotated (315 MB), batch 1 and 8
     layers = [(random_q4_tiles(INTER, HIDDEN, gen, dev), random_q4_tiles(INTER, HIDDEN, gen, dev),
                random_q4_tiles(HIDDEN, INTER, gen, dev)) for _ in range(8)]
     wsp = ops.Workspace(8 << 20, device=dev)
-    for bb in (1, 8):
+    # batch 8 runs on the matrix cores by default; "_valu" pins the VALU GEMV for comparison
+    for bb, path in ((1, ""), (8, ""), (8, "_valu")):
         xb = torch.randn(bb, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
         hb = torch.empty(bb, INTER, dtype=torch.bfloat16, device=dev)
         yb = torch.empty(bb, HIDDEN, dtype=torch.float32, device=dev)
@@ -199,10 +208,27 @@ def secondary_bench(dev) -> dict:
             for g_, u_, d_ in layers:
                 ops.gate_up_swiglu(g_, u_, INTER // 32, HIDDEN // 256, xb, h_out=hb, ws=wsp)
                 ops.gemv(d_, "q4", hb, HIDDEN // 32, INTER // 256, out=yb, ws=wsp)
-        t = _graph_time(mlp, 10) / len(layers)
+        if path:
+            ops.set_mfma_rows("q4", 0)
+        try:
+            t = _graph_time(mlp, 10) / len(layers)
+        finally:
+            ops.set_mfma_rows("q4", 2)
         byt = 3 * q4_bytes(INTER, HIDDEN) + bb * (2 * HIDDEN + 2 * INTER * 2 + 4 * HIDDEN)
-        out[f"mlp_gate_up_swiglu_down_b{bb}"] = {"us": round(t * 1e6, 2),
-                                                 "GB/s": round(byt / t / 1e9, 1)}
+        out[f"mlp_gate_up_swiglu_down_b{bb}{path}"] = {"us": round(t * 1e6, 2),
+                                                       "GB/s": round(byt / t / 1e9, 1)}
+    # prefill: the batched contraction over 2048 rows (gate 2560->8192, down 8192->2560)
+    for name, (n_, k_) in (("gate_2560x8192", (INTER, HIDDEN)), ("down_8192x2560", (HIDDEN, INTER))):
+        m_ = 2048
+        xp = torch.randn(m_, k_, device=dev, generator=gen).to(torch.bfloat16)
+        yp = torch.empty(m_, n_, dtype=torch.float32, device=dev)
+        wl = [L[0] if n_ == INTER else L[2] for L in layers[:4]]
+        t = _graph_time(lambda: [ops.gemm(w_, "q4", xp, n_ // 32, k_ // 256, out=yp, ws=wsp)
+                                 for w_ in wl], 5) / len(wl)
+        fl = 2.0 * m_ * n_ * k_
+        out[f"prefill_q4_{name}_m{m_}"] = {"us": round(t * 1e6, 1),
+                                           "TFLOP/s": round(fl / t / 1e12, 1),
+                                           "frac_of_bf16_mfma_peak": round(fl / t / 2.5e15, 4)}
     del layers
     # RoPE on q [B,40,64] and k [B,8,64]
     tab = ops.rope_table(4096, 64, 10000.0, device=dev)
@@ -239,38 +265,44 @@ def secondary_bench(dev) -> dict:
     return out
 
 
-def decode_bytes_per_token(cfg: GraniteConfig, ctx: int, n_new: int) -> float:
+def decode_bytes_per_token(cfg: GraniteConfig, ctx: int, n_new: int, batch: int = 1) -> float:
     """Algorithmic HBM bytes of one decode step, averaged over the generated positions:
-    every weight tile once, the K/V cache up to the current position (read) plus one
-    appended row, norm weights, the embedding row and the logits."""
+    every weight tile once, and per sequence the K/V cache up to the current position (read)
+    plus one appended row, the embedding row and the logits; norm weights once."""
     mean_len = ctx + (n_new + 1) / 2.0
     kv = cfg.n_layers * cfg.n_kv * cfg.head_dim * 2 * 2 * (mean_len + 1)
     norms = (2 * cfg.n_layers + 1) * cfg.hidden * 2
-    return (cfg.n_layers * cfg.layer_bytes() + cfg.lm_head_bytes() + kv + norms
-            + cfg.hidden * 4 + cfg.vocab * 4)
+    return (cfg.n_layers * cfg.layer_bytes() + cfg.lm_head_bytes() + norms
+            + batch * (kv + cfg.hidden * 4 + cfg.vocab * 4))
 
 
-def decode_bench(ctx: int, n_new: int, dev, cpu_tokens: int) -> dict:
+def decode_bench(ctx: int, n_new: int, dev, cpu_tokens: int, batch: int = 1,
+                 w: GraniteWeights | None = None) -> dict:
+    """Greedy decode of n_new tokens for `batch` sequences at context ctx, timed with events
+    around the device token loop. Bytes per step: the weights once plus every sequence's
+    K/V cache."""
     cfg = GraniteConfig()
-    w = GraniteWeights.synthetic(cfg, seed=5, device=dev)
-    dec = GraniteDecoder(w, max_batch=1, max_len=ctx + n_new, device=dev)
+    if w is None:
+        w = GraniteWeights.synthetic(cfg, seed=5, device=dev)
+    dec = GraniteDecoder(w, max_batch=batch, max_len=ctx + n_new, device=dev)
     dec.seed_cache(ctx, seed=6)
-    first = int(np.random.default_rng(7).integers(0, cfg.vocab))
-    dec.generate([first], [ctx], 4)                     # capture + warm
+    first = np.random.default_rng(7).integers(0, cfg.vocab, batch).tolist()
+    dec.generate(first, [ctx] * batch, 4)               # capture + warm
     dec.seed_cache(ctx, seed=6)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    toks, _ = dec.generate([first], [ctx], n_new)
+    toks, _ = dec.generate(first, [ctx] * batch, n_new)
     e1.record()
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) / 1e3
-    bpt = decode_bytes_per_token(cfg, ctx, n_new)
-    out = {"tok_s": n_new / sec, "ms_per_token": sec / n_new * 1e3,
-           "bytes_per_token": int(bpt), "gbs": bpt * n_new / sec / 1e9, "ctx": ctx,
-           "new_tokens": n_new}
-    if cpu_tokens > 0:
-        out["cpu"] = decode_cpu_baseline(w, dec, first, ctx, toks[0], cpu_tokens)
+    step_bytes = decode_bytes_per_token(cfg, ctx, n_new, batch)
+    out = {"tok_s": batch * n_new / sec, "ms_per_token": sec / n_new * 1e3,
+           "bytes_per_token": int(step_bytes), "gbs": step_bytes * n_new / sec / 1e9, "ctx": ctx,
+           "new_tokens": n_new, "batch": batch, "weights": w}
+    if cpu_tokens > 0 and batch == 1:
+        out["cpu"] = decode_cpu_baseline(w, dec, first[0], ctx, toks[0], cpu_tokens)
+    del dec
     return out
 
 
@@ -360,6 +392,8 @@ def main() -> int:
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-decode-tokens", type=int, default=2)
+    ap.add_argument("--decode-batch", type=int, default=8,
+                    help="also time decode with this many sequences per step (1: skip)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the other shapes (lm_head, MLP, RoPE, attention, copy)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -381,9 +415,13 @@ def main() -> int:
 
     r = gemv_bench(a.steps, a.warmup, a.rot, dev)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
-    dec = None
+    dec = dec8 = None
     if not a.no_decode:
         dec = decode_bench(a.ctx, a.new_tokens, dev, 0 if a.no_cpu else a.cpu_decode_tokens)
+        if a.decode_batch > 1:   # the same weights, several sequences per step
+            dec8 = decode_bench(a.ctx, a.new_tokens, dev, 0, batch=a.decode_batch,
+                                w=dec["weights"])
+        dec.pop("weights")
     sec = None if a.no_secondary else secondary_bench(dev)
     gbs = r["gbs"]
     line = {
@@ -431,6 +469,15 @@ def main() -> int:
             "GB/s": round(dec["gbs"], 1),
             "roofline_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
             "cpu_baseline": dec.get("cpu"),
+        }
+    if dec8 is not None:
+        line["decode_batched"] = {
+            "workload": f"the same decode with {dec8['batch']} sequences per step (weights read "
+                        f"once per step, each sequence its own K/V cache)",
+            "tok_s": round(dec8["tok_s"], 1),
+            "ms_per_step": round(dec8["ms_per_token"], 4),
+            "bytes_per_step": dec8["bytes_per_token"],
+            "GB/s": round(dec8["gbs"], 1),
         }
     if sec is not None:
         line["other_shapes"] = sec

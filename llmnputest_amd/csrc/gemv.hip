@@ -162,7 +162,7 @@ __device__ __forceinline__ void transpose_reduce4(const float (&v)[16], float (&
 
 // One work item (an output group, or one K part of it) of a GEMV launch. Returns true when
 // this workgroup ran the epilogue (for a split group, only the last part to arrive does).
-template <int KIND, int B, int TPW>
+template <int KIND, int B, int TPW, bool SYS>
 __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   constexpr int TB = KIND == 4 ? kQ4TileBytes : kQ8TileBytes;
   constexpr int NCH = KIND == 4 ? 4 : 8;              // 16-byte chunks per lane per tile
@@ -227,7 +227,10 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   constexpr int kSsqIt = 3;
   float4 hs[B][kSsqIt];
   const bool split_norm = norm && ks > 1 && !pre_ssq;
-  const int sys = a.sys_io;
+  // SYS: a stage of a multi-stage launch, whose activations and outputs cross workgroups
+  // of the same launch (system-coherent loads and stores). A compile-time choice: loads in
+  // runtime branches make the compiler wait for them at the join, before the weight stream.
+  constexpr int sys = SYS ? 1 : 0;
   auto load_acts = [&]() {
     const void* xbase = norm ? (const void*)a.hres : (const void*)a.x;
     const uint32_t xbytes = (uint32_t)((size_t)a.batch * a.x_stride * (norm ? 4 : 2));
@@ -241,7 +244,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       for (int b = 0; b < B; ++b) {
         const int bb = min(b, a.batch - 1);
         const uint32_t off = (uint32_t)(((size_t)bb * a.x_stride + k) * (norm ? 4 : 2));
-        if (sys) {
+        if constexpr (SYS) {
           ar[b][t][0] = ld16_sys(xr_, off);
           ar[b][t][1] = ld16_sys(xr_, norm ? off + 16 : off);
         } else {
@@ -259,7 +262,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float* src = a.ssq_in + min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1);
-          sq[b][j] = sys ? load_sys(src) : *src;
+          if constexpr (SYS) sq[b][j] = load_sys(src);
+          else sq[b][j] = *src;
         }
     }
     // with K split and no partials given, this workgroup's tiles see only part of the row:
@@ -272,7 +276,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 #pragma unroll
         for (int b = 0; b < B; ++b) {
           const uint32_t off = (uint32_t)(((size_t)min(b, a.batch - 1) * a.x_stride + 4 * i) * 4);
-          if (sys) {
+          if constexpr (SYS) {
             const uint4 u = ld16_sys(xr_, off);
             hs[b][it] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y),
                                     __uint_as_float(u.z), __uint_as_float(u.w));
@@ -283,7 +287,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       }
     }
   };
-  const bool staged = a.wait_cnt != nullptr;
+  const bool staged = SYS && a.wait_cnt != nullptr;
   if (!staged) load_acts();
 
   // ---- 2. weights and per-group metadata of every tile of this wave
@@ -366,7 +370,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       if (b < a.batch)
         for (int i = tid + kSsqIt * (int)blockDim.x; i < K / 4; i += blockDim.x) {
           const float* hp = a.hres + b * a.x_stride + 4 * i;
-          const float4 h = sys ? make_float4(load_sys(hp), load_sys(hp + 1), load_sys(hp + 2),
+          const float4 h = SYS ? make_float4(load_sys(hp), load_sys(hp + 1), load_sys(hp + 2),
                                              load_sys(hp + 3))
                                : *(const float4*)hp;
           ssq[b] = fmaf(h.x, h.x, fmaf(h.y, h.y, fmaf(h.z, h.z, fmaf(h.w, h.w, ssq[b]))));
@@ -716,7 +720,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 
 template <int KIND, int B, int TPW>
 __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
-  (void)gemv_body<KIND, B, TPW>(a, blockIdx.x);
+  (void)gemv_body<KIND, B, TPW, false>(a, blockIdx.x);
 }
 
 // A chain of GEMV stages in one launch: stage s owns workgroups [wg_begin[s], wg_begin[s+1])
@@ -739,7 +743,7 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_multi_kernel(MultiGe
   __shared__ int s_final;
   int s = 0;
   while (s + 1 < m.n_stages && (int)blockIdx.x >= m.wg_begin[s + 1]) ++s;
-  const bool done_item = gemv_body<KIND, B, TPW>(m.st[s], blockIdx.x - m.wg_begin[s]);
+  const bool done_item = gemv_body<KIND, B, TPW, true>(m.st[s], blockIdx.x - m.wg_begin[s]);
   if (!done_item) return;   // a split part that was not last: the last part signals
   wait_vm();                // every output store of this item is acknowledged
   __syncthreads();
