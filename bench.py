@@ -169,99 +169,114 @@ def random_q8_tiles(n: int, k: int, gen: torch.Generator, dev) -> torch.Tensor:
     return w.reshape(-1)
 
 
-def secondary_bench(dev) -> dict:
+SECONDARY_GROUPS = ("lm_head", "mlp", "prefill", "rope", "attention", "copy")
+
+
+def secondary_bench(dev, groups=SECONDARY_GROUPS) -> dict:
     """The other shapes of the hot path, each timed over a graph of launches with inputs
     resident in HBM (weights rotated past the 256 MB Infinity Cache where they would fit):
-    the q8 lm_head GEMV, the [gate,up,SwiGLU] + down MLP at batch 1 and 8, RoPE, GQA decode
-    attention over the context lengths and batches of the parity tests, and a plain copy."""
+    the q8 lm_head GEMV (and its 512-row prefill block), the [gate,up,SwiGLU] + down MLP at
+    batch 1 and 8, the prefill contraction over 2048 rows, RoPE, GQA decode attention over
+    the context lengths and batches of the parity tests, and a plain copy. `groups` picks a
+    subset (profiling runs)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(99)
     out = {}
-    # q8 lm_head 248320 x 1024, two copies (540 MB)
-    n, k = 248320, 1024
-    ws = [random_q8_tiles(n, k, gen, dev) for _ in range(2)]
-    x = torch.randn(k, device=dev, generator=gen).to(torch.bfloat16)
-    y = torch.empty(n, dtype=torch.float32, device=dev)
-    t = _graph_time(lambda: [ops.gemv(w, "q8", x, n // 32, k // 256, out=y) for w in ws], 10) / 2
-    b = ws[0].numel() + 2 * k + 4 * n
-    out["lm_head_q8_248320x1024"] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
-    # the same lm_head over a 512-row prefill block (the rows the reference hands to torch)
-    xp = torch.randn(512, k, device=dev, generator=gen).to(torch.bfloat16)
-    yp = torch.empty(512, n, dtype=torch.float32, device=dev)
-    wsg = ops.Workspace(1 << 20, device=dev)
-    t = _graph_time(lambda: ops.gemm(ws[0], "q8", xp, n // 32, k // 256, out=yp, ws=wsg), 5)
-    fl = 2.0 * 512 * n * k
-    out["lm_head_q8_248320x1024_prefill_m512"] = {"us": round(t * 1e6, 1),
-                                                  "TFLOP/s": round(fl / t / 1e12, 1)}
-    del ws, xp, yp
-    # MLP: [gate, up, SwiGLU] then down, 8 layers rotated (315 MB), batch 1 and 8
-    layers = [(random_q4_tiles(INTER, HIDDEN, gen, dev), random_q4_tiles(INTER, HIDDEN, gen, dev),
-               random_q4_tiles(HIDDEN, INTER, gen, dev)) for _ in range(8)]
-    wsp = ops.Workspace(8 << 20, device=dev)
-    # batch 8 runs on the matrix cores by default; "_valu" pins the VALU GEMV for comparison
-    for bb, path in ((1, ""), (8, ""), (8, "_valu")):
-        xb = torch.randn(bb, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
-        hb = torch.empty(bb, INTER, dtype=torch.bfloat16, device=dev)
-        yb = torch.empty(bb, HIDDEN, dtype=torch.float32, device=dev)
+    if "lm_head" in groups:
+        # q8 lm_head 248320 x 1024, two copies (540 MB)
+        n, k = 248320, 1024
+        ws = [random_q8_tiles(n, k, gen, dev) for _ in range(2)]
+        x = torch.randn(k, device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty(n, dtype=torch.float32, device=dev)
+        t = _graph_time(lambda: [ops.gemv(w, "q8", x, n // 32, k // 256, out=y) for w in ws], 10) / 2
+        b = ws[0].numel() + 2 * k + 4 * n
+        out["lm_head_q8_248320x1024"] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+        # the same lm_head over a 512-row prefill block (the rows the reference hands to torch)
+        xp = torch.randn(512, k, device=dev, generator=gen).to(torch.bfloat16)
+        yp = torch.empty(512, n, dtype=torch.float32, device=dev)
+        wsg = ops.Workspace(1 << 20, device=dev)
+        t = _graph_time(lambda: ops.gemm(ws[0], "q8", xp, n // 32, k // 256, out=yp, ws=wsg), 5)
+        fl = 2.0 * 512 * n * k
+        out["lm_head_q8_248320x1024_prefill_m512"] = {"us": round(t * 1e6, 1),
+                                                      "TFLOP/s": round(fl / t / 1e12, 1)}
+        del ws, xp, yp
+    if "mlp" in groups or "prefill" in groups:
+        # MLP: [gate, up, SwiGLU] then down, 8 layers rotated (315 MB), batch 1 and 8
+        layers = [(random_q4_tiles(INTER, HIDDEN, gen, dev),
+                   random_q4_tiles(INTER, HIDDEN, gen, dev),
+                   random_q4_tiles(HIDDEN, INTER, gen, dev)) for _ in range(8)]
+        wsp = ops.Workspace(8 << 20, device=dev)
+    if "mlp" in groups:
+        # batch 8 runs on the matrix cores by default; "_valu" pins the VALU GEMV
+        for bb, path in ((1, ""), (8, ""), (8, "_valu")):
+            xb = torch.randn(bb, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
+            hb = torch.empty(bb, INTER, dtype=torch.bfloat16, device=dev)
+            yb = torch.empty(bb, HIDDEN, dtype=torch.float32, device=dev)
 
-        def mlp():
-            for g_, u_, d_ in layers:
-                ops.gate_up_swiglu(g_, u_, INTER // 32, HIDDEN // 256, xb, h_out=hb, ws=wsp)
-                ops.gemv(d_, "q4", hb, HIDDEN // 32, INTER // 256, out=yb, ws=wsp)
-        if path:
-            ops.set_mfma_rows("q4", 0)
-        try:
-            t = _graph_time(mlp, 10) / len(layers)
-        finally:
-            ops.set_mfma_rows("q4", 2)
-        byt = 3 * q4_bytes(INTER, HIDDEN) + bb * (2 * HIDDEN + 2 * INTER * 2 + 4 * HIDDEN)
-        out[f"mlp_gate_up_swiglu_down_b{bb}{path}"] = {"us": round(t * 1e6, 2),
-                                                       "GB/s": round(byt / t / 1e9, 1)}
-    # prefill: the batched contraction over 2048 rows (gate 2560->8192, down 8192->2560)
-    for name, (n_, k_) in (("gate_2560x8192", (INTER, HIDDEN)), ("down_8192x2560", (HIDDEN, INTER))):
-        m_ = 2048
-        xp = torch.randn(m_, k_, device=dev, generator=gen).to(torch.bfloat16)
-        yp = torch.empty(m_, n_, dtype=torch.float32, device=dev)
-        wl = [L[0] if n_ == INTER else L[2] for L in layers[:4]]
-        t = _graph_time(lambda: [ops.gemm(w_, "q4", xp, n_ // 32, k_ // 256, out=yp, ws=wsp)
-                                 for w_ in wl], 5) / len(wl)
-        fl = 2.0 * m_ * n_ * k_
-        out[f"prefill_q4_{name}_m{m_}"] = {"us": round(t * 1e6, 1),
-                                           "TFLOP/s": round(fl / t / 1e12, 1),
-                                           "frac_of_bf16_mfma_peak": round(fl / t / 2.5e15, 4)}
-    del layers
-    # RoPE on q [B,40,64] and k [B,8,64]
-    tab = ops.rope_table(4096, 64, 10000.0, device=dev)
-    for bb in (1, 8):
-        q = torch.randn(bb, 40, 64, device=dev, generator=gen).to(torch.bfloat16)
-        kk = torch.randn(bb, 8, 64, device=dev, generator=gen).to(torch.bfloat16)
-        pos = torch.randint(0, 4096, (bb,), dtype=torch.int32, device=dev, generator=gen)
-        qo_, ko_ = torch.empty_like(q), torch.empty_like(kk)
-        t = _graph_time(lambda: (ops.rope(q, pos, tab, out=qo_), ops.rope(kk, pos, tab, out=ko_)),
-                        50)
-        out[f"rope_q40_k8_b{bb}"] = {"us": round(t * 1e6, 2)}
-    # GQA decode attention, 40 q / 8 kv heads, d 64
-    wsa = ops.Workspace(64 << 20, device=dev)
-    for bb in (1, 8):
-        for L in (512, 4096, 32768):
-            kv_bytes = bb * 8 * L * 64 * 2 * 2
-            copies = max(1, min(8, (600 << 20) // kv_bytes))
-            caches = [(torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16),
-                       torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16))
-                      for _ in range(copies)]
+            def mlp():
+                for g_, u_, d_ in layers:
+                    ops.gate_up_swiglu(g_, u_, INTER // 32, HIDDEN // 256, xb, h_out=hb, ws=wsp)
+                    ops.gemv(d_, "q4", hb, HIDDEN // 32, INTER // 256, out=yb, ws=wsp)
+            if path:
+                ops.set_mfma_rows("q4", 0)
+            try:
+                t = _graph_time(mlp, 10) / len(layers)
+            finally:
+                ops.set_mfma_rows("q4", 2)
+            byt = 3 * q4_bytes(INTER, HIDDEN) + bb * (2 * HIDDEN + 2 * INTER * 2 + 4 * HIDDEN)
+            out[f"mlp_gate_up_swiglu_down_b{bb}{path}"] = {"us": round(t * 1e6, 2),
+                                                           "GB/s": round(byt / t / 1e9, 1)}
+    if "prefill" in groups:
+        # the batched contraction over 2048 rows (gate 2560->8192, down 8192->2560)
+        for name, (n_, k_) in (("gate_2560x8192", (INTER, HIDDEN)),
+                               ("down_8192x2560", (HIDDEN, INTER))):
+            m_ = 2048
+            xp = torch.randn(m_, k_, device=dev, generator=gen).to(torch.bfloat16)
+            yp = torch.empty(m_, n_, dtype=torch.float32, device=dev)
+            wl = [L[0] if n_ == INTER else L[2] for L in layers[:4]]
+            t = _graph_time(lambda: [ops.gemm(w_, "q4", xp, n_ // 32, k_ // 256, out=yp, ws=wsp)
+                                     for w_ in wl], 5) / len(wl)
+            fl = 2.0 * m_ * n_ * k_
+            out[f"prefill_q4_{name}_m{m_}"] = {"us": round(t * 1e6, 1),
+                                               "TFLOP/s": round(fl / t / 1e12, 1),
+                                               "frac_of_bf16_mfma_peak": round(fl / t / 2.5e15, 4)}
+    if "mlp" in groups or "prefill" in groups:
+        del layers
+    if "rope" in groups:
+        # RoPE on q [B,40,64] and k [B,8,64]
+        tab = ops.rope_table(4096, 64, 10000.0, device=dev)
+        for bb in (1, 8):
             q = torch.randn(bb, 40, 64, device=dev, generator=gen).to(torch.bfloat16)
-            lens = torch.full((bb,), L, dtype=torch.int32, device=dev)
-            o = torch.empty_like(q)
-            t = _graph_time(lambda: [ops.gqa_decode(q, kc, vc, lens, 0.125, out=o, ws=wsa)
-                                     for kc, vc in caches], 10) / copies
-            out[f"gqa_decode_b{bb}_L{L}"] = {"us": round(t * 1e6, 2),
-                                             "GB/s": round(kv_bytes / t / 1e9, 1)}
-            del caches
-    # plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB): the achievable streaming rate
-    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
-    dst = torch.empty_like(src)
-    t = _graph_time(lambda: dst.copy_(src), 5)
-    out["copy_1GiB"] = {"us": round(t * 1e6, 1), "GB/s": round(2 * (1 << 30) / t / 1e9, 1)}
+            kk = torch.randn(bb, 8, 64, device=dev, generator=gen).to(torch.bfloat16)
+            pos = torch.randint(0, 4096, (bb,), dtype=torch.int32, device=dev, generator=gen)
+            qo_, ko_ = torch.empty_like(q), torch.empty_like(kk)
+            t = _graph_time(lambda: (ops.rope(q, pos, tab, out=qo_),
+                                     ops.rope(kk, pos, tab, out=ko_)), 50)
+            out[f"rope_q40_k8_b{bb}"] = {"us": round(t * 1e6, 2)}
+    if "attention" in groups:
+        # GQA decode attention, 40 q / 8 kv heads, d 64
+        wsa = ops.Workspace(64 << 20, device=dev)
+        for bb in (1, 8):
+            for L in (512, 4096, 32768):
+                kv_bytes = bb * 8 * L * 64 * 2 * 2
+                copies = max(1, min(8, (600 << 20) // kv_bytes))
+                caches = [(torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16),
+                           torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16))
+                          for _ in range(copies)]
+                q = torch.randn(bb, 40, 64, device=dev, generator=gen).to(torch.bfloat16)
+                lens = torch.full((bb,), L, dtype=torch.int32, device=dev)
+                o = torch.empty_like(q)
+                t = _graph_time(lambda: [ops.gqa_decode(q, kc, vc, lens, 0.125, out=o, ws=wsa)
+                                         for kc, vc in caches], 10) / copies
+                out[f"gqa_decode_b{bb}_L{L}"] = {"us": round(t * 1e6, 2),
+                                                 "GB/s": round(kv_bytes / t / 1e9, 1)}
+                del caches
+    if "copy" in groups:
+        # plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB): the achievable streaming rate
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        t = _graph_time(lambda: dst.copy_(src), 5)
+        out["copy_1GiB"] = {"us": round(t * 1e6, 1), "GB/s": round(2 * (1 << 30) / t / 1e9, 1)}
     return out
 
 
@@ -398,6 +413,9 @@ def main() -> int:
                     help="skip the other shapes (lm_head, MLP, RoPE, attention, copy)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--only", default=None, metavar="GROUPS",
+                    help="profiling: only these comma-separated secondary groups (" +
+                         ",".join(SECONDARY_GROUPS) + "); prints their JSON and exits")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -412,6 +430,14 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if a.calibrate_copy:
         return copy_calibration(a.calibrate_copy, 10, dev)
+    if a.only:
+        groups = tuple(g for g in a.only.split(",") if g)
+        bad = [g for g in groups if g not in SECONDARY_GROUPS]
+        if bad:
+            print(f"unknown groups {bad}; choose from {SECONDARY_GROUPS}", file=sys.stderr)
+            return 2
+        print(json.dumps({"other_shapes": secondary_bench(dev, groups)}), flush=True)
+        return 0
 
     r = gemv_bench(a.steps, a.warmup, a.rot, dev)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
