@@ -212,6 +212,11 @@ int q4nx_ws_check(void *ws, void *stream);
  * granite_attn_finish). head_dim must be 64. q: bf16 [B][Hq][64]; out: bf16 and/or fp32
  * [B][Hq][64]; caches as in q4nx_qkv_rope. n_split = 0 chooses automatically. */
 size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len);
+/* Policy knob: 1 (default) runs q4nx_gqa_decode on the matrix cores (scores and P.V on
+ * v_mfma_f32_16x16x32_bf16, P carried as three bf16 terms), 0 on the VALU kernel. Both give
+ * fp32-accurate results. Process-wide; returns the previous setting. No reference
+ * counterpart. */
+int q4nx_set_attn_mfma(int on);
 int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                     uint16_t *out, float *out_f32, int batch, int n_q_heads,
                     int n_kv_heads, int head_dim, const int32_t *lens, int max_len,

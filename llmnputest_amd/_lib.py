@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple] = {
                               c_p, c_sz, c_p]),
     "q4nx_ws_check": (c_i, [c_p, c_p]),
     "q4nx_gqa_decode_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
+    "q4nx_set_attn_mfma": (c_i, [c_i]),
     "q4nx_gqa_decode": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
                               c_i64, c_f, c_i, c_p, c_sz, c_p]),
     "q4nx_round_bf16": (c_i, [c_p, c_p, c_i64, c_p]),

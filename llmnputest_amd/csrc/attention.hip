@@ -47,7 +47,7 @@ constexpr int kAttnSteps = 4;                              // 8-position steps p
 constexpr int kAttnRound = kAttnWaves * kAttnSteps * 8;    // positions per workgroup round
 constexpr int kAttnStates = kAttnWaves * 8;                // lane softmax states per WG
 constexpr int kPartStride = 68;                            // acc[64], m, l, 2 pad (16 B rows)
-constexpr int kMergeSplits = 16;                           // splits merged per LDS pass
+constexpr int kMergeSplits = 30;   // splits merged per LDS pass (30 records fit s_acc)
 
 __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -82,9 +82,11 @@ __device__ __forceinline__ void attn_round(AttnLane<G>& st, const uint4 (&kr)[kA
                                            const uint4 (&vr)[kAttnSteps], int r0, int end,
                                            int wave, int pl, float scale_l2) {
   float sc[kAttnSteps][G];
+  uint4 vm[kAttnSteps];   // V rows, zero past the length (p = 0 there, and 0 * NaN is NaN)
 #pragma unroll
   for (int s = 0; s < kAttnSteps; ++s) {
     const bool ok = r0 + (wave * kAttnSteps + s) * 8 + pl < end;
+    vm[s] = ok ? vr[s] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float d = dot2bf(st.q[h].x, kr[s].x, 0.f);
@@ -113,7 +115,7 @@ __device__ __forceinline__ void attn_round(AttnLane<G>& st, const uint4 (&kr)[kA
       for (int s = 0; s < kAttnSteps; ++s) {
         const float p = ex2(sc[s][h] - mn);   // masked positions: 2^-inf = 0
         st.l[h] += p;
-        const uint32_t vv[4] = {vr[s].x, vr[s].y, vr[s].z, vr[s].w};
+        const uint32_t vv[4] = {vm[s].x, vm[s].y, vm[s].z, vm[s].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           st.acc[h][2 * i] = fmaf(p, bf16lo(vv[i]), st.acc[h][2 * i]);
@@ -125,9 +127,107 @@ __device__ __forceinline__ void attn_round(AttnLane<G>& st, const uint4 (&kr)[kA
   }
 }
 
+// The end both kernels share. s_fin[h] holds the workgroup's (acc[64], m, l) for query head
+// h of the group. With one split that is the answer; otherwise the record is published and
+// the last workgroup of the (sequence, kv head) to arrive merges every split's record
+// exactly, in split order, through s_buf (kMergeSplits records per pass).
+template <int G>
+__device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kPartStride],
+                                            float* s_buf, float (*s_f)[kAttnStates], float* s_g,
+                                            int* s_last, int bk, int split, int b, int kvh) {
+  const int tid = threadIdx.x;
+  if (a.n_split > 1) {
+    // publish this split's (acc, m, l), then the last workgroup of (b, kv head) merges
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.partial, a.partial_bytes);
+    const uint32_t rec_bytes = G * kPartStride * 4;
+    const uint32_t rec = (uint32_t)((size_t)bk * a.n_split + split) * rec_bytes;
+    for (int e = tid; e < G * kPartStride / 4; e += 256)
+      st16_sys(pr, rec + e * 16, ((const uint4*)&s_fin[0][0])[e]);
+    wait_vm();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = atomicAdd(&a.counters[bk], 1u);
+      *s_last = (prev == (unsigned)(a.n_split - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+
+    constexpr int kRec16 = G * kPartStride / 4;                     // uint4 per split record
+    constexpr int kPer = (kMergeSplits * kRec16 + 255) / 256;       // loads per thread per pass
+    const uint32_t base = (uint32_t)((size_t)bk * a.n_split) * rec_bytes;
+    // running merged state: s_fin[h][64] = M, s_fin[h][65] = L, thread (h, d) holds A
+    float Ar[2] = {0.f, 0.f};
+    if (tid < G) {
+      s_fin[tid][64] = -INFINITY;
+      s_fin[tid][65] = 0.f;
+    }
+    for (int cs = 0; cs < a.n_split; cs += kMergeSplits) {
+      const int ns = min(kMergeSplits, a.n_split - cs);
+      const uint32_t src = base + (uint32_t)cs * rec_bytes;
+      uint4 v[kPer];   // unconditional: past the buffer end the loads return 0
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) v[i] = ld16_sys(pr, src + (tid + i * 256) * 16);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int e = tid + i * 256;
+        if (e < ns * kRec16) ((uint4*)s_buf)[e] = v[i];
+      }
+      __syncthreads();
+      if (tid < G * 32) {   // thread (h, split sp of the pass): weights in parallel
+        const int h = tid >> 5, sp = tid & 31;
+        const float ms = sp < ns ? s_buf[(sp * G + h) * kPartStride + 64] : -INFINITY;
+        const float ls = sp < ns ? s_buf[(sp * G + h) * kPartStride + 65] : 0.f;
+        const float Mh = group32_max(fmaxf(ms, s_fin[h][64]));   // s_fin[h][64]: running M
+        const float f = (Mh == -INFINITY) ? 0.f : ex2(ms - Mh);
+        const float Lp = group32_sum(ls * f);
+        s_f[h][sp] = f;
+        if (sp == 0) {
+          const float Mo = s_fin[h][64];
+          const float g = (Mo == -INFINITY) ? 0.f : ex2(Mo - Mh);
+          s_g[h] = g;
+          s_fin[h][65] = fmaf(s_fin[h][65], g, Lp);
+          s_fin[h][64] = Mh;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int e = tid + jj * 256;
+        if (e < G * 64) {
+          const int h = e >> 6, d = e & 63;
+          float As = Ar[jj] * s_g[h];
+          for (int sp = 0; sp < ns; ++sp)
+            As = fmaf(s_buf[(sp * G + h) * kPartStride + d], s_f[h][sp], As);
+          Ar[jj] = As;
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int e = tid + jj * 256;
+      if (e < G * 64) s_fin[e >> 6][e & 63] = Ar[jj];
+    }
+    if (tid == 0)  // ready for the next call
+      __hip_atomic_store(&a.counters[bk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+  }
+
+  for (int e = tid; e < G * 64; e += 256) {
+    const int h = e >> 6, d = e & 63;
+    const float Ls = s_fin[h][65];
+    const float o = Ls > 0.f ? s_fin[h][d] / Ls : 0.f;   // an empty sequence gives zeros
+    const size_t oi = ((size_t)b * a.hq + kvh * G + h) * 64 + d;
+    if (a.out) a.out[oi] = f32_to_bf16(o);
+    if (a.out_f32) a.out_f32[oi] = o;
+  }
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
   static_assert(G * 32 <= 256, "one thread per (head, lane state)");
+  static_assert(kMergeSplits <= 32 && kMergeSplits * kPartStride <= kAttnStates * 64,
+                "a merge pass fits s_acc and one 32-lane group per head");
   __shared__ float s_m[G][kAttnStates], s_f[G][kAttnStates];
   __shared__ __attribute__((aligned(16))) float s_acc[kAttnStates * G * 64];  // also merge buffer
   __shared__ __attribute__((aligned(16))) float s_fin[G][kPartStride];
@@ -209,91 +309,214 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  if (a.n_split > 1) {
-    // publish this split's (acc, m, l), then the last workgroup of (b, kv head) merges
-    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.partial, a.partial_bytes);
-    const uint32_t rec_bytes = G * kPartStride * 4;
-    const uint32_t rec = (uint32_t)((size_t)bk * a.n_split + split) * rec_bytes;
-    for (int e = tid; e < G * kPartStride / 4; e += 256)
-      st16_sys(pr, rec + e * 16, ((const uint4*)&s_fin[0][0])[e]);
-    wait_vm();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = atomicAdd(&a.counters[bk], 1u);
-      s_last = (prev == (unsigned)(a.n_split - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!s_last) return;
+  attn_finish<G>(a, s_fin, s_acc, s_f, s_g, &s_last, bk, split, b, kvh);
+}
 
-    constexpr int kRec16 = G * kPartStride / 4;                     // uint4 per split record
-    constexpr int kPer = (kMergeSplits * kRec16 + 255) / 256;       // loads per thread per pass
-    const uint32_t base = (uint32_t)((size_t)bk * a.n_split) * rec_bytes;
-    // running merged state: s_fin[h][64] = M, s_fin[h][65] = L, thread (h, d) holds A
-    float Ar[2] = {0.f, 0.f};
-    if (tid < G) {
-      s_fin[tid][64] = -INFINITY;
-      s_fin[tid][65] = 0.f;
+// ---------------------------------------------------------------- matrix-core kernel
+//
+// Same workgroups, splits, rounds (128 positions: 32 per wave) and split merge as above, but
+// each wave scores and accumulates its 32 positions for all query heads of the group at once
+// on v_mfma_f32_16x16x32_bf16 (the group's heads padded to 16 with zero rows):
+//   S^T[pos][head]  = K[pos][:] . Q[head][:]      A = 16 K rows as stored (16 B per lane),
+//                                                 B = Q^T; two MFMAs cover the 64 dims
+//   O^T[dim][head] += V^T[dim][pos] . P^T[pos][head]
+// Lane j + 16g of a score tile holds head j at positions 4g..4g+3 of the tile. The P.V
+// contraction takes its 32 positions in exactly that order (slot 8g + e <-> position
+// 16(e/4) + 4g + e%4), so P^T is already in place in the lanes; V^T is gathered to match:
+// each lane loads dims 4j..4j+3 (8 B) of its 8 positions and v_perm splits them into four
+// operands, operand u holding dims 4i + u, so every lane of an O^T tile belongs to one head
+// and the online-softmax rescale is per lane. P enters as three bf16 terms p1 + p2 + p3
+// (each the bf16 rounding of what the previous ones left), which carries it to fp32
+// precision: products are exact and sums fp32, as on the VALU path. A head's running max is
+// kept equal across its four lane groups, so the 32 positions share one scale; the four
+// waves' states merge through LDS with one barrier.
+
+struct MfmaLane {
+  u32x4_t q[2];   // Q^T operands, dims 0..31 and 32..63
+  f32x4_t o[4];   // O^T tiles: o[u][e] = head j, dim 16g + 4e + u
+  float m, l;     // running max (scaled log2 units, same in every lane of the head); l of
+                  // this lane's positions
+};
+
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  const f32x2_v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
+}
+
+// K rows (tile t, dims half c) and the 8-byte V pieces of one wave's 32 positions from p0;
+// positions at or past `stop` read row 0 instead (masked later).
+__device__ __forceinline__ void attn_mfma_load(const uint16_t* kbase, const uint16_t* vbase,
+                                               int p0, int stop, int j, int g,
+                                               u32x4_t (&kr)[4], uint2 (&vr)[8]) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int pos = p0 + 16 * t + j;
+    const size_t row = (size_t)(pos < stop ? pos : 0) * 64;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) kr[2 * t + c] = *(const u32x4_t*)(kbase + row + 32 * c + 8 * g);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int pos = p0 + 16 * (e >> 2) + 4 * g + (e & 3);
+    const size_t row = (size_t)(pos < stop ? pos : 0) * 64;
+    vr[e] = *(const uint2*)(vbase + row + 4 * j);
+  }
+}
+
+__device__ __forceinline__ void attn_mfma_round(MfmaLane& st, const u32x4_t (&kr)[4],
+                                                const uint2 (&vr)[8], int p0, int end, int g,
+                                                float scale_l2) {
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t s0 = mfma_bf16(kr[0], st.q[0], zero);
+  f32x4_t s1 = mfma_bf16(kr[2], st.q[0], zero);
+  s0 = mfma_bf16(kr[1], st.q[1], s0);
+  s1 = mfma_bf16(kr[3], st.q[1], s1);
+  float sc[8];
+  bool ok[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    ok[e] = p0 + 16 * (e >> 2) + 4 * g + (e & 3) < end;
+    sc[e] = ok[e] ? (e < 4 ? s0[e] : s1[e - 4]) * scale_l2 : -INFINITY;
+  }
+  float mr = sc[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mr = fmaxf(mr, sc[e]);
+  mr = fmaxf(mr, __shfl_xor(mr, 16));
+  mr = fmaxf(mr, __shfl_xor(mr, 32));
+  const float mn = fmaxf(st.m, mr);
+  const float mb = mn == -INFINITY ? 0.f : mn;   // nothing seen yet: every p and corr is 0
+  const float corr = ex2(st.m - mb);
+  float p[8], ls = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    p[e] = ex2(sc[e] - mb);
+    ls += p[e];
+  }
+  st.l = fmaf(st.l, corr, ls);
+  st.m = mn;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) st.o[u] *= corr;
+  u32x4_t pp[3];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float x0 = p[2 * w], x1 = p[2 * w + 1];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      const uint32_t h = pk_bf16(x0, x1);
+      pp[t][w] = h;
+      x0 -= bf16lo(h);
+      x1 -= bf16hi(h);
     }
-    for (int cs = 0; cs < a.n_split; cs += kMergeSplits) {
-      const int ns = min(kMergeSplits, a.n_split - cs);
-      const uint32_t src = base + (uint32_t)cs * rec_bytes;
-      uint4 v[kPer];   // unconditional: past the buffer end the loads return 0
+  }
+  uint2 v[8];
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) v[i] = ld16_sys(pr, src + (tid + i * 256) * 16);
+  for (int e = 0; e < 8; ++e) v[e] = ok[e] ? vr[e] : make_uint2(0u, 0u);
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int e = tid + i * 256;
-        if (e < ns * kRec16) ((uint4*)s_acc)[e] = v[i];
-      }
-      __syncthreads();
-      if (tid < G * 16) {   // thread (h, split sp of the pass): weights in parallel
-        const int h = tid >> 4, sp = tid & 15;
-        const float ms = sp < ns ? s_acc[(sp * G + h) * kPartStride + 64] : -INFINITY;
-        const float ls = sp < ns ? s_acc[(sp * G + h) * kPartStride + 65] : 0.f;
-        const float Mh = group16_max(fmaxf(ms, s_fin[h][64]));   // s_fin[h][64]: running M
-        const float f = (Mh == -INFINITY) ? 0.f : ex2(ms - Mh);
-        const float Lp = group16_sum(ls * f);
-        s_f[h][sp] = f;
-        if (sp == 0) {
-          const float Mo = s_fin[h][64];
-          const float g = (Mo == -INFINITY) ? 0.f : ex2(Mo - Mh);
-          s_g[h] = g;
-          s_fin[h][65] = fmaf(s_fin[h][65], g, Lp);
-          s_fin[h][64] = Mh;
-        }
-      }
-      __syncthreads();
+  for (int u = 0; u < 4; ++u) {
+    u32x4_t av;
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int e = tid + jj * 256;
-        if (e < G * 64) {
-          const int h = e >> 6, d = e & 63;
-          float As = Ar[jj] * s_g[h];
-          for (int sp = 0; sp < ns; ++sp)
-            As = fmaf(s_acc[(sp * G + h) * kPartStride + d], s_f[h][sp], As);
-          Ar[jj] = As;
-        }
-      }
-      __syncthreads();
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = u < 2 ? v[2 * w].x : v[2 * w].y;
+      const uint32_t hi = u < 2 ? v[2 * w + 1].x : v[2 * w + 1].y;
+      av[w] = perm(hi, lo, (u & 1) ? 0x07060302u : 0x05040100u);
     }
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int e = tid + jj * 256;
-      if (e < G * 64) s_fin[e >> 6][e & 63] = Ar[jj];
+    for (int t = 0; t < 3; ++t) st.o[u] = mfma_bf16(av, pp[t], st.o[u]);
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
+  static_assert(G * 32 <= 256 && G <= 16, "one thread per (head, split) in the merge");
+  static_assert(kAttnWaves * 64 <= kMergeSplits * kPartStride, "wave states fit s_buf");
+  __shared__ __attribute__((aligned(16))) float s_buf[kMergeSplits * G * kPartStride];
+  __shared__ __attribute__((aligned(16))) float s_fin[G][kPartStride];
+  __shared__ float s_wm[kAttnWaves][G], s_wl[kAttnWaves][G];
+  __shared__ float s_f[G][kAttnStates];
+  __shared__ float s_g[G];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int blk = blockIdx.x;
+  const int split = blk % a.n_split;
+  const int bk = blk / a.n_split;  // b * hkv + kvh
+  const int kvh = bk % a.hkv;
+  const int b = bk / a.hkv;
+  const int start = split * a.chunk;
+  const int stop = min(start + a.chunk, a.max_len);
+  const int j = lane & 15, g = lane >> 4;
+  const size_t head_off = (size_t)b * a.kv_b_stride + (size_t)kvh * a.kv_h_stride;
+  const uint16_t* kbase = a.k + head_off;
+  const uint16_t* vbase = a.v + head_off;
+  const int wo = wave * 32;
+
+  // first round's K/V, q and the length all in flight together
+  u32x4_t kA[4], kB[4];
+  uint2 vA[8], vB[8];
+  attn_mfma_load(kbase, vbase, start + wo, stop, j, g, kA, vA);
+  MfmaLane st;
+  {
+    const uint16_t* qrow = a.q + ((size_t)b * a.hq + kvh * G + (j < G ? j : 0)) * 64;
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const u32x4_t v = *(const u32x4_t*)(qrow + 32 * c + 8 * g);
+      st.q[c] = j < G ? v : z;   // padded heads: zero rows
     }
-    if (tid == 0)  // ready for the next call
-      __hip_atomic_store(&a.counters[bk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __syncthreads();
+  }
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) st.o[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int end = min(stop, max(0, a.lens[b]));
+  const int nr = end > start ? (end - start + kAttnRound - 1) / kAttnRound : 0;
+  for (int r = 0; r < nr; r += 2) {
+    const int r0 = start + r * kAttnRound;
+    if (r + 1 < nr) attn_mfma_load(kbase, vbase, r0 + kAttnRound + wo, stop, j, g, kB, vB);
+    attn_mfma_round(st, kA, vA, r0 + wo, end, g, a.scale_l2);
+    if (r + 2 < nr) attn_mfma_load(kbase, vbase, r0 + 2 * kAttnRound + wo, stop, j, g, kA, vA);
+    if (r + 1 < nr) attn_mfma_round(st, kB, vB, r0 + kAttnRound + wo, end, g, a.scale_l2);
   }
 
+  // ---- merge the four waves: l over each head's lane groups, then (m, l, O) through LDS
+  st.l += __shfl_xor(st.l, 16);
+  st.l += __shfl_xor(st.l, 32);
+  float* s_o = s_buf;   // [wave][head][64]
+  if (j < G) {
+    if (g == 0) {
+      s_wm[wave][j] = st.m;
+      s_wl[wave][j] = st.l;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      *(float4*)(s_o + (wave * G + j) * 64 + 16 * g + 4 * e) =
+          make_float4(st.o[0][e], st.o[1][e], st.o[2][e], st.o[3][e]);
+  }
+  __syncthreads();
   for (int e = tid; e < G * 64; e += 256) {
     const int h = e >> 6, d = e & 63;
-    const float Ls = s_fin[h][65];
-    const float o = Ls > 0.f ? s_fin[h][d] / Ls : 0.f;   // an empty sequence gives zeros
-    const size_t oi = ((size_t)b * a.hq + kvh * G + h) * 64 + d;
-    if (a.out) a.out[oi] = f32_to_bf16(o);
-    if (a.out_f32) a.out_f32[oi] = o;
+    float M = s_wm[0][h];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, s_wm[w][h]);
+    const float Mb = M == -INFINITY ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float f = ex2(s_wm[w][h] - Mb);
+      L = fmaf(s_wl[w][h], f, L);
+      A = fmaf(s_o[(w * G + h) * 64 + d], f, A);
+    }
+    s_fin[h][d] = A;
+    if (d == 0) {
+      s_fin[h][64] = M;
+      s_fin[h][65] = L;
+      s_fin[h][66] = 0.f;
+      s_fin[h][67] = 0.f;
+    }
   }
+  __syncthreads();
+  attn_finish<G>(a, s_fin, s_buf, s_f, s_g, &s_last, bk, split, b, kvh);
 }
 
 // Splits per (sequence, kv head): enough workgroups to cover the GPU (about 512), at least
@@ -306,6 +529,14 @@ static int auto_split(int batch, int hkv, int max_len) {
   return s < 1 ? 1 : s;
 }
 
+static int g_attn_mfma = 1;   // 1: matrix-core kernel, 0: VALU kernel
+
+template <int G>
+static void launch_attn(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (g_attn_mfma) hipLaunchKernelGGL(gqa_mfma_kernel<G>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(gqa_decode_kernel<G>, grid, dim3(256), 0, s, a);
+}
+
 static size_t partial_bytes(int batch, int hkv, int n_split, int G) {
   return (size_t)batch * hkv * n_split * G * kPartStride * 4;
 }
@@ -315,6 +546,12 @@ static size_t partial_bytes(int batch, int hkv, int n_split, int G) {
 using namespace q4nx;
 
 extern "C" {
+
+int q4nx_set_attn_mfma(int on) {
+  const int prev = g_attn_mfma;
+  g_attn_mfma = on ? 1 : 0;
+  return prev;
+}
 
 size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len) {
   if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1) return 0;
@@ -375,17 +612,17 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
     a.partial = (float*)((uint8_t*)ws + Q4NX_WS_COUNTER_BYTES);
     a.partial_bytes = (uint32_t)pb;
   }
-  const dim3 grid((unsigned)(batch * n_kv_heads * a.n_split)), block(256);
+  const dim3 grid((unsigned)(batch * n_kv_heads * a.n_split));
   hipStream_t s = (hipStream_t)stream;
   switch (n_q_heads / n_kv_heads) {
-    case 1: hipLaunchKernelGGL(gqa_decode_kernel<1>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(gqa_decode_kernel<2>, grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL(gqa_decode_kernel<3>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(gqa_decode_kernel<4>, grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL(gqa_decode_kernel<5>, grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL(gqa_decode_kernel<6>, grid, block, 0, s, a); break;
-    case 7: hipLaunchKernelGGL(gqa_decode_kernel<7>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(gqa_decode_kernel<8>, grid, block, 0, s, a); break;
+    case 1: launch_attn<1>(a, grid, s); break;
+    case 2: launch_attn<2>(a, grid, s); break;
+    case 3: launch_attn<3>(a, grid, s); break;
+    case 4: launch_attn<4>(a, grid, s); break;
+    case 5: launch_attn<5>(a, grid, s); break;
+    case 6: launch_attn<6>(a, grid, s); break;
+    case 7: launch_attn<7>(a, grid, s); break;
+    default: launch_attn<8>(a, grid, s); break;
   }
   return check_launch(what);
 }

@@ -50,6 +50,17 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), acc, false);
 }
 
+// v_mfma_f32_16x16x32_bf16: D = A.B + C with A 16x32, B 32x16 (8 bf16 per lane each) and
+// D 16x16 fp32 (4 per lane). Operand layout on gfx950: A[i][k] in lane i + 16(k/8), element
+// k%8; B[k][j] in lane j + 16(k/8), element k%8; D[i][j] in lane j + 16(i/4), element i%4.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4_t mfma_bf16(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
 // v_perm_b32: bytes of {hi:s0, lo:s1} selected by `sel`, 0x0c selects zero.
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);

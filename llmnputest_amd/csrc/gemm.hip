@@ -30,10 +30,7 @@
 
 namespace q4nx {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
 
 template <int KIND>
@@ -52,11 +49,6 @@ struct GemmFmt<8> {
   static constexpr int kLoads = 9;                // 8704 B: the 9th load of lanes 32..63 is padding
   static constexpr int kSlot = 9216;
 };
-
-__device__ __forceinline__ f32x4_t mfma_bf16(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
 
 // 8 transposed code bytes (k-slots 0..7 of one row pair) -> bf16 16 + c for the even row (low
 // nibbles) and the odd row (high nibbles).

@@ -231,6 +231,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   // of the same launch (system-coherent loads and stores). A compile-time choice: loads in
   // runtime branches make the compiler wait for them at the join, before the weight stream.
   constexpr int sys = SYS ? 1 : 0;
+  float ep_res = 0.f;   // epilogue prefetches (see the end of load_acts)
+  int ep_pos = 0;
   auto load_acts = [&]() {
     const void* xbase = norm ? (const void*)a.hres : (const void*)a.x;
     const uint32_t xbytes = (uint32_t)((size_t)a.batch * a.x_stride * (norm ? 4 : 2));
@@ -286,6 +288,19 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         }
       }
     }
+    // the epilogue's own inputs for this thread's first output (batch row tid / 32, row
+    // tid % 32 of the group): the residual (plain) or the sequence position (q/k/v), in
+    // flight with the activations instead of a memory round trip after the reduction.
+    // Unconditional loads, from the weights when the launch has no such input.
+    {
+      const int eb = min(tid >> 5, a.batch - 1), er = tid & 31;
+      const bool res = a.op == OP_PLAIN && a.residual != nullptr;
+      const float* rp = res ? a.residual + (int64_t)eb * a.y_stride + (int64_t)tr * 32 + er
+                            : (const float*)a.w[0];
+      if constexpr (SYS) ep_res = load_sys(rp);
+      else ep_res = *rp;
+      ep_pos = *(a.op == OP_QKV ? a.pos + eb : (const int32_t*)a.w[0]);
+    }
   };
   const bool staged = SYS && a.wait_cnt != nullptr;
   if (!staged) load_acts();
@@ -329,6 +344,15 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
     for (int it = 0; it < kSsqIt; ++it)
 #pragma unroll
       for (int b = 0; b < B; ++b) pin(hs[b][it]);
+  }
+  // RoPE cos/sin of the first epilogue output, now that its position is here (the wait for
+  // it is the activations' wait); they arrive while the tiles are reduced
+  float ep_c, ep_s;
+  {
+    const bool rope = a.op == OP_QKV && ep_pos >= 0 && ep_pos < a.max_pos;
+    const float* tb = rope ? a.rope_tab + (int64_t)ep_pos * 64 + (tid & 31) : (const float*)a.w[0];
+    ep_c = tb[0];
+    ep_s = tb[32];
   }
   if (pre_ssq) {
 #pragma unroll
@@ -643,7 +667,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       if (live) {
         const int64_t n = (int64_t)tr * 32 + r;
         v = sgrp[b][r];
-        if (a.residual != nullptr) v += a.residual[b * a.y_stride + n];
+        if (a.residual != nullptr) v += e0 == 0 ? ep_res : a.residual[b * a.y_stride + n];
         if (a.y != nullptr) put(a.y + b * a.y_stride + n, v, sys);
         if (a.argmax_keys != nullptr) atomicMax(&skey[b], argmax_key(v, (uint32_t)n));
       }
@@ -693,7 +717,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         }
         const float x0 = bf16_to_f32(f32_to_bf16(r0));
         const float x1 = bf16_to_f32(f32_to_bf16(r1));
-        const int p = a.pos[b];
+        const bool first = e == tid;   // prefetched position and RoPE row
+        const int p = first ? ep_pos : a.pos[b];
         const bool pos_ok = p >= 0 && p < a.max_pos;
         if (seg == 2) {
           if (pos_ok) {
@@ -702,8 +727,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
             put(dst + 32 + d, f32_to_bf16(x1), sys);
           }
         } else if (pos_ok) {
-          const float c = a.rope_tab[(int64_t)p * 64 + d];
-          const float sn = a.rope_tab[(int64_t)p * 64 + 32 + d];
+          const float c = first ? ep_c : a.rope_tab[(int64_t)p * 64 + d];
+          const float sn = first ? ep_s : a.rope_tab[(int64_t)p * 64 + 32 + d];
           const float y0 = fmaf(x0, c, -(x1 * sn));
           const float y1 = fmaf(x1, c, x0 * sn);
           uint16_t* dst = (seg == 0)

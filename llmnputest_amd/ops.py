@@ -376,6 +376,12 @@ def ws_check(ws: Workspace | None = None) -> None:
 
 # ---------------------------------------------------------------- attention
 
+def set_attn_mfma(on: bool) -> bool:
+    """Run attention on the matrix-core kernel (True, the default) or the VALU kernel.
+    Returns the previous setting."""
+    return bool(_lib.lib().q4nx_set_attn_mfma(1 if on else 0))
+
+
 def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                lens: torch.Tensor, scale: float = 0.125, max_len: int | None = None,
                n_split: int = 0, out: torch.Tensor | None = None, want_f32: bool = False,

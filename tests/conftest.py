@@ -69,3 +69,12 @@ def mfma(dev):
     _set_kernel_path("mfma")
     yield
     _set_kernel_path("default")
+
+
+@pytest.fixture(params=["mfma", "valu"])
+def apath(request, dev):
+    """Run an attention test on each attention kernel (matrix-core and VALU)."""
+    from llmnputest_amd import ops
+    ops.set_attn_mfma(request.param == "mfma")
+    yield request.param
+    ops.set_attn_mfma(True)

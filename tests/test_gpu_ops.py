@@ -264,7 +264,7 @@ def test_gate_up_swiglu(dev, valu, batch, norm, ksplit):
     (1, 1, False), (1, 32, False), (1, 100, False), (1, 512, False), (1, 4096, False),
     (8, 512, True), (8, 4096, False), (1, 32768, False),
 ])
-def test_gqa_decode(dev, batch, L, ragged):
+def test_gqa_decode(dev, apath, batch, L, ragged):
     rng = np.random.default_rng(15 + L)
     hq, hkv = 40, 8
     q = synth.random_bf16(rng, (batch, hq, 64))
@@ -281,7 +281,7 @@ def test_gqa_decode(dev, batch, L, ragged):
         assert np.array_equal(of.cpu().numpy(), expect)     # one position: out = V[0]
 
 
-def test_gqa_decode_uniform_softmax(dev):
+def test_gqa_decode_uniform_softmax(dev, apath):
     """Constant K gives a uniform softmax, so out = mean(V) (a closed form)."""
     rng = np.random.default_rng(16)
     L = 1000
@@ -296,7 +296,7 @@ def test_gqa_decode_uniform_softmax(dev):
 
 
 @pytest.mark.parametrize("hq,hkv,L", [(8, 8, 300), (16, 2, 1500), (64, 8, 700), (24, 8, 129)])
-def test_gqa_decode_group_sizes(dev, hq, hkv, L):
+def test_gqa_decode_group_sizes(dev, apath, hq, hkv, L):
     """Other query-group sizes (1, 8, 8, 3 query heads per kv head), called twice on one
     workspace so the split counters must have been left at zero."""
     rng = np.random.default_rng(19 + hq)
@@ -315,7 +315,7 @@ def test_gqa_decode_group_sizes(dev, hq, hkv, L):
 
 
 @pytest.mark.parametrize("n_split", [1, 2, 7, 33])
-def test_gqa_decode_splits(dev, n_split):
+def test_gqa_decode_splits(dev, apath, n_split):
     rng = np.random.default_rng(17)
     L = 2100
     q = synth.random_bf16(rng, (2, 40, 64))
@@ -326,6 +326,29 @@ def test_gqa_decode_splits(dev, n_split):
                         torch.from_numpy(lens).to(dev), 0.125, n_split=n_split, want_f32=True)[1]
     ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v), lens, 0.125)
     assert_close(of.cpu().numpy(), ref)
+
+
+def test_gqa_decode_garbage_past_length(dev, apath):
+    """Cache rows at and past a sequence's length take no part in the result whatever they
+    hold: K = +Inf and V = NaN bit patterns there leave the output equal to the oracle's on
+    the clean cache (a masked position contributes p = 0, and 0 * NaN would be NaN)."""
+    rng = np.random.default_rng(20)
+    L = 700
+    q = synth.random_bf16(rng, (2, 40, 64))
+    k = synth.random_bf16(rng, (2, 8, L, 64))
+    v = synth.random_bf16(rng, (2, 8, L, 64))
+    lens = np.array([333, 1], np.int32)
+    kg, vg = k.copy(), v.copy()
+    for b, n in enumerate(lens):
+        kg[b, :, n:] = 0x7F80
+        vg[b, :, n:] = 0x7FC1
+    for n_split in (0, 1, 3):
+        of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(kg, dev), bf16_dev(vg, dev),
+                            torch.from_numpy(lens).to(dev), 0.125, n_split=n_split,
+                            want_f32=True)[1]
+        ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v), lens,
+                               0.125)
+        assert_close(of.cpu().numpy(), ref)
 
 
 # ------------------------------------------------------------------ helpers
