@@ -188,7 +188,8 @@ def secondary_bench(dev, groups=SECONDARY_GROUPS) -> dict:
         ws = [random_q8_tiles(n, k, gen, dev) for _ in range(2)]
         x = torch.randn(k, device=dev, generator=gen).to(torch.bfloat16)
         y = torch.empty(n, dtype=torch.float32, device=dev)
-        t = _graph_time(lambda: [ops.gemv(w, "q8", x, n // 32, k // 256, out=y) for w in ws], 10) / 2
+        t = _graph_time(lambda: [ops.gemv(ws[i % 2], "q8", x, n // 32, k // 256, out=y)
+                                 for i in range(8)], 10) / 8   # alternating: each read cold
         b = ws[0].numel() + 2 * k + 4 * n
         out["lm_head_q8_248320x1024"] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
         # the same lm_head over a 512-row prefill block (the rows the reference hands to torch)
@@ -250,24 +251,29 @@ def secondary_bench(dev, groups=SECONDARY_GROUPS) -> dict:
             kk = torch.randn(bb, 8, 64, device=dev, generator=gen).to(torch.bfloat16)
             pos = torch.randint(0, 4096, (bb,), dtype=torch.int32, device=dev, generator=gen)
             qo_, ko_ = torch.empty_like(q), torch.empty_like(kk)
-            t = _graph_time(lambda: (ops.rope(q, pos, tab, out=qo_),
-                                     ops.rope(kk, pos, tab, out=ko_)), 50)
+            t = _graph_time(lambda: [(ops.rope(q, pos, tab, out=qo_),
+                                      ops.rope(kk, pos, tab, out=ko_)) for _ in range(16)],
+                            20) / 16
             out[f"rope_q40_k8_b{bb}"] = {"us": round(t * 1e6, 2)}
     if "attention" in groups:
         # GQA decode attention, 40 q / 8 kv heads, d 64
         wsa = ops.Workspace(64 << 20, device=dev)
         for bb in (1, 8):
             for L in (512, 4096, 32768):
+                # enough cache copies to pass the 256 MB Infinity Cache (each launch reads its
+                # K/V cold, as a decode step does), at least 8 launches per graph
                 kv_bytes = bb * 8 * L * 64 * 2 * 2
-                copies = max(1, min(8, (600 << 20) // kv_bytes))
+                copies = max(2, min(600, -(-(600 << 20) // kv_bytes)))
                 caches = [(torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16),
                            torch.randn(bb, 8, L, 64, device=dev, generator=gen).to(torch.bfloat16))
                           for _ in range(copies)]
                 q = torch.randn(bb, 40, 64, device=dev, generator=gen).to(torch.bfloat16)
                 lens = torch.full((bb,), L, dtype=torch.int32, device=dev)
                 o = torch.empty_like(q)
-                t = _graph_time(lambda: [ops.gqa_decode(q, kc, vc, lens, 0.125, out=o, ws=wsa)
-                                         for kc, vc in caches], 10) / copies
+                nl = max(8, copies)
+                t = _graph_time(lambda: [ops.gqa_decode(q, *caches[i % copies], lens, 0.125,
+                                                        out=o, ws=wsa)
+                                         for i in range(nl)], 10) / nl
                 out[f"gqa_decode_b{bb}_L{L}"] = {"us": round(t * 1e6, 2),
                                                  "GB/s": round(kv_bytes / t / 1e9, 1)}
                 del caches
