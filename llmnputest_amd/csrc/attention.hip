@@ -519,13 +519,24 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   attn_finish<G>(a, s_fin, s_buf, s_f, s_g, &s_last, bk, split, b, kvh);
 }
 
-// Splits per (sequence, kv head): enough workgroups to cover the GPU (about 512), at least
-// one round of positions each, at most 64 so the merge stays short.
-static int auto_split(int batch, int hkv, int max_len) {
+// Splits per (sequence, kv head), at least one round of positions each. VALU kernel: about
+// 512 workgroups, at most 64 splits. Matrix-core kernel (less work per round, so the split
+// merge weighs more): about four rounds per workgroup, between 192 and 512 workgroups, at most
+// 32 splits (two merge passes) -- measured at L = 2112: batch 1 17 splits, 2 12, 4 6, 8 5,
+// 16 4, each within 0.5 us of the best count; at L = 32768, batch 1 32 splits (21.4 us
+// against 25.1 with 64), batch 8 8 splits (within 3 % of the best).
+static int auto_split(int batch, int hkv, int max_len, bool mfma) {
   const int by_len = (max_len + kAttnRound - 1) / kAttnRound;
-  const int by_grid = (512 + batch * hkv - 1) / (batch * hkv);
+  const int bh = batch * hkv;
+  int target = 512;
+  if (mfma) {
+    const long long quarter = (long long)bh * by_len / 4;
+    target = quarter < 192 ? 192 : quarter > 512 ? 512 : (int)quarter;
+  }
+  const int by_grid = (target + bh - 1) / bh;
   int s = by_len < by_grid ? by_len : by_grid;
-  s = s > 64 ? 64 : s;
+  const int cap = mfma ? 32 : 64;
+  s = s > cap ? cap : s;
   return s < 1 ? 1 : s;
 }
 
@@ -555,7 +566,7 @@ int q4nx_set_attn_mfma(int on) {
 
 size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len) {
   if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1) return 0;
-  const int ns = auto_split(batch, n_kv_heads, max_len);
+  const int ns = auto_split(batch, n_kv_heads, max_len, false);   // the larger of the two
   if (ns == 1) return 0;
   return (size_t)Q4NX_WS_COUNTER_BYTES +
          partial_bytes(batch, n_kv_heads, ns, n_q_heads / n_kv_heads);
@@ -596,7 +607,7 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   a.scale_l2 = (float)((double)scale * 1.4426950408889634);
   Q4NX_REQUIRE(n_split >= 0 && n_split <= 4096, Q4NX_ERR_ARG, "%s: n_split=%d outside 0..4096",
                what, n_split);
-  a.n_split = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len);
+  a.n_split = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len, g_attn_mfma != 0);
   a.chunk = ((max_len + a.n_split - 1) / a.n_split + 7) & ~7;
   if (a.n_split > 1) {
     const int G = n_q_heads / n_kv_heads;

@@ -430,8 +430,13 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
     const int n_sum_waves = ks == 1 ? WM : W;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
+      float v[kMaxWaves];   // all loads first, then the sum in wave order
+#pragma unroll
+      for (int w = 0; w < kMaxWaves; ++w) v[w] = snorm[w][b];
       float s = 0.f;
-      for (int w = 0; w < n_sum_waves; ++w) s += snorm[w][b];
+#pragma unroll
+      for (int w = 0; w < kMaxWaves; ++w)
+        if (w < n_sum_waves) s += v[w];
       inv_rms[b] = 1.0f / sqrtf(s / (float)K + a.eps);
     }
   }
@@ -606,8 +611,15 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   for (int e = tid; e < a.G * B * 32; e += blockDim.x) {
     const int m = e / (B * 32), rest = e % (B * 32);
     const int b = rest >> 5, r = rest & 31;
+    // every wave's value read at once (not one LDS round trip per wave), then added in
+    // wave order
+    float v[kMaxWaves];
+#pragma unroll
+    for (int c = 0; c < kMaxWaves; ++c) v[c] = sred[min(m * WM + c, kMaxWaves - 1)][b][r];
     float s = 0.f;
-    for (int c = 0; c < WM; ++c) s += sred[m * WM + c][b][r];
+#pragma unroll
+    for (int c = 0; c < kMaxWaves; ++c)
+      if (c < WM) s += v[c];
     sgrp[b][m * 32 + r] = s;
   }
   __syncthreads();
