@@ -379,6 +379,7 @@ def cpu_baseline(sample_iters: int) -> dict | None:
         rg = cpu_oracle.run_ref_baseline(gate, INTER // 32, HIDDEN // 256, threads, sample_iters)
         rd = cpu_oracle.run_ref_baseline(down, HIDDEN // 32, INTER // 256, threads, sample_iters)
         t_layer = (2 * rg["gemv_ms"] + rd["gemv_ms"]) / 1e3
+        stream = rg["stream_gbs"]
         kind = "reference"
         sample = (f"cpu_baseline.cpp (reference source, AVX2) on gate 8192x2560 and down "
                   f"2560x8192 q4 tiles, {sample_iters} iterations each; per layer = 2*gate + down")
@@ -394,11 +395,30 @@ def cpu_baseline(sample_iters: int) -> dict | None:
             cpu_oracle.gemv(down, "q4", xd, HIDDEN // 32, INTER // 256, threads)
         td = (time.perf_counter() - s) / sample_iters
         t_layer = 2 * tg + td
+        stream = None
         kind = "port"
         sample = f"oracle/cpu_oracle.c fp64 GEMV, {sample_iters} iterations per shape"
-    return {"value": round((2 * b_gu + b_d) / t_layer / 1e9, 2), "unit": "GB/s",
-            "cores": threads, "kind": kind, "sample": sample,
-            "wall_s": round(time.time() - t0, 1)}
+    out = {"value": round((2 * b_gu + b_d) / t_layer / 1e9, 2), "unit": "GB/s",
+           "cores": threads, "kind": kind, "sample": sample}
+    if stream is not None:   # the reference binary's STREAM read of the same gate tiles
+        out["stream_read_GBs"] = stream
+    # the q8 lm_head 248320 x 1024 shape: the reference has no CPU q8 GEMV, so the oracle's
+    # threaded C port (float64) is timed, over a few iterations
+    n8, k8 = 248320, 1024
+    w8 = synth.q8_tiles(rng, n8, k8).reshape(-1)
+    x8 = synth.random_bf16(rng, k8)
+    cpu_oracle.gemv(w8, "q8", x8, n8 // 32, k8 // 256, threads)
+    it8 = 3
+    s = time.perf_counter()
+    for _ in range(it8):
+        cpu_oracle.gemv(w8, "q8", x8, n8 // 32, k8 // 256, threads)
+    t8 = (time.perf_counter() - s) / it8
+    out["lm_head_q8"] = {"value": round((w8.size + 2 * k8 + 4 * n8) / t8 / 1e9, 2),
+                         "unit": "GB/s", "kind": "port",
+                         "sample": f"oracle/cpu_oracle.c float64 GEMV on 248320x1024 q8 tiles, "
+                                   f"{it8} iterations"}
+    out["wall_s"] = round(time.time() - t0, 1)
+    return out
 
 
 def main() -> int:
