@@ -47,7 +47,7 @@ constexpr int kAttnSteps = 4;                              // 8-position steps p
 constexpr int kAttnRound = kAttnWaves * kAttnSteps * 8;    // positions per workgroup round
 constexpr int kAttnStates = kAttnWaves * 8;                // lane softmax states per WG
 constexpr int kPartStride = 68;                            // acc[64], m, l, 2 pad (16 B rows)
-constexpr int kMergeSplits = 30;   // splits merged per LDS pass (30 records fit s_acc)
+constexpr int kMergeSplits = 20;   // splits merged per pass (loads in flight per output)
 
 __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -127,13 +127,58 @@ __device__ __forceinline__ void attn_round(AttnLane<G>& st, const uint4 (&kr)[kA
   }
 }
 
+// One pass of the split merge for this thread's outputs (thread t owns outputs t, t + 256, ..
+// = (head e / 64, dim e % 64)): the (m, l, acc[dim]) of splits cs .. cs + ns - 1 (ns <= P),
+// all loaded at once (past ns the last record again, masked), then folded into the running
+// (M, L, A) in split order.
+template <int G, int P>
+__device__ __forceinline__ void attn_merge_pass(const float* recs, int cs, int ns,
+                                                float (&M)[(G * 64 + 255) / 256],
+                                                float (&L)[(G * 64 + 255) / 256],
+                                                float (&A)[(G * 64 + 255) / 256]) {
+  constexpr int kE = (G * 64 + 255) / 256;
+  float mv[kE][P], lv[kE][P], av[kE][P];
+#pragma unroll
+  for (int j = 0; j < kE; ++j) {
+    const int e = min((int)threadIdx.x + 256 * j, G * 64 - 1);
+    const int h = e >> 6, d = e & 63;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const float* r = recs + ((size_t)(cs + min(i, ns - 1)) * G + h) * kPartStride;
+      mv[j][i] = load_sys(r + 64);
+      lv[j][i] = load_sys(r + 65);
+      av[j][i] = load_sys(r + d);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kE; ++j) {
+    float Mn = M[j];
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (i < ns) Mn = fmaxf(Mn, mv[j][i]);
+    if (Mn != -INFINITY) {
+      const float g = ex2(M[j] - Mn);   // 0 while nothing was merged (M = -inf)
+      float Ln = L[j] * g, An = A[j] * g;
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (i < ns) {
+          const float f = ex2(mv[j][i] - Mn);
+          Ln = fmaf(lv[j][i], f, Ln);
+          An = fmaf(av[j][i], f, An);
+        }
+      M[j] = Mn;
+      L[j] = Ln;
+      A[j] = An;
+    }
+  }
+}
+
 // The end both kernels share. s_fin[h] holds the workgroup's (acc[64], m, l) for query head
 // h of the group. With one split that is the answer; otherwise the record is published and
 // the last workgroup of the (sequence, kv head) to arrive merges every split's record
-// exactly, in split order, through s_buf (kMergeSplits records per pass).
+// exactly, in split order (kMergeSplits records per pass).
 template <int G>
 __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kPartStride],
-                                            float* s_buf, float (*s_f)[kAttnStates], float* s_g,
                                             int* s_last, int bk, int split, int b, int kvh) {
   const int tid = threadIdx.x;
   if (a.n_split > 1) {
@@ -152,61 +197,33 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
     __syncthreads();
     if (!*s_last) return;
 
-    constexpr int kRec16 = G * kPartStride / 4;                     // uint4 per split record
-    constexpr int kPer = (kMergeSplits * kRec16 + 255) / 256;       // loads per thread per pass
-    const uint32_t base = (uint32_t)((size_t)bk * a.n_split) * rec_bytes;
-    // running merged state: s_fin[h][64] = M, s_fin[h][65] = L, thread (h, d) holds A
-    float Ar[2] = {0.f, 0.f};
-    if (tid < G) {
-      s_fin[tid][64] = -INFINITY;
-      s_fin[tid][65] = 0.f;
+    // every thread merges its own output columns over the split records, straight from
+    // memory: one round of loads per pass, no staging through LDS, no barriers
+    constexpr int kE = (G * 64 + 255) / 256;   // outputs per thread
+    const float* recs = a.partial + (size_t)bk * a.n_split * G * kPartStride;
+    float M[kE], L[kE], A[kE];
+#pragma unroll
+    for (int j = 0; j < kE; ++j) {
+      M[j] = -INFINITY;
+      L[j] = 0.f;
+      A[j] = 0.f;
     }
     for (int cs = 0; cs < a.n_split; cs += kMergeSplits) {
       const int ns = min(kMergeSplits, a.n_split - cs);
-      const uint32_t src = base + (uint32_t)cs * rec_bytes;
-      uint4 v[kPer];   // unconditional: past the buffer end the loads return 0
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) v[i] = ld16_sys(pr, src + (tid + i * 256) * 16);
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int e = tid + i * 256;
-        if (e < ns * kRec16) ((uint4*)s_buf)[e] = v[i];
-      }
-      __syncthreads();
-      if (tid < G * 32) {   // thread (h, split sp of the pass): weights in parallel
-        const int h = tid >> 5, sp = tid & 31;
-        const float ms = sp < ns ? s_buf[(sp * G + h) * kPartStride + 64] : -INFINITY;
-        const float ls = sp < ns ? s_buf[(sp * G + h) * kPartStride + 65] : 0.f;
-        const float Mh = group32_max(fmaxf(ms, s_fin[h][64]));   // s_fin[h][64]: running M
-        const float f = (Mh == -INFINITY) ? 0.f : ex2(ms - Mh);
-        const float Lp = group32_sum(ls * f);
-        s_f[h][sp] = f;
-        if (sp == 0) {
-          const float Mo = s_fin[h][64];
-          const float g = (Mo == -INFINITY) ? 0.f : ex2(Mo - Mh);
-          s_g[h] = g;
-          s_fin[h][65] = fmaf(s_fin[h][65], g, Lp);
-          s_fin[h][64] = Mh;
-        }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int e = tid + jj * 256;
-        if (e < G * 64) {
-          const int h = e >> 6, d = e & 63;
-          float As = Ar[jj] * s_g[h];
-          for (int sp = 0; sp < ns; ++sp)
-            As = fmaf(s_buf[(sp * G + h) * kPartStride + d], s_f[h][sp], As);
-          Ar[jj] = As;
-        }
-      }
-      __syncthreads();
+      if (ns <= 8) attn_merge_pass<G, 8>(recs, cs, ns, M, L, A);
+      else attn_merge_pass<G, kMergeSplits>(recs, cs, ns, M, L, A);
     }
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int e = tid + jj * 256;
-      if (e < G * 64) s_fin[e >> 6][e & 63] = Ar[jj];
+    for (int j = 0; j < kE; ++j) {
+      const int e = tid + 256 * j;
+      if (e < G * 64) {
+        const int h = e >> 6, d = e & 63;
+        s_fin[h][d] = A[j];
+        if (d == 0) {
+          s_fin[h][64] = M[j];
+          s_fin[h][65] = L[j];
+        }
+      }
     }
     if (tid == 0)  // ready for the next call
       __hip_atomic_store(&a.counters[bk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -226,12 +243,9 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
 template <int G>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
   static_assert(G * 32 <= 256, "one thread per (head, lane state)");
-  static_assert(kMergeSplits <= 32 && kMergeSplits * kPartStride <= kAttnStates * 64,
-                "a merge pass fits s_acc and one 32-lane group per head");
   __shared__ float s_m[G][kAttnStates], s_f[G][kAttnStates];
-  __shared__ __attribute__((aligned(16))) float s_acc[kAttnStates * G * 64];  // also merge buffer
+  __shared__ __attribute__((aligned(16))) float s_acc[kAttnStates * G * 64];
   __shared__ __attribute__((aligned(16))) float s_fin[G][kPartStride];
-  __shared__ float s_g[G];
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -309,7 +323,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  attn_finish<G>(a, s_fin, s_acc, s_f, s_g, &s_last, bk, split, b, kvh);
+  attn_finish<G>(a, s_fin, &s_last, bk, split, b, kvh);
 }
 
 // ---------------------------------------------------------------- matrix-core kernel
@@ -428,12 +442,9 @@ __device__ __forceinline__ void attn_mfma_round(MfmaLane& st, const u32x4_t (&kr
 template <int G>
 __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   static_assert(G * 32 <= 256 && G <= 16, "one thread per (head, split) in the merge");
-  static_assert(kAttnWaves * 64 <= kMergeSplits * kPartStride, "wave states fit s_buf");
-  __shared__ __attribute__((aligned(16))) float s_buf[kMergeSplits * G * kPartStride];
+  __shared__ __attribute__((aligned(16))) float s_o[kAttnWaves * G * 64];   // wave states
   __shared__ __attribute__((aligned(16))) float s_fin[G][kPartStride];
   __shared__ float s_wm[kAttnWaves][G], s_wl[kAttnWaves][G];
-  __shared__ float s_f[G][kAttnStates];
-  __shared__ float s_g[G];
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -482,7 +493,6 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   // ---- merge the four waves: l over each head's lane groups, then (m, l, O) through LDS
   st.l += __shfl_xor(st.l, 16);
   st.l += __shfl_xor(st.l, 32);
-  float* s_o = s_buf;   // [wave][head][64]
   if (j < G) {
     if (g == 0) {
       s_wm[wave][j] = st.m;
@@ -516,7 +526,7 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  attn_finish<G>(a, s_fin, s_buf, s_f, s_g, &s_last, bk, split, b, kvh);
+  attn_finish<G>(a, s_fin, &s_last, bk, split, b, kvh);
 }
 
 // Splits per (sequence, kv head), at least one round of positions each. VALU kernel: about
