@@ -322,10 +322,14 @@ def test_gqa_decode_splits(dev, apath, n_split):
     k = synth.random_bf16(rng, (2, 8, L, 64))
     v = synth.random_bf16(rng, (2, 8, L, 64))
     lens = np.array([L, 777], np.int32)
+    ws = ops.Workspace(8 << 20, device=dev)
     of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
-                        torch.from_numpy(lens).to(dev), 0.125, n_split=n_split, want_f32=True)[1]
+                        torch.from_numpy(lens).to(dev), 0.125, n_split=n_split, want_f32=True,
+                        ws=ws)[1]
     ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v), lens, 0.125)
     assert_close(of.cpu().numpy(), ref)
+    # the split arrival counters are back at zero for the next call on this workspace
+    assert not ws.buf[:ops.WS_COUNTER_BYTES].cpu().numpy().any()
 
 
 def test_gqa_decode_garbage_past_length(dev, apath):
