@@ -283,6 +283,16 @@ def secondary_bench(dev, groups=SECONDARY_GROUPS) -> dict:
         dst = torch.empty_like(src)
         t = _graph_time(lambda: dst.copy_(src), 5)
         out["copy_1GiB"] = {"us": round(t * 1e6, 1), "GB/s": round(2 * (1 << 30) / t / 1e9, 1)}
+        del src, dst
+        # the same copy at the size of one 2560->8192 q4 weight tensor (13,107,200 B read and
+        # written), 48 buffers rotated past the Infinity Cache: what a single launch of this
+        # size reaches, the per-launch reference for the GEMV
+        nb = q4_bytes(INTER, HIDDEN)
+        srcs = [torch.ones(nb // 4, dtype=torch.float32, device=dev) for _ in range(48)]
+        dsts = [torch.empty_like(x) for x in srcs]
+        t = _graph_time(lambda: [d.copy_(x) for d, x in zip(dsts, srcs)], 10) / len(srcs)
+        out["copy_13MB"] = {"us": round(t * 1e6, 2), "GB/s": round(2 * nb / t / 1e9, 1)}
+        del srcs, dsts
     return out
 
 
