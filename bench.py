@@ -455,8 +455,9 @@ def main() -> int:
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build runs the decode hot path on a single "
-              "MI355X and has no multi-GPU path (see DESIGN.md for how it would shard).",
+        print("bench.py measures one GPU: the decode hot path runs on a single MI355X and has "
+              "no multi-GPU path (every tile-row is independent, so q/k/v/gate/up would split "
+              "by tile-row and o/down by K with one 10 KB all-reduce per layer).",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():

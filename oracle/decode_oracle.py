@@ -187,7 +187,7 @@ def embed_rows(lm_head_raw: np.ndarray, tokens, vocab: int, hidden: int) -> np.n
 
 
 class DecodeOracle:
-    """Numpy decode step in the build's convention (module docstring). Pure float64 /
+    """Numpy decode step in the conventions of the module docstring. Pure float64 /
     float32 reference with bf16 narrowing at the same points as the GPU path; slow,
     meant for reduced layer counts in tests."""
 
