@@ -848,14 +848,22 @@ static size_t split_bytes(int n_groups, int G, int ks, int batch) {
   return (size_t)Q4NX_WS_COUNTER_BYTES + (size_t)n_groups * ks * batch * G * 32 * 4;
 }
 
+// K parts per group: plan_ksplit's choice, raised (up to 8) until one part fits in a
+// workgroup at this batch's wave budget (long K with more than two rows).
+static int plan_ksplit_fit(int n_groups, int G, int k_t, int batch) {
+  int ks = plan_ksplit(n_groups, G, k_t);
+  while (ks < 8 && ks < k_t && plan_tpw(G, (k_t + ks - 1) / ks, batch) == 0) ++ks;
+  return ks;
+}
+
 static size_t ws_need(int n_groups, int G, int k_t, int batch) {
-  return split_bytes(n_groups, G, plan_ksplit(n_groups, G, k_t), batch);
+  return split_bytes(n_groups, G, plan_ksplit_fit(n_groups, G, k_t, batch), batch);
 }
 
 static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char* what,
                   void* ws = nullptr, size_t ws_bytes = 0) {
   const int B = round_batch(a.batch);
-  int ks = plan_ksplit(n_groups, a.G, a.k_t);
+  int ks = plan_ksplit_fit(n_groups, a.G, a.k_t, a.batch);
   const size_t need = split_bytes(n_groups, a.G, ks, a.batch);
   if (ks > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256)))
     ks = 1;   // no (or too small a) workspace: one workgroup per group

@@ -221,3 +221,23 @@ def test_gemv_activation_range(dev, kpath, scale):
     ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
     rel, cos = qo.metrics(y, ref)
     assert rel < REL and cos > COS, (rel, cos)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("case", range(8))
+def test_gemv_random_shapes(dev, kpath, kind, case):
+    """Seeded random shapes off the usual grid (tile-row counts that do not fill a split,
+    single-tile and long K, odd batches; beyond 8 rows on the matrix cores): every row within
+    the bar of the float64 oracle."""
+    rng = np.random.default_rng(1000 + 17 * case + (kind == "q8"))
+    n_t = int(rng.integers(1, 200))
+    k_t = int(rng.choice([1, 2, 3, 5, 7, 10, 13, 32, 40]))
+    batch = int(rng.integers(1, 9 if kpath == "valu" else 41))
+    raw, rng2 = _tiles(kind, 32 * n_t, 256 * k_t, 2000 + case)
+    x = synth.random_bf16(rng2, (batch, 256 * k_t))
+    y = ops.gemv(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n_t, k_t).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n_t, k_t, acc=np.float64).reshape(batch, -1)
+    y = y.reshape(batch, -1)
+    for b in range(batch):
+        rel, cos = qo.metrics(y[b], ref[b])
+        assert rel < REL and cos > COS, (n_t, k_t, batch, b, rel, cos)
