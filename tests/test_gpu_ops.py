@@ -441,3 +441,31 @@ def test_layer_tail_equals_chain(dev, valu, batch):
     r = qo.bf16_to_f32(mlp_bits).astype(np.float64)
     ref_m = do.swiglu_from_raw(g, u)
     assert qo.metrics(r, ref_m)[1] > 0.9999      # xn may differ from the kernel's by 1 ulp
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_gqa_decode_random_shapes(dev, apath, case):
+    """Seeded random batches, head groupings, cache lengths, ragged lengths (including empty
+    and single-position sequences) and split counts, against the float64 oracle."""
+    rng = np.random.default_rng(500 + case)
+    batch = int(rng.integers(1, 13))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.integers(1, 9))
+    lmax = int(rng.integers(1, 3000))
+    lens = rng.integers(0, lmax + 1, batch).astype(np.int32)
+    lens[0] = min(lmax, 1 if case % 2 else lmax)
+    if batch > 1 and case % 3 == 0:
+        lens[-1] = 0
+    n_split = int(rng.choice([0, 0, 1, 3, 40]))
+    q = synth.random_bf16(rng, (batch, hq, 64))
+    k = synth.random_bf16(rng, (batch, hkv, lmax, 64))
+    v = synth.random_bf16(rng, (batch, hkv, lmax, 64))
+    of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
+                        torch.from_numpy(lens).to(dev), 0.125, n_split=n_split,
+                        want_f32=True)[1].cpu().numpy()
+    ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v),
+                           np.maximum(lens, 1), 0.125)   # empty rows are checked apart
+    empty = lens == 0
+    assert not of[empty].any()                           # no positions: zeros
+    if (~empty).any():
+        assert_close(of[~empty], ref[~empty])
