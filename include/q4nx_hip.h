@@ -97,6 +97,19 @@ int q4nx_gemv_ex(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const
                  int batch, float *y, int64_t y_stride, const float *residual, float *ssq_out,
                  uint64_t *argmax_keys, void *ws, size_t ws_bytes, void *stream);
 
+/* The o-projection of a batch-1 decode step fed straight from attention's split records:
+ * y = residual + W * bf16(merge(att_rec)), where merge(att_rec) is the attention output
+ * q4nx_gqa_decode would have written for the same records (same operations, same order:
+ * the results equal q4nx_gqa_decode followed by q4nx_gemv_ex bit for bit). W: q4 tiles
+ * [n_tile_rows][n_q_heads/4]; K = 64 * n_q_heads <= 2560; att_rec: the records of
+ * q4nx_gqa_decode_records at batch 1 (ws + Q4NX_WS_COUNTER_BYTES), n_split <= 18, which are
+ * only read; y, residual, ssq_out as in q4nx_gemv_ex. One workgroup per tile-row, no K
+ * split, no workspace. Fuses granite_attn_finish (granite_attention.h:193-212, 232-237) into the
+ * o-projection GEMV of designs/granite_gemv/granite_gemv.h:79-91. */
+int q4nx_gemv_attn_q4(const uint8_t *w, int n_tile_rows, const float *att_rec, int n_split,
+                      int n_q_heads, int n_kv_heads, float *y, const float *residual,
+                      float *ssq_out, void *stream);
+
 /* Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
 int q4nx_set_split_tiles(int tiles_per_wave);
 /* Tuning knob: workgroups per output group along K (1..8), 0 = automatic (split only
@@ -222,6 +235,28 @@ int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *
                     int n_kv_heads, int head_dim, const int32_t *lens, int max_len,
                     int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
                     void *ws, size_t ws_bytes, void *stream);
+/* The split count q4nx_gqa_decode chooses for n_split = 0 under the current policy knob
+ * (what q4nx_gqa_decode_records and q4nx_gemv_attn_q4 should be given for the same
+ * shape); 0 for an invalid shape. */
+int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len);
+/* The split count to give q4nx_gqa_decode_records when q4nx_gemv_attn_q4 merges the
+ * records: q4nx_gqa_decode_splits capped at 10 (every split is a record each o-projection
+ * workgroup reads, so the pair runs fastest with fewer, longer splits). */
+int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len);
+/* The first half of q4nx_gqa_decode: every split of every (b, kv head) writes its record
+ * (fp32 acc[64], m (log2 domain), l, 2 pad; 68 floats per q head) to the workspace at
+ * ws + Q4NX_WS_COUNTER_BYTES, laid out [b][kv head][split][head in group][68], and ends;
+ * nothing is merged, no counter is touched and no output is written. The second half is
+ * the merge in q4nx_gemv_attn_q4 (batch 1). n_split >= 1 must be given (records for
+ * n_split = 1 too). ws: Q4NX_WS_COUNTER_BYTES + B*Hkv*n_split*(Hq/Hkv)*68*4 bytes,
+ * 256-byte aligned. Splits granite_attn_block / granite_attn_finish
+ * (designs/granite_gemv/granite_attention.h:221-237) the way the reference does: the
+ * blocks publish partials, a separate step combines them. */
+int q4nx_gqa_decode_records(const uint16_t *q, const uint16_t *k_cache,
+                            const uint16_t *v_cache, int batch, int n_q_heads, int n_kv_heads,
+                            int head_dim, const int32_t *lens, int max_len,
+                            int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
+                            void *ws, size_t ws_bytes, void *stream);
 
 /* y[i] = bf16(x[i]), round to nearest even, NaN kept quiet: the device form of the bf16
  * rounding every kernel applies to its outputs (tools/q4nx.py:97-111 rounds the same way

@@ -54,6 +54,11 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_set_attn_mfma": (c_i, [c_i]),
     "q4nx_gqa_decode": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
                               c_i64, c_f, c_i, c_p, c_sz, c_p]),
+    "q4nx_gqa_decode_splits": (c_i, [c_i, c_i, c_i, c_i]),
+    "q4nx_gqa_decode_records_splits": (c_i, [c_i, c_i, c_i, c_i]),
+    "q4nx_gqa_decode_records": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
+                                      c_i64, c_f, c_i, c_p, c_sz, c_p]),
+    "q4nx_gemv_attn_q4": (c_i, [c_p, c_i, c_p, c_i, c_i, c_i, c_p, c_p, c_p, c_p]),
     "q4nx_round_bf16": (c_i, [c_p, c_p, c_i64, c_p]),
     "q4nx_embed_q8": (c_i, [c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
     "q4nx_argmax": (c_i, [c_p, c_i, c_i, c_i64, c_p, c_p, c_p]),

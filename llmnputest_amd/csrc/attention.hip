@@ -38,6 +38,7 @@ struct AttnArgs {
   float* partial;  // [b*hkv + kvh][n_split][G][kPartStride]
   uint32_t partial_bytes;
   unsigned* counters;
+  int publish_only;   // every split writes its record and ends; a later launch merges
 };
 
 typedef short bf16x2_t __attribute__((ext_vector_type(2)));
@@ -46,7 +47,7 @@ constexpr int kAttnWaves = 4;
 constexpr int kAttnSteps = 4;                              // 8-position steps per round
 constexpr int kAttnRound = kAttnWaves * kAttnSteps * 8;    // positions per workgroup round
 constexpr int kAttnStates = kAttnWaves * 8;                // lane softmax states per WG
-constexpr int kPartStride = 68;                            // acc[64], m, l, 2 pad (16 B rows)
+constexpr int kPartStride = kAttnRecFloats;                // acc[64], m, l, 2 pad (16 B rows)
 constexpr int kMergeSplits = 20;   // splits merged per pass (loads in flight per output)
 
 __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
@@ -181,13 +182,15 @@ template <int G>
 __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kPartStride],
                                             int* s_last, int bk, int split, int b, int kvh) {
   const int tid = threadIdx.x;
-  if (a.n_split > 1) {
-    // publish this split's (acc, m, l), then the last workgroup of (b, kv head) merges
+  if (a.publish_only || a.n_split > 1) {
+    // publish this split's (acc, m, l), then the last workgroup of (b, kv head) merges (or,
+    // publishing only, a later launch does)
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.partial, a.partial_bytes);
     const uint32_t rec_bytes = G * kPartStride * 4;
     const uint32_t rec = (uint32_t)((size_t)bk * a.n_split + split) * rec_bytes;
     for (int e = tid; e < G * kPartStride / 4; e += 256)
       st16_sys(pr, rec + e * 16, ((const uint4*)&s_fin[0][0])[e]);
+    if (a.publish_only) return;
     wait_vm();
     __syncthreads();
     if (tid == 0) {
@@ -582,13 +585,12 @@ size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int ma
          partial_bytes(batch, n_kv_heads, ns, n_q_heads / n_kv_heads);
 }
 
-int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+static int attn_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                     uint16_t* out, float* out_f32, int batch, int n_q_heads, int n_kv_heads,
                     int head_dim, const int32_t* lens, int max_len, int64_t kv_b_stride,
                     int64_t kv_h_stride, float scale, int n_split, void* ws, size_t ws_bytes,
-                    void* stream) {
-  const char* what = "q4nx_gqa_decode";
-  Q4NX_REQUIRE(q && k_cache && v_cache && lens && (out || out_f32), Q4NX_ERR_ARG,
+                    void* stream, bool publish_only, const char* what) {
+  Q4NX_REQUIRE(q && k_cache && v_cache && lens && (publish_only || out || out_f32), Q4NX_ERR_ARG,
                "%s: q, caches, lens and an output are required", what);
   Q4NX_REQUIRE(Q4NX_ALIGNED(q, 16) && Q4NX_ALIGNED(k_cache, 16) && Q4NX_ALIGNED(v_cache, 16),
                Q4NX_ERR_ARG, "%s: q and caches must be 16-byte aligned", what);
@@ -619,7 +621,8 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
                what, n_split);
   a.n_split = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len, g_attn_mfma != 0);
   a.chunk = ((max_len + a.n_split - 1) / a.n_split + 7) & ~7;
-  if (a.n_split > 1) {
+  a.publish_only = publish_only ? 1 : 0;
+  if (publish_only || a.n_split > 1) {
     const int G = n_q_heads / n_kv_heads;
     const size_t pb = partial_bytes(batch, n_kv_heads, a.n_split, G);
     Q4NX_REQUIRE(pb < (size_t)1 << 31, Q4NX_ERR_SHAPE, "%s: split partials exceed 2 GB", what);
@@ -646,6 +649,44 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
     default: launch_attn<8>(a, grid, s); break;
   }
   return check_launch(what);
+}
+
+int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                    uint16_t* out, float* out_f32, int batch, int n_q_heads, int n_kv_heads,
+                    int head_dim, const int32_t* lens, int max_len, int64_t kv_b_stride,
+                    int64_t kv_h_stride, float scale, int n_split, void* ws, size_t ws_bytes,
+                    void* stream) {
+  return attn_run(q, k_cache, v_cache, out, out_f32, batch, n_q_heads, n_kv_heads, head_dim,
+                  lens, max_len, kv_b_stride, kv_h_stride, scale, n_split, ws, ws_bytes, stream,
+                  false, "q4nx_gqa_decode");
+}
+
+int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len) {
+  if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1) return 0;
+  return auto_split(batch, n_kv_heads, max_len, g_attn_mfma != 0);
+}
+
+// Splits for records an o-projection merges: the attention policy's count, capped at 10.
+// Every split adds a record that each o-projection workgroup reads (0.16 us a split at the
+// 3B shape), so the pair is fastest with fewer, longer splits than attention alone: at one
+// sequence, 40 q / 8 kv heads and contexts 512-4000 the measured optimum was 6-12.
+constexpr int kRecordSplitCap = 10;
+
+int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len) {
+  const int ns = q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len);
+  return ns < kRecordSplitCap ? ns : kRecordSplitCap;
+}
+
+int q4nx_gqa_decode_records(const uint16_t* q, const uint16_t* k_cache,
+                            const uint16_t* v_cache, int batch, int n_q_heads, int n_kv_heads,
+                            int head_dim, const int32_t* lens, int max_len, int64_t kv_b_stride,
+                            int64_t kv_h_stride, float scale, int n_split, void* ws,
+                            size_t ws_bytes, void* stream) {
+  const char* what = "q4nx_gqa_decode_records";
+  Q4NX_REQUIRE(n_split >= 1, Q4NX_ERR_ARG, "%s: n_split=%d must be given (>= 1)", what, n_split);
+  return attn_run(q, k_cache, v_cache, nullptr, nullptr, batch, n_q_heads, n_kv_heads,
+                  head_dim, lens, max_len, kv_b_stride, kv_h_stride, scale, n_split, ws,
+                  ws_bytes, stream, true, what);
 }
 
 }  // extern "C"

@@ -89,6 +89,15 @@ __device__ __forceinline__ float load_sys(const float* p) {
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Attention split record: per (sequence, kv head, split, query head of the group) the fp32
+// acc[64] of the split's positions, its running max m (scale*log2e units) at [64], its sum l
+// at [65], two pad words; records of one (sequence, kv head) consecutive by split.
+constexpr int kAttnRecFloats = 68;
+// The o-projection that reads them directly (q4nx_gemv_attn_q4): at most this many splits and
+// K-tiles (one 640-thread workgroup per tile-row, four activations per thread).
+constexpr int kAttnRecMaxSplits = 18;
+constexpr int kAttnRecMaxKTiles = 10;
+
 // 16-byte system-coherent (sc0 sc1) loads and stores through a raw buffer resource over
 // [base, base + bytes): the compiler tracks their completion like any other load, and
 // out-of-range offsets read 0 / drop the store (the buffer unit's own bounds check).

@@ -91,6 +91,10 @@ struct GemvArgs {
   const unsigned* wait_cnt;
   unsigned wait_target;
   unsigned* err;
+  // o-projection from attention split records (batch 1): x[k] is the bf16 of head k / 64's
+  // output merged from att_split records at att_rec ([kv head][split][head in group][68])
+  const float* att_rec;
+  int att_split, att_g;
 };
 
 // Output stores: plain, or system-coherent when a later stage of the same launch reads them.
@@ -162,7 +166,9 @@ __device__ __forceinline__ void transpose_reduce4(const float (&v)[16], float (&
 
 // One work item (an output group, or one K part of it) of a GEMV launch. Returns true when
 // this workgroup ran the epilogue (for a split group, only the last part to arrive does).
-template <int KIND, int B, int TPW, bool SYS>
+// XNS > 0: the activations are attention split records to merge (see GemvArgs::att_rec),
+// at most XNS of them (one tile-row of one member, a wave per K-tile, no K split).
+template <int KIND, int B, int TPW, bool SYS, int XNS = 0>
 __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   constexpr int TB = KIND == 4 ? kQ4TileBytes : kQ8TileBytes;
   constexpr int NCH = KIND == 4 ? 4 : 8;              // 16-byte chunks per lane per tile
@@ -233,6 +239,9 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   constexpr int sys = SYS ? 1 : 0;
   float ep_res = 0.f;   // epilogue prefetches (see the end of load_acts)
   int ep_pos = 0;
+  constexpr bool XREC = XNS > 0;
+  float4 rec_acc[XREC ? XNS : 1];
+  float2 rec_ml[2];
   auto load_acts = [&]() {
     const void* xbase = norm ? (const void*)a.hres : (const void*)a.x;
     const uint32_t xbytes = (uint32_t)((size_t)a.batch * a.x_stride * (norm ? 4 : 2));
@@ -249,11 +258,31 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         if constexpr (SYS) {
           ar[b][t][0] = ld16_sys(xr_, off);
           ar[b][t][1] = ld16_sys(xr_, norm ? off + 16 : off);
-        } else {
+        } else if constexpr (!XREC) {
           const uint4* src = (const uint4*)((const uint8_t*)xbase + off);
           ar[b][t][0] = src[0];
           ar[b][t][1] = src[norm ? 1 : 0];
         }
+      }
+    }
+    // attention split records, ahead of the weights: the (m, l) pairs of this wave's four
+    // heads (4 x splits <= 72 pairs, two per lane) and this thread's four activations
+    // 4 tid .. 4 tid + 3 (one head) in every split (clamped: the last split again)
+    if constexpr (XREC) {
+      const int e0 = 4 * tid, h = e0 >> 6, kvh = h / a.att_g, hh = h - kvh * a.att_g;
+      const float* r0 = a.att_rec + ((size_t)kvh * a.att_split * a.att_g + hh) * kAttnRecFloats;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int p = min(lane + 64 * j, 4 * a.att_split - 1);
+        const int ph = 4 * wave + p / a.att_split, pi = p % a.att_split, pk = ph / a.att_g;
+        rec_ml[j] = *(const float2*)(a.att_rec +
+                                     (((size_t)pk * a.att_split + pi) * a.att_g + ph - pk * a.att_g) *
+                                         kAttnRecFloats + 64);
+      }
+#pragma unroll
+      for (int i = 0; i < XNS; ++i) {
+        const float* r = r0 + (size_t)min(i, a.att_split - 1) * a.att_g * kAttnRecFloats;
+        rec_acc[i] = *(const float4*)(r + (e0 & 63));
       }
     }
     // RMSNorm sum of squares handed over by the producer of x: K/32 partials per row,
@@ -327,6 +356,54 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   if (staged) {
     stage_wait(a.wait_cnt, a.wait_target, a.err);
     load_acts();
+  }
+
+  // attention records -> the bf16 activations: wave w owns K-tile w (heads 4w .. 4w + 3),
+  // so each wave merges exactly the 256 activations it uses, and its (m, l) pairs and merged
+  // row pass through its own slice of LDS (in order within the wave: no workgroup barrier).
+  // Each thread merges its four in split order with the operations of the attention
+  // kernel's last workgroup, so the row is the one that kernel would have written.
+  if constexpr (XREC) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[kAttnRecMaxKTiles * kTileK];
+    __shared__ float2 s_ml[kAttnRecMaxKTiles][4 * kAttnRecMaxSplits];   // [wave][head][split]
+    const int ns = a.att_split;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)   // past the end: the last pair again, the same value
+      s_ml[wave][min(lane + 64 * j, 4 * ns - 1)] = rec_ml[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float2* ml = &s_ml[wave][(lane >> 4) * ns];   // this thread's head
+    float2 mv[XNS];
+#pragma unroll
+    for (int i = 0; i < XNS; ++i) mv[i] = ml[min(i, ns - 1)];
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < XNS; ++i)
+      if (i < ns) M = fmaxf(M, mv[i].x);
+    float L = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < XNS; ++i)
+        if (i < ns) {
+          const float f = __builtin_amdgcn_exp2f(mv[i].x - M);
+          L = fmaf(mv[i].y, f, L);
+          A0 = fmaf(rec_acc[i].x, f, A0);
+          A1 = fmaf(rec_acc[i].y, f, A1);
+          A2 = fmaf(rec_acc[i].z, f, A2);
+          A3 = fmaf(rec_acc[i].w, f, A3);
+        }
+    }
+    const float o0 = L > 0.f ? A0 / L : 0.f, o1 = L > 0.f ? A1 / L : 0.f;
+    const float o2 = L > 0.f ? A2 / L : 0.f, o3 = L > 0.f ? A3 / L : 0.f;
+    *(uint2*)(s_x + 4 * tid) = make_uint2(
+        (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16),
+        (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    ar[0][0][0] = *(const uint4*)(s_x + kt0 * kTileK + kx);   // kt0 = wave
+    ar[0][0][1] = ar[0][0][0];
   }
 
   // the activations are used from here on (their waits come after the weight stream)
@@ -760,6 +837,14 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
   (void)gemv_body<KIND, B, TPW, false>(a, blockIdx.x);
 }
 
+// The o-projection from attention split records: batch 1, one K-tile per wave, at most
+// kAttnRecMaxKTiles waves (the launch bound leaves room for the records in registers), at
+// most XNS splits (loads are issued for XNS; the launch picks the next even bucket).
+template <int XNS>
+__global__ __launch_bounds__(64 * kAttnRecMaxKTiles) void gemv_attn_kernel(GemvArgs a) {
+  (void)gemv_body<4, 1, 1, false, XNS>(a, blockIdx.x);
+}
+
 // A chain of GEMV stages in one launch: stage s owns workgroups [wg_begin[s], wg_begin[s+1])
 // and (after the first) waits until every item of stage s-1 is done before reading its
 // activations; its weights are already streaming by then. Workgroups are dispatched in
@@ -1170,6 +1255,61 @@ int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const
   return gemv_plain(kind, w, x, norm_w, eps, ssq_in, y, n_tile_rows, k_tiles, batch, x_stride,
                     y_stride, residual, ssq_out, (unsigned long long*)argmax_keys, stream,
                     "q4nx_gemv_ex", ws, ws_bytes);
+}
+
+int q4nx_gemv_attn_q4(const uint8_t* w, int n_tile_rows, const float* att_rec, int n_split,
+                      int n_q_heads, int n_kv_heads, float* y, const float* residual,
+                      float* ssq_out, void* stream) {
+  const char* what = "q4nx_gemv_attn_q4";
+  Q4NX_REQUIRE(n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0 &&
+                   n_q_heads % 4 == 0,
+               Q4NX_ERR_SHAPE, "%s: n_q_heads=%d must be a multiple of 4 and of n_kv_heads=%d",
+               what, n_q_heads, n_kv_heads);
+  const int k_tiles = n_q_heads / 4;   // K = 64 per head
+  Q4NX_REQUIRE(k_tiles <= kAttnRecMaxKTiles, Q4NX_ERR_SHAPE,
+               "%s: %d query heads, at most %d (the merged row stays in one workgroup)", what,
+               n_q_heads, 4 * kAttnRecMaxKTiles);
+  int rc = check_common(w, n_tile_rows, k_tiles, 1, what);
+  if (rc) return rc;
+  Q4NX_REQUIRE(att_rec != nullptr && Q4NX_ALIGNED(att_rec, 16), Q4NX_ERR_ARG,
+               "%s: the split records must be a non-null 16-byte aligned device pointer", what);
+  Q4NX_REQUIRE(n_split >= 1 && n_split <= kAttnRecMaxSplits, Q4NX_ERR_SHAPE,
+               "%s: n_split=%d outside 1..%d", what, n_split, kAttnRecMaxSplits);
+  Q4NX_REQUIRE(y != nullptr && Q4NX_ALIGNED(y, 4), Q4NX_ERR_ARG,
+               "%s: y must be a 4-byte aligned device pointer", what);
+  Q4NX_REQUIRE(ssq_out == nullptr || Q4NX_ALIGNED(ssq_out, 4), Q4NX_ERR_ARG,
+               "%s: ssq_out must be 4-byte aligned", what);
+  GemvArgs a{};
+  a.w[0] = w;
+  a.n_tr[0] = n_tile_rows;
+  a.op = OP_PLAIN;
+  a.G = 1;
+  a.k_t = k_tiles;
+  a.batch = 1;
+  a.x = (const uint16_t*)att_rec;   // not read: the row is merged from the records
+  a.x_stride = k_tiles * kTileK;
+  a.y = y;
+  a.y_stride = n_tile_rows * 32;
+  a.residual = residual;
+  a.ssq_out = ssq_out;
+  a.ksplit = 1;
+  a.att_rec = att_rec;
+  a.att_split = n_split;
+  a.att_g = n_q_heads / n_kv_heads;
+  const dim3 grid(n_tile_rows), block(64 * k_tiles);
+  hipStream_t st = (hipStream_t)stream;
+  switch ((n_split + 1) / 2) {   // record loads for the next even count of splits
+    case 1: hipLaunchKernelGGL(gemv_attn_kernel<2>, grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(gemv_attn_kernel<4>, grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL(gemv_attn_kernel<6>, grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL(gemv_attn_kernel<8>, grid, block, 0, st, a); break;
+    case 5: hipLaunchKernelGGL(gemv_attn_kernel<10>, grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL(gemv_attn_kernel<12>, grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL(gemv_attn_kernel<14>, grid, block, 0, st, a); break;
+    case 8: hipLaunchKernelGGL(gemv_attn_kernel<16>, grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL(gemv_attn_kernel<18>, grid, block, 0, st, a); break;
+  }
+  return check_launch(what);
 }
 
 size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {

@@ -7,13 +7,16 @@ groups the projections by shared input:
 
     [RMSNorm, q, k, v, RoPE, KV append]   q4nx_qkv_rope (norm fused as the prologue)
     [GQA flash-decode attention]          q4nx_gqa_decode
-    [o, residual add]                     q4nx_gemv_q4 (residual epilogue, in place)
+    [o, residual add]                     q4nx_gemv_ex (residual epilogue, in place)
     [RMSNorm, gate, up, SwiGLU]           q4nx_gate_up_swiglu (norm fused)
-    [down, residual add]                  q4nx_gemv_q4
+    [down, residual add]                  q4nx_gemv_ex
 
-then one q8 lm_head launch (final RMSNorm fused as its prologue, the greedy argmax folded
-into its epilogue as a 64-bit atomic max) and one bookkeeping launch that turns the argmax
-into the next token and advances positions. A whole step is captured once in a HIP graph
+At one sequence the attention launch only publishes its split records
+(q4nx_gqa_decode_records) and the o-projection merges them in its prologue
+(q4nx_gemv_attn_q4), which gives the same bits sooner. Then one q8 lm_head launch (final
+RMSNorm fused as its prologue, one order-preserving (max, row) key per tile-row in its
+epilogue) and one bookkeeping launch that reduces the keys to the next token and advances
+positions. A whole step is captured once in a HIP graph
 and replayed; the greedy loop never leaves the device.
 
 Conventions (the reference fixes none of them): fp32 residual stream, pre-norm
@@ -172,13 +175,18 @@ class GraniteDecoder:
     greedy loop on the device from a HIP graph of one step."""
 
     def __init__(self, weights: GraniteWeights, max_batch: int = 1, max_len: int = 4096,
-                 device="cuda", fused_tail: bool = False):
+                 device="cuda", fused_tail: bool = False, fused_attn_o: bool = True,
+                 attn_splits: int = 0):
         c = weights.cfg
         self.cfg, self.w = c, weights
         # o-proj + MLP of a layer as one three-stage launch (q4nx_layer_tail) instead of three.
         # Off by default: measured slower on MI355X (the stages' cross-XCD hand-offs cost
         # more than the weight streams they overlap).
         self.fused_tail = fused_tail
+        # batch 1: attention only publishes its split records and the o-projection merges
+        # them in its prologue (q4nx_gemv_attn_q4), saving attention's cross-workgroup merge
+        self.fused_attn_o = fused_attn_o
+        self.attn_splits = attn_splits   # 0: the library's policy for the path taken
         self.dev = torch.device(device)
         self.max_batch = max_batch
         self.max_len = (max_len + 63) // 64 * 64
@@ -206,6 +214,14 @@ class GraniteDecoder:
         self.calls = 0
         self.seconds = 0.0
 
+    def fuses_attn_o(self, b: int, n_split: int) -> bool:
+        """Whether a step of b sequences runs attention's merge inside the o-projection
+        (q4nx_gemv_attn_q4: one sequence, at most 18 splits, the attention row of at most 40
+        heads held by one workgroup)."""
+        c = self.cfg
+        return (self.fused_attn_o and not self.fused_tail and b == 1 and 1 <= n_split <= 18
+                and c.n_q % 4 == 0 and c.n_q <= 40)
+
     # ------------------------------------------------------------ one step, eager
     def _launch_step(self, b: int) -> None:
         """Every kernel of one decode step for the first b sequences (no allocation)."""
@@ -213,21 +229,31 @@ class GraniteDecoder:
         kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
         h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
         ssq = self.ssq[:b]
+        n_split = self.attn_splits or ops.gqa_decode_records_splits(b, c.n_q, c.n_kv,
+                                                                    self.max_len)
+        fuse_o = self.fuses_attn_o(b, n_split)
         ops.embed_q8(w.lm_head, self.tokens[:b], c.vocab, c.hidden, out=h, ssq_out=ssq)
         for li, L in enumerate(w.layers):
             kc, vc = self.k_cache[li], self.v_cache[li]
             ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
                          kc, vc, q_out=q, norm_w=L["norm_in"], eps=c.eps, ws=self.ws,
                          ssq_in=ssq)
-            ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
-                           max_len=self.max_len, out=attn, ws=self.ws)
+            if fuse_o:
+                rec = ops.gqa_decode_records(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b],
+                                             n_split, c.scale, max_len=self.max_len, ws=self.ws)
+                ops.gemv_attn_q4(L["o"], c.hidden // 32, rec, residual=h, out=h, ssq_out=ssq)
+            else:
+                ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
+                               max_len=self.max_len, n_split=self.attn_splits, out=attn,
+                               ws=self.ws)
             if self.fused_tail:   # o-proj, norm + gate/up + SwiGLU, down: one launch
                 ops.layer_tail(L["o"], L["gate"], L["up"], L["down"], c.hidden, c.q_dim, c.inter,
                                attn.view(b, c.q_dim), h, ssq, L["norm_post"], c.eps, mlp,
                                ws=self.ws)
                 continue
-            ops.gemv_ex(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q, residual=h,
-                        out=h, ssq_out=ssq, ws=self.ws)
+            if not fuse_o:
+                ops.gemv_ex(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q,
+                            residual=h, out=h, ssq_out=ssq, ws=self.ws)
             ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
                                norm_w=L["norm_post"], eps=c.eps, ws=self.ws, ssq_in=ssq)
             ops.gemv_ex(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h,

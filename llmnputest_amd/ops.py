@@ -411,6 +411,67 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return (out, of) if want_f32 else out
 
 
+def gqa_decode_splits(batch: int, n_q_heads: int, n_kv_heads: int, max_len: int) -> int:
+    """The split count `gqa_decode` chooses for n_split=0 under the current kernel policy."""
+    return int(_lib.lib().q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len))
+
+
+def gqa_decode_records_splits(batch: int, n_q_heads: int, n_kv_heads: int,
+                              max_len: int) -> int:
+    """The split count for records that `gemv_attn_q4` merges (the attention policy's, capped
+    at 10: fewer, longer splits make the pair faster)."""
+    return int(_lib.lib().q4nx_gqa_decode_records_splits(batch, n_q_heads, n_kv_heads, max_len))
+
+
+def gqa_decode_records(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       lens: torch.Tensor, n_split: int, scale: float = 0.125,
+                       max_len: int | None = None, ws: Workspace | None = None) -> torch.Tensor:
+    """The publishing half of `gqa_decode`: every split writes its (acc[64], m, l) record and
+    nothing is merged. Returns the records, an fp32 view of the workspace shaped
+    [B, Hkv, n_split, Hq/Hkv, 68] (valid until the workspace is next used)."""
+    _dev(q, "q", torch.bfloat16)
+    _dev(lens, "lens", torch.int32)
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.stride(3) != 1 or t.stride(2) != 64:
+            raise ValueError(f"{n} must be a bf16 device tensor [B, Hkv, Lmax, 64] with "
+                             f"contiguous rows")
+    if n_split < 1:
+        raise ValueError("n_split must be >= 1 (see gqa_decode_splits)")
+    b, hq, d = q.shape
+    hkv, lmax = k_cache.shape[1], k_cache.shape[2]
+    max_len = lmax if max_len is None else min(max_len, lmax)
+    g = hq // hkv
+    pb = b * hkv * n_split * g * 68 * 4
+    ws = ws or default_workspace()
+    wp, wn = ws.get(WS_COUNTER_BYTES + pb)
+    _lib.call("q4nx_gqa_decode_records", _ptr(q), _ptr(k_cache), _ptr(v_cache), b, hq, hkv, d,
+              _ptr(lens), max_len, k_cache.stride(0), k_cache.stride(1), float(scale),
+              int(n_split), wp, wn, _stream())
+    return ws.buf[WS_COUNTER_BYTES:WS_COUNTER_BYTES + pb].view(torch.float32).view(
+        b, hkv, n_split, g, 68)
+
+
+def gemv_attn_q4(tiles: torch.Tensor, n_tile_rows: int, records: torch.Tensor,
+                 residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 ssq_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Batch-1 o-projection from attention split records: y = residual + W bf16(merge(records)),
+    equal bit for bit to `gqa_decode` followed by `gemv_ex`. records: fp32
+    [1, Hkv, n_split, Hq/Hkv, 68] from `gqa_decode_records`; W: q4 tiles, K = 64 Hq."""
+    _dev(records, "records", torch.float32)
+    if records.dim() != 5 or records.shape[0] != 1 or records.shape[4] != 68:
+        raise ValueError("records must be [1, Hkv, n_split, Hq/Hkv, 68] (gqa_decode_records)")
+    _, hkv, ns, g, _ = records.shape
+    hq = hkv * g
+    _tiles(tiles, "q4", n_tile_rows, hq // 4)
+    n = n_tile_rows * 32
+    if out is None:
+        out = torch.empty((1, n), dtype=torch.float32, device=records.device)
+    _ssq(ssq_out, "ssq_out", 1, n_tile_rows)
+    _lib.call("q4nx_gemv_attn_q4", _ptr(tiles), n_tile_rows, _ptr(records), ns, hq, hkv,
+              _ptr(out), _ptr(residual), _ptr(ssq_out), _stream())
+    return out
+
+
 # ---------------------------------------------------------------- decode helpers
 
 def embed_q8(tiles: torch.Tensor, tokens: torch.Tensor, vocab: int, hidden: int,

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+from llmnputest_amd import ops
 from llmnputest_amd.granite import GraniteConfig, GraniteDecoder, GraniteWeights
 from oracle import cpu_oracle
 from oracle import decode_oracle as do
@@ -76,6 +77,27 @@ def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new, fused):
         for b in range(batch):
             check_step(got[b], ref[b], int(toks[b, i]))
         prev = toks[:, i]
+
+
+@pytest.mark.parametrize("ctx", [300, 2100])
+def test_fused_attn_o_equals_unfused(dev, apath, ctx):
+    """Batch 1 with attention's merge in the o-projection prologue decodes the same tokens with
+    bit-identical logits as attention merging on its own at the same split count."""
+    cfg = GraniteConfig(n_layers=2)
+    w = GraniteWeights.synthetic(cfg, seed=41, device=dev)
+    n_split = ops.gqa_decode_records_splits(1, cfg.n_q, cfg.n_kv, ctx + 64)
+    assert 1 <= n_split <= ops.gqa_decode_splits(1, cfg.n_q, cfg.n_kv, ctx + 64)
+    out = []
+    for fused in (True, False):   # the same split count on both paths
+        dec = GraniteDecoder(w, max_batch=1, max_len=ctx + 64, device=dev, fused_attn_o=fused,
+                             attn_splits=n_split)
+        assert dec.fuses_attn_o(1, n_split) == fused
+        dec.seed_cache(ctx, seed=42)
+        out.append(dec.generate([77], [ctx], 3, record_logits=True))
+    (t_f, l_f), (t_u, l_u) = out
+    assert np.array_equal(t_f, t_u)
+    for a, b in zip(l_f, l_u):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
 
 
 @pytest.mark.parametrize("fused", [False, True])

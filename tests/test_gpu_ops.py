@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from llmnputest_amd import ops, synth
+from llmnputest_amd._lib import Q4NXError
 from oracle import decode_oracle as do
 from oracle import q4nx_oracle as qo
 
@@ -377,6 +378,80 @@ def test_embed_and_argmax(dev):
     logits[1, 5000] = logits[1, 7000] = 99.0         # first maximum wins
     idx = ops.argmax(torch.from_numpy(logits).to(dev)).cpu().numpy()
     assert idx.tolist() == np.argmax(logits, axis=1).tolist()
+
+
+@pytest.mark.parametrize("hq,hkv,L,lmax,n_split,n_out", [
+    (40, 8, 2112, 2176, 17, 2560),   # the 3B decode shape at the automatic split count
+    (40, 8, 2112, 2176, 18, 2560),   # the most splits the merge holds
+    (40, 8, 300, 320, 1, 512),       # one split still publishes a record
+    (32, 8, 1000, 1024, 5, 512),
+    (8, 8, 40, 64, 18, 256),         # splits past the length: records with m = -inf, l = 0
+    (16, 2, 0, 64, 3, 512),          # empty sequence: zeros into the projection
+    (4, 1, 700, 768, 7, 256),        # one K-tile, four heads sharing one kv head
+    (40, 40, 500, 512, 2, 512)])     # no grouping
+def test_attn_records_o_proj_equals_chain(dev, apath, hq, hkv, L, lmax, n_split, n_out):
+    """Attention publishing split records, then the o-projection merging them in its prologue,
+    gives bit for bit what attention with its own merge followed by the o-projection GEMV
+    gives (y and the per-tile-row sums of squares); the records merge to the oracle's
+    attention output."""
+    rng = np.random.default_rng(hq * 1000 + L + n_split)
+    q = synth.random_bf16(rng, (1, hq, 64))
+    k = synth.random_bf16(rng, (1, hkv, lmax, 64))
+    v = synth.random_bf16(rng, (1, hkv, lmax, 64))
+    wo = synth.q4_tiles(rng, n_out, hq * 64).reshape(-1)
+    h0 = (rng.standard_normal((1, n_out)) * 3).astype(np.float32)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    qd, kd, vd, W = bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev), d(wo)
+    lens = torch.tensor([L], dtype=torch.int32, device=dev)
+    ws = ops.Workspace(1 << 20, device=dev)
+    nt = n_out // 32
+
+    attn, af = ops.gqa_decode(qd, kd, vd, lens, 0.125, n_split=n_split, want_f32=True, ws=ws)
+    h_c = d(h0)
+    ss_c = torch.zeros((1, nt), dtype=torch.float32, device=dev)
+    ops.gemv_ex(W, "q4", attn.view(1, hq * 64), nt, hq // 4, residual=h_c, out=h_c,
+                ssq_out=ss_c, ws=ws)
+
+    rec = ops.gqa_decode_records(qd, kd, vd, lens, n_split, 0.125, ws=ws)
+    assert rec.shape == (1, hkv, n_split, hq // hkv, 68)
+    h_f = d(h0)
+    ss_f = torch.zeros((1, nt), dtype=torch.float32, device=dev)
+    ops.gemv_attn_q4(W, nt, rec, residual=h_f, out=h_f, ssq_out=ss_f)
+    torch.cuda.synchronize()
+    assert np.array_equal(h_f.cpu().numpy().view(np.uint32), h_c.cpu().numpy().view(np.uint32))
+    assert np.array_equal(ss_f.cpu().numpy().view(np.uint32), ss_c.cpu().numpy().view(np.uint32))
+    # the records themselves hold the attention: merged on the host in float64
+    r = rec.cpu().numpy().astype(np.float64)[0]             # [hkv][split][g][68]
+    m, l_, acc = r[..., 64], r[..., 65], r[..., :64]
+    mx = m.max(axis=1, keepdims=True)
+    f = np.where(np.isfinite(m), np.exp2(m - np.where(np.isfinite(mx), mx, 0.0)), 0.0)
+    lt = (l_ * f).sum(axis=1)
+    at = (acc * f[..., None]).sum(axis=1)
+    o = np.where(lt[..., None] > 0, at / np.where(lt > 0, lt, 1.0)[..., None], 0.0)
+    o = o.reshape(1, hq, 64)
+    if L == 0:
+        assert not o.any() and not af.cpu().numpy().any()
+    else:
+        ref = do.gqa_attention(qo.bf16_to_f32(q), qo.bf16_to_f32(k), qo.bf16_to_f32(v),
+                               np.array([L], np.int32), 0.125)
+        assert_close(o, ref)
+    # and the projection of the attention row is the oracle's GEMV of it
+    ref_y = h0 + qo.gemv(wo.reshape(-1, 5120), "q4", bits(attn).reshape(1, -1), nt, hq // 4,
+                         acc=np.float64).reshape(1, n_out)
+    assert_close(h_f.cpu().numpy(), ref_y)
+
+
+def test_attn_records_o_proj_rejects(dev):
+    """Shapes the fused o-projection does not hold are refused before any launch."""
+    rng = np.random.default_rng(7)
+    W = torch.from_numpy(synth.q4_tiles(rng, 256, 44 * 64).reshape(-1)).to(dev)
+    rec = torch.zeros((1, 4, 3, 11, 68), dtype=torch.float32, device=dev)
+    with pytest.raises(Q4NXError, match="query heads"):
+        ops.gemv_attn_q4(W, 8, rec)               # 44 heads: the row needs 11 K-tiles
+    W = torch.from_numpy(synth.q4_tiles(rng, 256, 40 * 64).reshape(-1)).to(dev)
+    rec = torch.zeros((1, 8, 19, 5, 68), dtype=torch.float32, device=dev)
+    with pytest.raises(Q4NXError, match="n_split"):
+        ops.gemv_attn_q4(W, 8, rec)               # 19 splits: more than the merge holds
 
 
 # ------------------------------------------------------------------ fused layer tail
