@@ -361,22 +361,30 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 }
 
 // K rows (tile t, dims half c) and the 8-byte V pieces of one wave's 32 positions from p0;
-// positions at or past `stop` read row 0 instead (masked later).
+// positions at or past `stop` read row 0 instead (masked later). NT: streaming (non-temporal)
+// loads, for launches whose K/V is too large to stay in the caches.
+template <bool NT>
 __device__ __forceinline__ void attn_mfma_load(const uint16_t* kbase, const uint16_t* vbase,
                                                int p0, int stop, int j, int g,
                                                u32x4_t (&kr)[4], uint2 (&vr)[8]) {
+  typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int pos = p0 + 16 * t + j;
     const size_t row = (size_t)(pos < stop ? pos : 0) * 64;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) kr[2 * t + c] = *(const u32x4_t*)(kbase + row + 32 * c + 8 * g);
+    for (int c = 0; c < 2; ++c) {
+      const u32x4_t* p = (const u32x4_t*)(kbase + row + 32 * c + 8 * g);
+      kr[2 * t + c] = NT ? __builtin_nontemporal_load(p) : *p;
+    }
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int pos = p0 + 16 * (e >> 2) + 4 * g + (e & 3);
     const size_t row = (size_t)(pos < stop ? pos : 0) * 64;
-    vr[e] = *(const uint2*)(vbase + row + 4 * j);
+    const u32x2_v* p = (const u32x2_v*)(vbase + row + 4 * j);
+    const u32x2_v v2 = NT ? __builtin_nontemporal_load(p) : *p;
+    vr[e] = make_uint2(v2.x, v2.y);
   }
 }
 
@@ -442,7 +450,7 @@ __device__ __forceinline__ void attn_mfma_round(MfmaLane& st, const u32x4_t (&kr
   }
 }
 
-template <int G>
+template <int G, bool NT>
 __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   static_assert(G * 32 <= 256 && G <= 16, "one thread per (head, split) in the merge");
   __shared__ __attribute__((aligned(16))) float s_o[kAttnWaves * G * 64];   // wave states
@@ -465,10 +473,14 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   const uint16_t* vbase = a.v + head_off;
   const int wo = wave * 32;
 
-  // first round's K/V, q and the length all in flight together
-  u32x4_t kA[4], kB[4];
-  uint2 vA[8], vB[8];
-  attn_mfma_load(kbase, vbase, start + wo, stop, j, g, kA, vA);
+  // the first two rounds' K/V, q and the length all in flight together; three buffers, so
+  // that two rounds are in flight while one is computed (one wave per SIMD at long
+  // contexts: nothing else hides a round's latency)
+  u32x4_t kA[4], kB[4], kC[4];
+  uint2 vA[8], vB[8], vC[8];
+  attn_mfma_load<NT>(kbase, vbase, start + wo, stop, j, g, kA, vA);
+  if (stop - start > kAttnRound)   // a second round exists (known before the length is)
+    attn_mfma_load<NT>(kbase, vbase, start + kAttnRound + wo, stop, j, g, kB, vB);
   MfmaLane st;
   {
     const uint16_t* qrow = a.q + ((size_t)b * a.hq + kvh * G + (j < G ? j : 0)) * 64;
@@ -485,12 +497,14 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   for (int u = 0; u < 4; ++u) st.o[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int end = min(stop, max(0, a.lens[b]));
   const int nr = end > start ? (end - start + kAttnRound - 1) / kAttnRound : 0;
-  for (int r = 0; r < nr; r += 2) {
-    const int r0 = start + r * kAttnRound;
-    if (r + 1 < nr) attn_mfma_load(kbase, vbase, r0 + kAttnRound + wo, stop, j, g, kB, vB);
-    attn_mfma_round(st, kA, vA, r0 + wo, end, g, a.scale_l2);
-    if (r + 2 < nr) attn_mfma_load(kbase, vbase, r0 + 2 * kAttnRound + wo, stop, j, g, kA, vA);
-    if (r + 1 < nr) attn_mfma_round(st, kB, vB, r0 + kAttnRound + wo, end, g, a.scale_l2);
+  for (int r = 0; r < nr; r += 3) {
+    const int p0 = start + r * kAttnRound + wo;   // this wave's first position of round r
+    if (r + 2 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 2 * kAttnRound, stop, j, g, kC, vC);
+    attn_mfma_round(st, kA, vA, p0, end, g, a.scale_l2);
+    if (r + 3 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 3 * kAttnRound, stop, j, g, kA, vA);
+    if (r + 1 < nr) attn_mfma_round(st, kB, vB, p0 + kAttnRound, end, g, a.scale_l2);
+    if (r + 4 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 4 * kAttnRound, stop, j, g, kB, vB);
+    if (r + 2 < nr) attn_mfma_round(st, kC, vC, p0 + 2 * kAttnRound, end, g, a.scale_l2);
   }
 
   // ---- merge the four waves: l over each head's lane groups, then (m, l, O) through LDS
@@ -557,7 +571,11 @@ static int g_attn_mfma = 1;   // 1: matrix-core kernel, 0: VALU kernel
 
 template <int G>
 static void launch_attn(const AttnArgs& a, dim3 grid, hipStream_t s) {
-  if (g_attn_mfma) hipLaunchKernelGGL(gqa_mfma_kernel<G>, grid, dim3(256), 0, s, a);
+  // K/V of 64 MB or more per launch streams past the caches (measured: batch 8 at 32768
+  // positions 101 -> 93 us); smaller launches, decode's included, keep cached loads
+  const bool nt = (size_t)a.batch * a.hkv * a.max_len * 256 >= ((size_t)64 << 20);
+  if (g_attn_mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
+  else if (g_attn_mfma) hipLaunchKernelGGL((gqa_mfma_kernel<G, false>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(gqa_decode_kernel<G>, grid, dim3(256), 0, s, a);
 }
 

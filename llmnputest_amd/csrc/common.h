@@ -126,6 +126,16 @@ __device__ __forceinline__ void pin(float4& v) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w) : : "memory");
 }
 
+// v + (v of lane ^ 16), in every lane, with no LDS round trip: v_permlane16_swap exchanges
+// the odd 16-lane rows of its first operand with the even rows of its second, so with v in
+// both the two results hold rows (v0, v0, v2, v2) and (v1, v1, v3, v3). The sum is the same
+// in both lanes of a pair (addition commutes), as with a shuffle.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // DPP lane exchanges (a VALU operand modifier, no LDS traffic).
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
@@ -154,10 +164,7 @@ __device__ __forceinline__ float group32_max(float v) {
   v = group16_max(v);
   return fmaxf(v, __shfl_xor(v, 16));
 }
-__device__ __forceinline__ float group32_sum(float v) {
-  v = group16_sum(v);
-  return v + __shfl_xor(v, 16);
-}
+__device__ __forceinline__ float group32_sum(float v) { return xor16_sum(group16_sum(v)); }
 
 // Sum / max over the wave: DPP inside each row of 16 lanes, then the four row results read
 // into scalars and combined in a fixed order (every lane gets the same value).

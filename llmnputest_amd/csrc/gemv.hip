@@ -275,9 +275,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       for (int j = 0; j < 2; ++j) {
         const int p = min(lane + 64 * j, 4 * a.att_split - 1);
         const int ph = 4 * wave + p / a.att_split, pi = p % a.att_split, pk = ph / a.att_g;
-        rec_ml[j] = *(const float2*)(a.att_rec +
-                                     (((size_t)pk * a.att_split + pi) * a.att_g + ph - pk * a.att_g) *
-                                         kAttnRecFloats + 64);
+        const size_t rec = ((size_t)pk * a.att_split + pi) * a.att_g + ph - pk * a.att_g;
+        rec_ml[j] = *(const float2*)(a.att_rec + rec * kAttnRecFloats + 64);
       }
 #pragma unroll
       for (int i = 0; i < XNS; ++i) {
@@ -678,7 +677,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       float v = acc[b][i];
       v += dpp<kDppRor4>(v);      // kb 0..3 of the row of 16 (lane bits 2-3)
       v += dpp<kDppRor8>(v);
-      v += __shfl_xor(v, 16);     // kb 4..7
+      v = xor16_sum(v);           // kb 4..7
       if ((lane & 28) == 0) sred[wave][b][rb * 16 + q * 4 + i] = v * sc;
     }
   }
@@ -699,7 +698,9 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       if (c < WM) s += v[c];
     sgrp[b][m * 32 + r] = s;
   }
-  __syncthreads();
+  // a plain launch of one tile-row per group, K unsplit, reads each group sum back in the
+  // thread that wrote it (the same e = tid + i * blockDim mapping below): no barrier
+  if (!(a.op == OP_PLAIN && a.G == 1 && ks == 1)) __syncthreads();
 
   // ---- 7b. split K: publish this part, the last workgroup of the group adds all parts
   if (ks > 1) {
