@@ -87,6 +87,40 @@ def test_fused_and_attention_argument_errors():
     assert rc == ERR_ARG
 
 
+def test_attention_record_splits_and_errors():
+    """Split policies (host-only queries) and the argument checks of the attention records and
+    the o-projection that merges them, which all return before any launch."""
+    lib = _lib.lib()
+    fake = C.c_void_p(0x10000)
+    for lmax, auto in ((640, 5), (2176, 17), (4160, 24)):   # the 3B decode shapes
+        assert lib.q4nx_gqa_decode_splits(1, 40, 8, lmax) == auto
+        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, lmax) == min(auto, 10)
+    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 32
+    prev = lib.q4nx_set_attn_mfma(0)
+    try:                                                     # VALU policy: up to 64 splits
+        assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 64
+        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, 32768) == 10
+    finally:
+        lib.q4nx_set_attn_mfma(prev)
+    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 0) == 0       # invalid shapes: 0
+    assert lib.q4nx_gqa_decode_records_splits(0, 40, 8, 64) == 0
+    rc, msg = rc_msg("q4nx_gqa_decode_records", fake, fake, fake, 1, 40, 8, 64, fake, 512,
+                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 0, fake, 1 << 20, None)
+    assert rc == ERR_ARG and "n_split" in msg               # the count must be given
+    rc, msg = rc_msg("q4nx_gqa_decode_records", fake, fake, fake, 1, 40, 8, 64, fake, 512,
+                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 4, fake, 4096, None)
+    assert rc == ERR_WS and "workspace" in msg              # 4 splits need 64 KB + 43,520 B
+    rc, msg = rc_msg("q4nx_gemv_attn_q4", fake, 80, fake, 10, 44, 4, fake, None, None, None)
+    assert rc == ERR_SHAPE and "query heads" in msg         # 11 K-tiles
+    rc, msg = rc_msg("q4nx_gemv_attn_q4", fake, 80, fake, 10, 40, 7, fake, None, None, None)
+    assert rc == ERR_SHAPE                                   # 40 % 7 != 0
+    rc, msg = rc_msg("q4nx_gemv_attn_q4", fake, 80, fake, 19, 40, 8, fake, None, None, None)
+    assert rc == ERR_SHAPE and "n_split" in msg             # more than the merge holds
+    rc, msg = rc_msg("q4nx_gemv_attn_q4", fake, 80, C.c_void_p(0x10008), 10, 40, 8, fake, None,
+                     None, None)
+    assert rc == ERR_ARG and "16-byte" in msg               # misaligned records
+
+
 def test_gemm_argument_errors():
     fake = C.c_void_p(0x10000)
     rc, msg = rc_msg("q4nx_gemm", 3, fake, 8, 10, fake, 2560, 4, fake, 256, None, None, 0, None)
