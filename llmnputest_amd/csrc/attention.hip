@@ -547,23 +547,30 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
 }
 
 // Splits per (sequence, kv head), at least one round of positions each. VALU kernel: about
-// 512 workgroups, at most 64 splits. Matrix-core kernel (less work per round, so the split
-// merge weighs more): about four rounds per workgroup, between 192 and 512 workgroups, at most
-// 32 splits (two merge passes) -- measured at L = 2112: batch 1 17 splits, 2 12, 4 6, 8 5,
-// 16 4, each within 0.5 us of the best count; at L = 32768, batch 1 32 splits (21.4 us
-// against 25.1 with 64), batch 8 8 splits (within 3 % of the best).
+// 512 workgroups, at most 64 splits.
 static int auto_split(int batch, int hkv, int max_len, bool mfma) {
-  const int by_len = (max_len + kAttnRound - 1) / kAttnRound;
+  const int by_len = (max_len + kAttnRound - 1) / kAttnRound;   // rounds per (b, kv head)
   const int bh = batch * hkv;
-  int target = 512;
   if (mfma) {
-    const long long quarter = (long long)bh * by_len / 4;
-    target = quarter < 192 ? 192 : quarter > 512 ? 512 : (int)quarter;
+    // A split's rounds pipeline through its three K/V buffers, and each split adds a record
+    // to the merge: a split per round while the whole launch is short, then two rounds per
+    // split up to 16 splits, 16 splits up to 128 rounds, then a split per 8 rounds up to 32;
+    // at most 512 workgroups. Swept on MI355X at batch 1 and 8, 40 q / 8 kv heads,
+    // L = 512-32768: within 5 % of the best count everywhere (batch 1, L = 4096: 16 splits,
+    // 9.5 us against 10.9 us with the earlier policy's 24).
+    const long long total = (long long)bh * by_len;
+    int s;
+    if (by_len <= 8 && total <= 256) s = by_len;
+    else if (by_len <= 128) s = (by_len + 1) / 2 < 16 ? (by_len + 1) / 2 : 16;
+    else s = by_len / 8;
+    const int by_grid = 512 / bh;
+    s = s > by_grid ? by_grid : s;
+    s = s > 32 ? 32 : s;
+    return s < 1 ? 1 : s;
   }
-  const int by_grid = (target + bh - 1) / bh;
+  const int by_grid = (512 + bh - 1) / bh;
   int s = by_len < by_grid ? by_len : by_grid;
-  const int cap = mfma ? 32 : 64;
-  s = s > cap ? cap : s;
+  s = s > 64 ? 64 : s;
   return s < 1 ? 1 : s;
 }
 

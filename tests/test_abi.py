@@ -92,7 +92,7 @@ def test_attention_record_splits_and_errors():
     the o-projection that merges them, which all return before any launch."""
     lib = _lib.lib()
     fake = C.c_void_p(0x10000)
-    for lmax, auto in ((640, 5), (2176, 17), (4160, 24)):   # the 3B decode shapes
+    for lmax, auto in ((640, 5), (2176, 9), (4160, 16)):   # the 3B decode shapes
         assert lib.q4nx_gqa_decode_splits(1, 40, 8, lmax) == auto
         assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, lmax) == min(auto, 10)
     assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 32
