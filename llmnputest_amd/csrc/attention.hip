@@ -406,8 +406,7 @@ __device__ __forceinline__ void attn_mfma_round(MfmaLane& st, const u32x4_t (&kr
   float mr = sc[0];
 #pragma unroll
   for (int e = 1; e < 8; ++e) mr = fmaxf(mr, sc[e]);
-  mr = fmaxf(mr, __shfl_xor(mr, 16));
-  mr = fmaxf(mr, __shfl_xor(mr, 32));
+  mr = xor32_max(xor16_max(mr));   // no LDS round trips (the swaps are VALU)
   const float mn = fmaxf(st.m, mr);
   const float mb = mn == -INFINITY ? 0.f : mn;   // nothing seen yet: every p and corr is 0
   const float corr = ex2(st.m - mb);
@@ -508,8 +507,7 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   }
 
   // ---- merge the four waves: l over each head's lane groups, then (m, l, O) through LDS
-  st.l += __shfl_xor(st.l, 16);
-  st.l += __shfl_xor(st.l, 32);
+  st.l = xor32_sum(xor16_sum(st.l));
   if (j < G) {
     if (g == 0) {
       s_wm[wave][j] = st.m;
