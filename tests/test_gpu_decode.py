@@ -57,7 +57,8 @@ def check_step(got, ref, token):
 
 @pytest.mark.parametrize("n_layers,batch,ctx,n_new,fused", [(2, 1, 256, 6, False),
                                                             (1, 3, 100, 3, False),
-                                                            (2, 1, 200, 3, True)])
+                                                            (2, 1, 200, 3, True),
+                                                            (2, 1, 2100, 2, False)])
 def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new, fused):
     cfg = GraniteConfig(n_layers=n_layers)
     w = GraniteWeights.synthetic(cfg, seed=11, device=dev)
