@@ -296,6 +296,29 @@ def test_gqa_decode_uniform_softmax(dev, apath):
     assert_close(of.cpu().numpy(), expect)
 
 
+def test_gqa_decode_uniform_full_size(dev, apath):
+    """The largest attention config (batch 8, 32768 positions, 40 q / 8 kv heads: 537 MB of
+    K/V, the streaming-load variant) through a closed form: K constant along the positions
+    makes the softmax uniform, so each output is the mean of V over its sequence's length
+    (ragged lengths, including one position)."""
+    b, hq, hkv, L = 8, 40, 8, 32768
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(81)
+    q = torch.randn(b, hq, 64, device=dev, generator=gen).to(torch.bfloat16)
+    krow = torch.randn(b, hkv, 1, 64, device=dev, generator=gen).to(torch.bfloat16)
+    k = krow.expand(b, hkv, L, 64).contiguous()
+    v = torch.randn(b, hkv, L, 64, device=dev, generator=gen).to(torch.bfloat16)
+    lens = torch.tensor([L, 1, 4095, 20000, 32767, 129, 8192, 30001], dtype=torch.int32,
+                        device=dev)
+    of = ops.gqa_decode(q, k, v, lens, 0.125, want_f32=True)[1]
+    ref = torch.empty((b, hq, 64), dtype=torch.float64, device=dev)
+    for i in range(b):
+        m = v[i, :, :int(lens[i])].double().mean(dim=1)          # [hkv, 64]
+        ref[i] = m.repeat_interleave(hq // hkv, dim=0)
+    assert_close(of.cpu().numpy(), ref.cpu().numpy())
+    del k, v
+
+
 @pytest.mark.parametrize("hq,hkv,L", [(8, 8, 300), (16, 2, 1500), (64, 8, 700), (24, 8, 129)])
 def test_gqa_decode_group_sizes(dev, apath, hq, hkv, L):
     """Other query-group sizes (1, 8, 8, 3 query heads per kv head), called twice on one
