@@ -80,6 +80,28 @@ def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new, fused):
         prev = toks[:, i]
 
 
+def test_full_granite_step_vs_oracle(dev):
+    """The full granite-3B-shaped decode (40 layers, q8 lm_head 2560->100352, batch 1, context
+    2048, the default kernels and fusions) against the CPU oracle for two greedy tokens."""
+    cfg = GraniteConfig()
+    assert cfg.n_layers == 40
+    w = GraniteWeights.synthetic(cfg, seed=91, device=dev)
+    ctx, n_new = 2048, 2
+    dec = GraniteDecoder(w, max_batch=1, max_len=ctx + n_new, device=dev)
+    dec.seed_cache(ctx, seed=92)
+    kc = [host_bits(t) for t in dec.k_cache]
+    vc = [host_bits(t) for t in dec.v_cache]
+    first = np.array([4242], np.int32)
+    start = np.array([ctx], np.int32)
+    toks, logits = dec.generate(first, start, n_new, record_logits=True)
+    oracle = do.DecodeOracle(host_copy(w), kc, vc, dec.max_len, gemv=cpu_oracle.gemv)
+    prev = first
+    for i in range(n_new):
+        ref = oracle.step(prev, start + i)
+        check_step(logits[i].cpu().numpy()[0], ref[0], int(toks[0, i]))
+        prev = toks[:, i]
+
+
 @pytest.mark.parametrize("ctx", [300, 2100])
 def test_fused_attn_o_equals_unfused(dev, apath, ctx):
     """Batch 1 with attention's merge in the o-projection prologue decodes the same tokens with
