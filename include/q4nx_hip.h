@@ -240,7 +240,7 @@ int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *
  * shape); 0 for an invalid shape. */
 int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len);
 /* The split count to give q4nx_gqa_decode_records when q4nx_gemv_attn_q4 merges the
- * records: q4nx_gqa_decode_splits capped at 10 (every split is a record each o-projection
+ * records: q4nx_gqa_decode_splits capped at 12 (every split is a record each o-projection
  * workgroup reads, so the pair runs fastest with fewer, longer splits). */
 int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len);
 /* The first half of q4nx_gqa_decode: every split of every (b, kv head) writes its record

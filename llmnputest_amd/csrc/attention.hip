@@ -689,11 +689,12 @@ int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len
   return auto_split(batch, n_kv_heads, max_len, g_attn_mfma != 0);
 }
 
-// Splits for records an o-projection merges: the attention policy's count, capped at 10.
+// Splits for records an o-projection merges: the attention policy's count, capped at 12.
 // Every split adds a record that each o-projection workgroup reads (0.16 us a split at the
-// 3B shape), so the pair is fastest with fewer, longer splits than attention alone: at one
-// sequence, 40 q / 8 kv heads and contexts 512-4000 the measured optimum was 6-12.
-constexpr int kRecordSplitCap = 10;
+// 3B shape), so the pair is fastest with fewer, longer splits than attention alone: decode
+// at one sequence, 40 q / 8 kv heads, measured best at 5 (context 512), 9 (2048) and 12
+// (4000) splits.
+constexpr int kRecordSplitCap = 12;
 
 int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len) {
   const int ns = q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len);

@@ -419,7 +419,7 @@ def gqa_decode_splits(batch: int, n_q_heads: int, n_kv_heads: int, max_len: int)
 def gqa_decode_records_splits(batch: int, n_q_heads: int, n_kv_heads: int,
                               max_len: int) -> int:
     """The split count for records that `gemv_attn_q4` merges (the attention policy's, capped
-    at 10: fewer, longer splits make the pair faster)."""
+    at 12: fewer, longer splits make the pair faster)."""
     return int(_lib.lib().q4nx_gqa_decode_records_splits(batch, n_q_heads, n_kv_heads, max_len))
 
 

@@ -94,12 +94,12 @@ def test_attention_record_splits_and_errors():
     fake = C.c_void_p(0x10000)
     for lmax, auto in ((640, 5), (2176, 9), (4160, 16)):   # the 3B decode shapes
         assert lib.q4nx_gqa_decode_splits(1, 40, 8, lmax) == auto
-        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, lmax) == min(auto, 10)
+        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, lmax) == min(auto, 12)
     assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 32
     prev = lib.q4nx_set_attn_mfma(0)
     try:                                                     # VALU policy: up to 64 splits
         assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 64
-        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, 32768) == 10
+        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, 32768) == 12
     finally:
         lib.q4nx_set_attn_mfma(prev)
     assert lib.q4nx_gqa_decode_splits(1, 40, 8, 0) == 0       # invalid shapes: 0
