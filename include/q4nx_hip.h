@@ -110,7 +110,10 @@ int q4nx_gemv_attn_q4(const uint8_t *w, int n_tile_rows, const float *att_rec, i
                       int n_q_heads, int n_kv_heads, float *y, const float *residual,
                       float *ssq_out, void *stream);
 
-/* Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
+/* The q4nx_set_* knobs are process-wide atomics: a launch reads each knob it uses once, so
+ * setting one while another thread launches is safe and that launch sees the old or the new
+ * value, never a mix.
+ * Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
 int q4nx_set_split_tiles(int tiles_per_wave);
 /* Tuning knob: workgroups per output group along K (1..8), 0 = automatic (split only
  * launches with too few groups to fill the GPU, when a large enough workspace is given).

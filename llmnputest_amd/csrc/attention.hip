@@ -19,6 +19,7 @@
 // saw (p.v in fp32) and the 32 lane states of the workgroup are merged once, in parallel,
 // through LDS. Scores are scaled by scale*log2(e) so the softmax is exp2.
 
+#include <atomic>
 #include <math.h>
 
 #include "common.h"
@@ -572,15 +573,17 @@ static int auto_split(int batch, int hkv, int max_len, bool mfma) {
   return s < 1 ? 1 : s;
 }
 
-static int g_attn_mfma = 1;   // 1: matrix-core kernel, 0: VALU kernel
+// 1: matrix-core kernel, 0: VALU kernel. Process-wide; a launch reads it once, so its split
+// policy and its kernel always agree.
+static std::atomic<int> g_attn_mfma{1};
 
 template <int G>
-static void launch_attn(const AttnArgs& a, dim3 grid, hipStream_t s) {
+static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) {
   // K/V of 64 MB or more per launch streams past the caches (measured: batch 8 at 32768
   // positions 101 -> 93 us); smaller launches, decode's included, keep cached loads
   const bool nt = (size_t)a.batch * a.hkv * a.max_len * 256 >= ((size_t)64 << 20);
-  if (g_attn_mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
-  else if (g_attn_mfma) hipLaunchKernelGGL((gqa_mfma_kernel<G, false>), grid, dim3(256), 0, s, a);
+  if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
+  else if (mfma) hipLaunchKernelGGL((gqa_mfma_kernel<G, false>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(gqa_decode_kernel<G>, grid, dim3(256), 0, s, a);
 }
 
@@ -595,9 +598,7 @@ using namespace q4nx;
 extern "C" {
 
 int q4nx_set_attn_mfma(int on) {
-  const int prev = g_attn_mfma;
-  g_attn_mfma = on ? 1 : 0;
-  return prev;
+  return g_attn_mfma.exchange(on ? 1 : 0);
 }
 
 size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len) {
@@ -642,7 +643,8 @@ static int attn_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   a.scale_l2 = (float)((double)scale * 1.4426950408889634);
   Q4NX_REQUIRE(n_split >= 0 && n_split <= 4096, Q4NX_ERR_ARG, "%s: n_split=%d outside 0..4096",
                what, n_split);
-  a.n_split = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len, g_attn_mfma != 0);
+  const bool mfma = g_attn_mfma.load(std::memory_order_relaxed) != 0;
+  a.n_split = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len, mfma);
   a.chunk = ((max_len + a.n_split - 1) / a.n_split + 7) & ~7;
   a.publish_only = publish_only ? 1 : 0;
   if (publish_only || a.n_split > 1) {
@@ -662,14 +664,14 @@ static int attn_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   const dim3 grid((unsigned)(batch * n_kv_heads * a.n_split));
   hipStream_t s = (hipStream_t)stream;
   switch (n_q_heads / n_kv_heads) {
-    case 1: launch_attn<1>(a, grid, s); break;
-    case 2: launch_attn<2>(a, grid, s); break;
-    case 3: launch_attn<3>(a, grid, s); break;
-    case 4: launch_attn<4>(a, grid, s); break;
-    case 5: launch_attn<5>(a, grid, s); break;
-    case 6: launch_attn<6>(a, grid, s); break;
-    case 7: launch_attn<7>(a, grid, s); break;
-    default: launch_attn<8>(a, grid, s); break;
+    case 1: launch_attn<1>(a, mfma, grid, s); break;
+    case 2: launch_attn<2>(a, mfma, grid, s); break;
+    case 3: launch_attn<3>(a, mfma, grid, s); break;
+    case 4: launch_attn<4>(a, mfma, grid, s); break;
+    case 5: launch_attn<5>(a, mfma, grid, s); break;
+    case 6: launch_attn<6>(a, mfma, grid, s); break;
+    case 7: launch_attn<7>(a, mfma, grid, s); break;
+    default: launch_attn<8>(a, mfma, grid, s); break;
   }
   return check_launch(what);
 }
@@ -686,7 +688,7 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
 
 int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len) {
   if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1) return 0;
-  return auto_split(batch, n_kv_heads, max_len, g_attn_mfma != 0);
+  return auto_split(batch, n_kv_heads, max_len, g_attn_mfma.load(std::memory_order_relaxed) != 0);
 }
 
 // Splits for records an o-projection merges: the attention policy's count, capped at 12.

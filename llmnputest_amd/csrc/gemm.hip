@@ -25,6 +25,7 @@
 // across workgroups publishes parts with system-scope stores and the last arriver adds them
 // in part order, as the GEMV does, so results are bit-reproducible.
 
+#include <atomic>
 #include "common.h"
 #include "gemm.h"
 
@@ -448,7 +449,7 @@ struct GemmPlan {
   int rt, mt, wk, ksplit, kpp, mb, m_blocks, groups;
 };
 
-static int g_gemm_ksplit = 0;   // 0: automatic
+static std::atomic<int> g_gemm_ksplit{0};   // 0: automatic; process-wide, read once per launch
 
 // Workgroup shape by row count: up to 16 rows the four waves split K; more rows go to more
 // waves and, past 32, two m-tiles per wave. Past 64 rows (prefill) a workgroup takes two
@@ -477,8 +478,9 @@ static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows) {
   p.m_blocks = (m_rows + p.mb - 1) / p.mb;
   const int wgs = p.groups * p.m_blocks;
   int ks = 1;
-  if (g_gemm_ksplit > 0) {
-    ks = g_gemm_ksplit;
+  const int forced = g_gemm_ksplit.load(std::memory_order_relaxed);
+  if (forced > 0) {
+    ks = forced;
   } else if (wgs < 192 && k_t >= 4) {
     ks = (240 + wgs - 1) / wgs;
     const int cap = k_t / 2;                 // >= 2 K-tiles per workgroup
@@ -526,10 +528,10 @@ static void gemm_launch_op(const GemmArgs& a, const GemmPlan& p, hipStream_t st)
 
 // Rows from which the GEMV entry points run on the matrix cores, per kind (0: never).
 // Measured on MI355X: q4 from 2 rows (one row is as fast on the VALU kernel), q8 from one.
-static int g_mfma_rows[2] = {2, 1};
+static std::atomic<int> g_mfma_rows[2] = {{2}, {1}};
 
 bool mfma_use(int kind, int rows) {
-  const int t = g_mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0];
+  const int t = g_mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0].load(std::memory_order_relaxed);
   return t > 0 && rows >= t;
 }
 

@@ -36,6 +36,7 @@
 //   128 * sum(x). The Q4_1 minimum factors out of the K sum (granite_gemv.h:19-29):
 //   y_r += d_r * sum(c x) + m_r * sum(x) per 32-K group.
 
+#include <atomic>
 #include "common.h"
 #include "gemm.h"
 
@@ -881,7 +882,7 @@ __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_multi_kernel(MultiGe
 
 // ------------------------------------------------------------------ host side
 
-static int g_tiles_per_wave = 0;
+static std::atomic<int> g_tiles_per_wave{0};   // process-wide
 
 static int round_batch(int batch) { return batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : 8; }
 
@@ -889,7 +890,8 @@ static int round_batch(int batch) { return batch <= 1 ? 1 : batch <= 2 ? 2 : bat
 // (16 waves for batch <= 2, 8 above); 1, 2 or 4.
 static int plan_tpw(int G, int k_t, int batch) {
   const int max_waves = round_batch(batch) <= 2 ? kMaxWaves : kMaxWaves / 2;
-  int tpw = g_tiles_per_wave > 0 ? g_tiles_per_wave : (G * k_t + max_waves - 1) / max_waves;
+  const int forced = g_tiles_per_wave.load(std::memory_order_relaxed);
+  int tpw = forced > 0 ? forced : (G * k_t + max_waves - 1) / max_waves;
   tpw = tpw <= 1 ? 1 : tpw <= 2 ? 2 : tpw <= 4 ? 4 : 0;
   if (tpw && G * ((k_t + tpw - 1) / tpw) > max_waves) tpw = 0;
   return tpw;  // 0: K too long for one workgroup
@@ -909,7 +911,7 @@ static void launch_b(const GemvArgs& a, int tpw, int blocks, int threads, hipStr
   }
 }
 
-static int g_ksplit = 0;   // 0: automatic
+static std::atomic<int> g_ksplit{0};   // 0: automatic; process-wide
 
 // Workgroups per group along K: enough groups x parts to fill the GPU (about 240
 // workgroups) when a launch has few output groups of many tiles (a group of 10 tiles
@@ -917,8 +919,9 @@ static int g_ksplit = 0;   // 0: automatic
 // K-tiles per part, at most 8.
 static int plan_ksplit(int n_groups, int G, int k_t) {
   int ks;
-  if (g_ksplit > 0) {
-    ks = g_ksplit;
+  const int forced_ks = g_ksplit.load(std::memory_order_relaxed);
+  if (forced_ks > 0) {
+    ks = forced_ks;
   } else {
     if (n_groups >= 192 || G * k_t < 20) return 1;
     ks = (240 + n_groups - 1) / n_groups;
