@@ -121,6 +121,40 @@ def test_attention_record_splits_and_errors():
     assert rc == ERR_ARG and "16-byte" in msg               # misaligned records
 
 
+def test_attn_policy_knob_is_atomic():
+    """q4nx_set_attn_mfma exchanges the process-wide setting and returns the one it replaced;
+    setters and split queries racing from several threads (ctypes drops the GIL in the call)
+    leave every query with one policy whole: 32 (matrix cores) or 64 (VALU) splits at 32768
+    positions. Host-only calls, no launch."""
+    import threading
+    lib = _lib.lib()
+    prev = lib.q4nx_set_attn_mfma(1)
+    try:
+        assert lib.q4nx_set_attn_mfma(0) == 1
+        assert lib.q4nx_set_attn_mfma(0) == 0
+        assert lib.q4nx_set_attn_mfma(7) == 0                  # any nonzero value means on
+        assert lib.q4nx_set_attn_mfma(1) == 1
+        seen = set()
+
+        def worker(i):
+            for n in range(2000):
+                if (i + n) % 2:
+                    lib.q4nx_set_attn_mfma(n & 1)
+                else:
+                    seen.add(lib.q4nx_gqa_decode_splits(1, 40, 8, 32768))
+
+        threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert seen and seen <= {32, 64}
+        lib.q4nx_set_attn_mfma(1)
+        assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 32
+    finally:
+        lib.q4nx_set_attn_mfma(prev)
+
+
 def test_gemm_argument_errors():
     fake = C.c_void_p(0x10000)
     rc, msg = rc_msg("q4nx_gemm", 3, fake, 8, 10, fake, 2560, 4, fake, 256, None, None, 0, None)
