@@ -18,8 +18,14 @@ Conventions the reference leaves open and the build fixes:
     (designs/granite_gemv/granite_mlp_full.py:231-237);
   * GQA maps q head h to kv head h // (Hq // Hkv);
   * decode step (no token loop exists in the reference): fp32 residual stream,
-    pre-norm Llama/Granite order, final RMSNorm, tied q8 lm_head whose dequantised
-    row t is also the embedding of token t.
+    pre-norm Llama/Granite order, final RMSNorm, a q8 or q4 lm_head; the embedding of
+    token t is row t of a stored embedding matrix when the model has one, else row t of
+    the dequantised (tied) lm_head.
+
+`DecodeOracle(narrow=False)` runs the same step with every bf16 narrowing point removed
+(float64 throughout); that mode is what the composition is pinned with: it must equal a
+float64 transformers Llama decoder built from the same dequantised weights
+(tests/test_decode_oracle_cpu.py).
 """
 
 from __future__ import annotations
@@ -160,7 +166,9 @@ class DecodeConfig:
 
 @dataclass
 class DecodeWeights:
-    """Raw tile bytes per layer (uint8 [n_t*k_t, tile_bytes]) and bf16 norm weights."""
+    """Raw tile bytes per layer (uint8 [n_t*k_t, tile_bytes]) and bf16 norm weights.
+    lm_head: q8 or q4 tiles [vocab/32 * hidden/256, tile bytes] (lm_head_kind);
+    embed: optional float32 or bf16-bits [vocab, hidden] embedding (None: tied lm_head)."""
     cfg: DecodeConfig
     wq: list = field(default_factory=list)
     wk: list = field(default_factory=list)
@@ -172,72 +180,128 @@ class DecodeWeights:
     norm_in: list = field(default_factory=list)
     norm_post: list = field(default_factory=list)
     norm_final: np.ndarray | None = None
-    lm_head: np.ndarray | None = None       # q8 tiles [vocab/32 * hidden/256, 8704]
+    lm_head: np.ndarray | None = None
+    lm_head_kind: str = "q8"
+    embed: np.ndarray | None = None
 
 
-def embed_rows(lm_head_raw: np.ndarray, tokens, vocab: int, hidden: int) -> np.ndarray:
-    """Tied embedding: row t of the dequantised q8 lm_head, float32 [len(tokens), hidden]."""
+def embed_rows(lm_head_raw: np.ndarray, tokens, vocab: int, hidden: int,
+               kind: str = "q8") -> np.ndarray:
+    """Tied embedding: row t of the dequantised lm_head (q8 or q4 tiles), float32
+    [len(tokens), hidden]."""
     k_t = hidden // 256
-    tiles = np.asarray(lm_head_raw, np.uint8).reshape(vocab // 32, k_t, qo.Q8_TILE_BYTES)
+    tb = qo.Q8_TILE_BYTES if kind == "q8" else qo.Q4_TILE_BYTES
+    tiles = np.asarray(lm_head_raw, np.uint8).reshape(vocab // 32, k_t, tb)
     out = []
     for t in np.asarray(tokens).ravel():
-        w = qo.dequant_matrix(tiles[t // 32].reshape(k_t, -1), "q8", 1, k_t)
+        w = qo.dequant_matrix(tiles[t // 32].reshape(k_t, -1), kind, 1, k_t)
         out.append(w[t % 32])
     return np.stack(out).astype(np.float32)
 
 
+def embedding(w: "DecodeWeights", tokens) -> np.ndarray:
+    """Embedding rows of `tokens`: the stored matrix (bf16 bits or float) when present,
+    else the tied lm_head's dequantised rows."""
+    c = w.cfg
+    if w.embed is None:
+        return embed_rows(w.lm_head, tokens, c.vocab, c.hidden, w.lm_head_kind)
+    e = np.asarray(w.embed)
+    rows = e[np.asarray(tokens).ravel()]
+    return qo.bf16_to_f32(rows) if e.dtype == np.uint16 else rows.astype(np.float32)
+
+
 class DecodeOracle:
-    """Numpy decode step in the conventions of the module docstring. Pure float64 /
-    float32 reference with bf16 narrowing at the same points as the GPU path; slow,
-    meant for reduced layer counts in tests."""
+    """Numpy decode step in the conventions of the module docstring. Float64 / float32
+    reference with bf16 narrowing at the same points as the GPU path (narrow=True), or
+    with no narrowing at all (narrow=False: float64 everywhere, used to pin the
+    composition against an independent decoder); slow, meant for reduced layer counts."""
 
     def __init__(self, w: DecodeWeights, k_cache: list, v_cache: list, max_pos: int,
-                 gemv=None):
+                 gemv=None, narrow: bool = True, mats: dict | None = None):
         self.w = w
         self.cfg = w.cfg
-        self.k_cache = k_cache      # per layer: bf16 bits [B, Hkv, Lmax, hd]
-        self.v_cache = v_cache
+        self.narrow = narrow
+        if narrow:
+            self.k_cache = k_cache      # per layer: bf16 bits [B, Hkv, Lmax, hd]
+            self.v_cache = v_cache
+        else:                           # per layer: float64 values [B, Hkv, Lmax, hd]
+            val = lambda c: f64(qo.bf16_to_f32(c)) if np.asarray(c).dtype == np.uint16 else f64(c)
+            self.k_cache = [val(c) for c in k_cache]
+            self.v_cache = [val(c) for c in v_cache]
         self.table = rope_table(max_pos, self.cfg.head_dim, self.cfg.theta)
         # float64 GEMV from tile bytes: the numpy restatement, or the equal C one
         self.gemv = gemv or (lambda raw, kind, x, n_t, k_t: qo.gemv(raw, kind, x, n_t, k_t, acc=np.float64))
+        self._mats = {} if mats is None else mats   # float64 matrices (narrow=False), shareable
+
+    # ---- the narrowing points and the GEMV on values
+    def _bf(self, a) -> np.ndarray:
+        """A bf16 narrowing point: the value rounded to bf16 (narrow) or kept (float64)."""
+        a = np.asarray(a)
+        if self.narrow:
+            return f64(qo.bf16_round_f32(a.astype(np.float32)))
+        return f64(a)
+
+    def _res(self, a) -> np.ndarray:
+        """The residual stream's storage type: float32 (narrow) or float64."""
+        return np.asarray(a, np.float32) if self.narrow else f64(a)
+
+    def _mv(self, raw, kind: str, xv, n_t: int, k_t: int) -> np.ndarray:
+        """y = W x for x given as values (bf16-exact values when narrowing)."""
+        if self.narrow:
+            return f64(self.gemv(raw, kind, qo.bf16_round(np.asarray(xv, np.float32)), n_t, k_t))
+        key = (id(raw), kind)
+        m = self._mats.get(key)
+        if m is None:
+            m = self._mats[key] = f64(qo.dequant_matrix(raw, kind, n_t, k_t))
+        return f64(xv) @ m.T
 
     def step(self, tokens, pos) -> np.ndarray:
-        """One decode step for B sequences at positions pos[b]; returns fp32 logits [B, V]
-        and appends this step's k, v to the caches."""
+        """One decode step for B sequences at positions pos[b]; returns the float64 logits
+        [B, V] and appends this step's k, v to the caches."""
         c = self.cfg
         w = self.w
         tokens = np.asarray(tokens).ravel()
         pos = np.asarray(pos).ravel()
         b_n = tokens.size
+        hd = c.head_dim
         kt_h = c.hidden // 256
         kt_i = c.inter // 256
-        kt_q = c.n_q * c.head_dim // 256
-        h = embed_rows(w.lm_head, tokens, c.vocab, c.hidden).astype(np.float32)
+        kt_q = c.n_q * hd // 256
+        h = self._res(embedding(w, tokens))
         for layer in range(c.n_layers):
-            xn = qo.bf16_round(rmsnorm(h, w.norm_in[layer], c.eps).astype(np.float32))
-            q_raw = self.gemv(w.wq[layer], "q4", xn, c.n_q * c.head_dim // 32, kt_h)
-            k_raw = self.gemv(w.wk[layer], "q4", xn, c.n_kv * c.head_dim // 32, kt_h)
-            v_raw = self.gemv(w.wv[layer], "q4", xn, c.n_kv * c.head_dim // 32, kt_h)
-            qr, kr, vr = qkv_rope_from_raw(q_raw.reshape(b_n, -1), k_raw.reshape(b_n, -1),
-                                           v_raw.reshape(b_n, -1), pos, self.table, c.head_dim)
-            qb = qo.bf16_round(qr.astype(np.float32))
-            kb = qo.bf16_round(kr.astype(np.float32))
-            vb = qo.bf16_round(vr.astype(np.float32))
+            xn = self._bf(rmsnorm(h, w.norm_in[layer], c.eps).astype(np.float32)
+                          if self.narrow else rmsnorm(h, w.norm_in[layer], c.eps))
+            q_raw = self._mv(w.wq[layer], "q4", xn, c.n_q * hd // 32, kt_h).reshape(b_n, -1, hd)
+            k_raw = self._mv(w.wk[layer], "q4", xn, c.n_kv * hd // 32, kt_h).reshape(b_n, -1, hd)
+            v_raw = self._mv(w.wv[layer], "q4", xn, c.n_kv * hd // 32, kt_h).reshape(b_n, -1, hd)
+            # q and k narrowed before the rotation, the rotated values narrowed again
+            # (designs/granite_gemv/granite_qkv_rope.h:37-69); v only narrowed
+            qr = np.stack([rope(self._bf(q_raw[b]), pos[b], self.table) for b in range(b_n)])
+            kr = np.stack([rope(self._bf(k_raw[b]), pos[b], self.table) for b in range(b_n)])
+            qv, kv, vv = self._bf(qr), self._bf(kr), self._bf(v_raw)
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             for b in range(b_n):
-                kc[b, :, pos[b]] = kb[b]
-                vc[b, :, pos[b]] = vb[b]
+                if self.narrow:
+                    kc[b, :, pos[b]] = qo.bf16_round(kv[b].astype(np.float32))
+                    vc[b, :, pos[b]] = qo.bf16_round(vv[b].astype(np.float32))
+                else:
+                    kc[b, :, pos[b]] = kv[b]
+                    vc[b, :, pos[b]] = vv[b]
             lens = pos + 1
-            att = gqa_attention(qo.bf16_to_f32(qb), qo.bf16_to_f32(kc), qo.bf16_to_f32(vc),
-                                lens, c.scale)
-            ab = qo.bf16_round(att.astype(np.float32).reshape(b_n, -1))
-            o = self.gemv(w.wo[layer], "q4", ab, c.hidden // 32, kt_q)
-            h = (h + o.reshape(b_n, -1)).astype(np.float32)   # fp32 residual add
-            xn2 = qo.bf16_round(rmsnorm(h, w.norm_post[layer], c.eps).astype(np.float32))
-            g_raw = self.gemv(w.wg[layer], "q4", xn2, c.inter // 32, kt_h)
-            u_raw = self.gemv(w.wu[layer], "q4", xn2, c.inter // 32, kt_h)
-            m = qo.bf16_round(swiglu_from_raw(g_raw, u_raw).astype(np.float32)).reshape(b_n, -1)
-            dn = self.gemv(w.wd[layer], "q4", m, c.hidden // 32, kt_i)
-            h = (h + dn.reshape(b_n, -1)).astype(np.float32)
-        hf = qo.bf16_round(rmsnorm(h, w.norm_final, c.eps).astype(np.float32))
-        return self.gemv(w.lm_head, "q8", hf, c.vocab // 32, kt_h).reshape(b_n, -1)
+            kval = qo.bf16_to_f32(kc) if self.narrow else kc
+            vval = qo.bf16_to_f32(vc) if self.narrow else vc
+            att = gqa_attention(qv, kval, vval, lens, c.scale)
+            ab = self._bf(att.astype(np.float32) if self.narrow else att).reshape(b_n, -1)
+            o = self._mv(w.wo[layer], "q4", ab, c.hidden // 32, kt_q)
+            h = self._res(h + o.reshape(b_n, -1))          # residual add (fp32 when narrowing)
+            xn2 = self._bf(rmsnorm(h, w.norm_post[layer], c.eps).astype(np.float32)
+                           if self.narrow else rmsnorm(h, w.norm_post[layer], c.eps))
+            g_raw = self._mv(w.wg[layer], "q4", xn2, c.inter // 32, kt_h)
+            u_raw = self._mv(w.wu[layer], "q4", xn2, c.inter // 32, kt_h)
+            sw = swiglu(self._bf(g_raw), self._bf(u_raw))
+            m = self._bf(sw.astype(np.float32) if self.narrow else sw).reshape(b_n, -1)
+            dn = self._mv(w.wd[layer], "q4", m, c.hidden // 32, kt_i)
+            h = self._res(h + dn.reshape(b_n, -1))
+        hf = self._bf(rmsnorm(h, w.norm_final, c.eps).astype(np.float32)
+                      if self.narrow else rmsnorm(h, w.norm_final, c.eps))
+        return self._mv(w.lm_head, w.lm_head_kind, hf, c.vocab // 32, kt_h).reshape(b_n, -1)

@@ -209,3 +209,16 @@ def test_rope_table_host(max_pos, theta):
     ref = do.rope_table(max_pos, 64, theta)
     assert np.abs(tab - ref).max() <= 6e-8
     assert np.array_equal(tab[0, 0], np.ones(32, np.float32)) and not tab[0, 1].any()
+
+
+def test_rope_table_host_closed_forms():
+    """The C table's frequencies pinned by closed forms, independent of the oracle:
+    pair i turns by pos * theta^(-2i/64), i.e. pos/10, pos/100, pos/1000 for i = 8, 16, 24
+    at theta = 10^4 and pos/1000 for i = 16 at theta = 10^6."""
+    from tests.pins import check_rope_frequencies
+
+    def c_table(max_pos, hd, theta):
+        tab = np.empty((max_pos, 2, hd // 2), np.float32)
+        _lib.call("q4nx_rope_table_host", tab.ctypes.data, max_pos, hd, C.c_double(theta))
+        return tab
+    check_rope_frequencies(c_table)
