@@ -213,17 +213,14 @@ def secondary_bench(dev, groups=SECONDARY_GROUPS) -> dict:
             xb = torch.randn(bb, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
             hb = torch.empty(bb, INTER, dtype=torch.bfloat16, device=dev)
             yb = torch.empty(bb, HIDDEN, dtype=torch.float32, device=dev)
+            pol = ops.Policy(mfma_rows_q4=0) if path else ops.Policy()
 
             def mlp():
                 for g_, u_, d_ in layers:
-                    ops.gate_up_swiglu(g_, u_, INTER // 32, HIDDEN // 256, xb, h_out=hb, ws=wsp)
-                    ops.gemv(d_, "q4", hb, HIDDEN // 32, INTER // 256, out=yb, ws=wsp)
-            if path:
-                ops.set_mfma_rows("q4", 0)
-            try:
-                t = _graph_time(mlp, 10) / len(layers)
-            finally:
-                ops.set_mfma_rows("q4", 2)
+                    ops.gate_up_swiglu(g_, u_, INTER // 32, HIDDEN // 256, xb, h_out=hb, ws=wsp,
+                                       policy=pol)
+                    ops.gemv(d_, "q4", hb, HIDDEN // 32, INTER // 256, out=yb, ws=wsp, policy=pol)
+            t = _graph_time(mlp, 10) / len(layers)
             byt = 3 * q4_bytes(INTER, HIDDEN) + bb * (2 * HIDDEN + 2 * INTER * 2 + 4 * HIDDEN)
             out[f"mlp_gate_up_swiglu_down_b{bb}{path}"] = {"us": round(t * 1e6, 2),
                                                            "GB/s": round(byt / t / 1e9, 1)}

@@ -16,6 +16,12 @@
  *     use; every call leaves the counters at zero again, whatever the shapes of the
  *     calls that share the workspace. Calls that share a workspace must be ordered on
  *     one stream. Any entry point's ws_bytes query includes the counter region.
+ *   - Entry points that choose between kernel families or work splits take a
+ *     `const q4nx_policy *policy` (NULL = the defaults of q4nx_policy_init). The library
+ *     keeps no mutable state of its own: calls with different policies, from any thread,
+ *     never affect each other. A ws_bytes query must be given the policy of the call.
+ *   - Sums of squares (ssq_in / ssq_out) and argmax keys are kept per 16-row block:
+ *     [batch][N/16] for an output of N rows, [batch][K/16] for an input of K entries.
  *
  * The reference interface each entry point replaces is cited beside it (paths relative
  * to the reference repository).
@@ -30,17 +36,17 @@
 extern "C" {
 #endif
 
-#define Q4NX_ABI_VERSION 1
+#define Q4NX_ABI_VERSION 2
 
 #define Q4NX_OK 0
 #define Q4NX_ERR_ARG (-1)     /* null or misaligned pointer, bad enum            */
 #define Q4NX_ERR_SHAPE (-2)   /* K % 256, N % 32, Hq % Hkv, head_dim, batch ...  */
 #define Q4NX_ERR_WS (-3)      /* workspace missing or too small                  */
-#define Q4NX_ERR_TIMEOUT (-5) /* a multi-stage launch gave up waiting            */
 #define Q4NX_ERR_LAUNCH (-4)  /* the HIP runtime refused the launch              */
 
 #define Q4NX_KIND_Q4 4
 #define Q4NX_KIND_Q8 8
+#define Q4NX_KIND_BF16 16   /* a plain bf16 matrix (embedding tables) */
 
 #define Q4NX_MAX_BATCH 8
 
@@ -50,6 +56,24 @@ extern "C" {
 int q4nx_abi_version(void);
 /* Message of the last error on this thread ("" if none). */
 const char *q4nx_last_error(void);
+
+/* ---------------------------------------------------------------- launch policy
+ * Which kernel family takes a call and how its work is split, passed per call. No reference
+ * counterpart: each NPU design fixed its mapping when it was built (export_design.py). */
+typedef struct q4nx_policy {
+  int mfma_rows_q4;   /* q4 GEMV / fused groups: rows from which they run on the matrix
+                         cores (the q4nx_gemm kernels); 0 = never. Default 2. */
+  int mfma_rows_q8;   /* the same for q8. Default 1. */
+  int rowblock;       /* 1 (default): one-row q4 calls on the row-block kernels (one
+                         workgroup per 16 output rows); 0: on the general VALU GEMV */
+  int gemv_ksplit;    /* general VALU GEMV: workgroups per output group along K, 1..8;
+                         0 = automatic (default) */
+  int gemv_tiles_per_wave; /* general VALU GEMV: K-tiles per wave, 1, 2 or 4; 0 = automatic */
+  int gemm_ksplit;    /* matrix-core contraction: workgroups along K, 1..8; 0 = automatic */
+  int attn_mfma;      /* 1 (default): attention on the matrix cores; 0: on the VALU kernel */
+} q4nx_policy;
+/* Fills *p with the defaults. */
+void q4nx_policy_init(q4nx_policy *p);
 
 /* ---------------------------------------------------------------- dequantisation
  * Replaces tools/q4nx.py:97-111 (dequant_q4 / dequant_q8, bf16 out) and :127-149
@@ -71,31 +95,35 @@ int q4nx_dequant_q8(const uint8_t *tiles, void *out, int n_tile_rows, int k_tile
  *   w: tile bytes, 16-byte aligned; x: bf16 [batch][x_stride]; y: fp32 [batch][y_stride];
  *   residual: fp32 [batch][y_stride] or NULL. K = 256*k_tiles, N = 32*n_tile_rows.
  *   ws: workspace of at least q4nx_gemv_ws_bytes(...) bytes (may be NULL when that is 0). */
-size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch);
+size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch,
+                          const q4nx_policy *policy);
 int q4nx_gemv_q4(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
                  int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
-                 const float *residual, void *ws, size_t ws_bytes, void *stream);
+                 const float *residual, void *ws, size_t ws_bytes,
+                 const q4nx_policy *policy, void *stream);
 int q4nx_gemv_q8(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
                  int k_tiles, int batch, int64_t x_stride, int64_t y_stride,
-                 const float *residual, void *ws, size_t ws_bytes, void *stream);
+                 const float *residual, void *ws, size_t ws_bytes,
+                 const q4nx_policy *policy, void *stream);
 
 /* General form of the two above: y = residual + W * f(x), where f is the identity on a
  * bf16 x, or, when norm_w != NULL, RMSNorm(x; norm_w, eps) of an fp32 x rounded to bf16
  * in the prologue (granite_rmsnorm.h:45-80 fused into the GEMV). kind is Q4NX_KIND_Q4 or
- * Q4NX_KIND_Q8. argmax_keys (optional, uint64 [batch][n_tile_rows]) receives for every
- * tile-row an order-preserving key of (max y over its 32 rows, first such row);
+ * Q4NX_KIND_Q8. argmax_keys (optional, uint64 [batch][N/16]) receives for every 16-row
+ * block an order-preserving key of (max y over its rows, first such row);
  * q4nx_decode_advance reduces them. y may be NULL when only the keys are wanted.
- * ssq_out (optional, fp32 [batch][n_tile_rows]): sum of y^2 over each tile-row's 32
- * outputs. ssq_in (optional, with norm_w; fp32 [batch][K/32], K <= 8192): the same
- * partial sums for x, as the producer of x wrote them; the prologue then adds these
- * (in a fixed order) instead of reducing x across the workgroup. ws as for the GEMVs
- * above (K split when the launch has few tile-rows). No reference counterpart for the
- * fusions: the reference runs the final norm and argmax on the host (chat.py:74-78
- * through transformers' generate). */
+ * ssq_out (optional, fp32 [batch][N/16]): sum of y^2 over each 16-row block.
+ * ssq_in (optional, with norm_w; fp32 [batch][K/16], K <= 8192): the same partial sums
+ * for x, as the producer of x wrote them; the prologue then adds these (in a fixed order)
+ * instead of reducing x across the workgroup (the one-row kernels need them with norm_w).
+ * ws as for the GEMVs above (K split when the launch has few tile-rows). No reference
+ * counterpart for the fusions: the reference runs the final norm and argmax on the host
+ * (chat.py:74-78 through transformers' generate). */
 int q4nx_gemv_ex(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const void *x,
                  int64_t x_stride, const uint16_t *norm_w, float eps, const float *ssq_in,
                  int batch, float *y, int64_t y_stride, const float *residual, float *ssq_out,
-                 uint64_t *argmax_keys, void *ws, size_t ws_bytes, void *stream);
+                 uint64_t *argmax_keys, void *ws, size_t ws_bytes,
+                 const q4nx_policy *policy, void *stream);
 
 /* The o-projection of a batch-1 decode step fed straight from attention's split records:
  * y = residual + W * bf16(merge(att_rec)), where merge(att_rec) is the attention output
@@ -103,22 +131,13 @@ int q4nx_gemv_ex(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const
  * the results equal q4nx_gqa_decode followed by q4nx_gemv_ex bit for bit). W: q4 tiles
  * [n_tile_rows][n_q_heads/4]; K = 64 * n_q_heads <= 2560; att_rec: the records of
  * q4nx_gqa_decode_records at batch 1 (ws + Q4NX_WS_COUNTER_BYTES), n_split <= 18, which are
- * only read; y, residual, ssq_out as in q4nx_gemv_ex. One workgroup per tile-row, no K
+ * only read; y, residual, ssq_out as in q4nx_gemv_ex. One workgroup per 16 output rows, no K
  * split, no workspace. Fuses granite_attn_finish (granite_attention.h:193-212, 232-237) into the
  * o-projection GEMV of designs/granite_gemv/granite_gemv.h:79-91. */
 int q4nx_gemv_attn_q4(const uint8_t *w, int n_tile_rows, const float *att_rec, int n_split,
                       int n_q_heads, int n_kv_heads, float *y, const float *residual,
                       float *ssq_out, void *stream);
 
-/* The q4nx_set_* knobs are process-wide atomics: a launch reads each knob it uses once, so
- * setting one while another thread launches is safe and that launch sees the old or the new
- * value, never a mix.
- * Tuning knob: K-tiles per wave (1, 2 or 4), 0 = automatic. Process-wide. */
-int q4nx_set_split_tiles(int tiles_per_wave);
-/* Tuning knob: workgroups per output group along K (1..8), 0 = automatic (split only
- * launches with too few groups to fill the GPU, when a large enough workspace is given).
- * Process-wide. No reference counterpart: on the NPU each core owned whole rows. */
-int q4nx_set_gemv_ksplit(int parts);
 
 /* ---------------------------------------------------------------- batched contraction (MFMA)
  * y[m][n] = residual[m][n] + sum_k W[n][k] * x[m][k] for m < m_rows, any m_rows >= 1, on the
@@ -129,19 +148,15 @@ int q4nx_set_gemv_ksplit(int parts);
  *   y, residual: fp32 [m_rows][y_stride], y_stride % 4 == 0, 16-byte aligned.
  *   ws: workspace of q4nx_gemm_ws_bytes(...) bytes, zeroed once (K is split across
  *   workgroups when the launch has few of them); NULL runs without the split. */
-size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows);
+size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows,
+                          const q4nx_policy *policy);
 int q4nx_gemm(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const uint16_t *x,
               int64_t x_stride, int m_rows, float *y, int64_t y_stride, const float *residual,
-              void *ws, size_t ws_bytes, void *stream);
-/* Tuning knob: workgroups along K for q4nx_gemm (1..8), 0 = automatic. Process-wide. */
-int q4nx_set_gemm_ksplit(int parts);
-/* Rows from which q4nx_gemv_q4/q8, q4nx_gemv_ex, q4nx_qkv_rope and q4nx_gate_up_swiglu run
- * on the matrix-core kernels of q4nx_gemm (fused prologue and epilogues included) instead of
- * the VALU GEMV, per kind; 0 = never. Defaults: q4 from 2 rows, q8 from 1 (measured faster
- * there). On that path `batch` may exceed Q4NX_MAX_BATCH; an RMSNorm prologue there needs
- * ssq_in (launches without it stay on the VALU kernel, batch <= 8).
- * Process-wide. No reference counterpart. */
-int q4nx_set_mfma_rows(int kind, int min_rows);
+              void *ws, size_t ws_bytes, const q4nx_policy *policy, void *stream);
+/* The GEMV and fused entry points hand calls of policy->mfma_rows_q4 / _q8 rows or more to
+ * these matrix-core kernels (fused prologue and epilogues included); there `batch` may
+ * exceed Q4NX_MAX_BATCH, and an RMSNorm prologue needs ssq_in (launches without it stay on
+ * the VALU kernel, batch <= 8). */
 
 /* ---------------------------------------------------------------- elementwise
  * RMSNorm y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, bf16 out (+ optional fp32
@@ -180,45 +195,29 @@ int q4nx_swiglu(const void *g, const void *u, int in_f32, uint16_t *y, float *y_
  * elements; l < max_pos. raw_out (optional): fp32 [batch][(n_q+2*n_kv)*64] GEMV outputs
  * before narrowing. xn_out (optional): bf16 [batch][K] normalised input. ssq_in: as in
  * q4nx_gemv_ex. */
-size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch);
+size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch,
+                              const q4nx_policy *policy);
 int q4nx_qkv_rope(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, int n_q_heads,
                   int n_kv_heads, int k_tiles, const void *x, int64_t x_stride,
                   const uint16_t *norm_w, float eps, const float *ssq_in, int batch,
                   const int32_t *positions,
                   const float *rope_tab, int max_pos, uint16_t *q_out, uint16_t *k_cache,
                   uint16_t *v_cache, int64_t kv_b_stride, int64_t kv_h_stride,
-                  float *raw_out, uint16_t *xn_out, void *ws, size_t ws_bytes, void *stream);
+                  float *raw_out, uint16_t *xn_out, void *ws, size_t ws_bytes,
+                  const q4nx_policy *policy, void *stream);
 
 /* [gate, up, SwiGLU] in one launch: h[b][n] = bf16(silu(bf16(gate.x)) * bf16(up.x)).
  * Replaces designs/granite_gemv/granite_mlp.py:48-133 with granite_swiglu_f32.h. Input
  * as q4nx_qkv_rope (bf16 x, or fp32 residual + norm_w). raw_out (optional): fp32
  * [batch][2*N] gate|up accumulators; xn_out (optional) as above. */
-size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch);
+size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch,
+                             const q4nx_policy *policy);
 int q4nx_gate_up_swiglu(const uint8_t *wg, const uint8_t *wu, int n_tile_rows,
                         int k_tiles, const void *x, int64_t x_stride,
                         const uint16_t *norm_w, float eps, const float *ssq_in, int batch,
                         uint16_t *h_out,
                         int64_t h_stride, float *raw_out, uint16_t *xn_out, void *ws,
-                        size_t ws_bytes, void *stream);
-
-/* Everything between attention and the next layer in one launch (three stages): o-proj
- * h += Wo attn (and per-32 sums of squares of h into ssq), then RMSNorm(h; norm_w) with
- * [gate, up, SwiGLU] into mlp (bf16 [batch][inter]), then down h += Wd mlp (ssq again).
- * Each stage streams its weights while the previous one runs and reads its inputs once
- * that stage is complete. Same arithmetic as q4nx_gemv_ex + q4nx_gate_up_swiglu +
- * q4nx_gemv_ex. attn: bf16 [batch][q_dim]; h: fp32 [batch][hidden], updated in place;
- * ssq: fp32 [batch][hidden/32]. Replaces the o-proj and MLP designs of one reference
- * layer (designs/granite_gemv/granite_layer.py:11-14, granite_mlp.py:48-133); no
- * single reference kernel does all three. */
-size_t q4nx_layer_tail_ws_bytes(int hidden, int q_dim, int inter, int batch);
-int q4nx_layer_tail(const uint8_t *wo, const uint8_t *wg, const uint8_t *wu,
-                    const uint8_t *wd, int hidden, int q_dim, int inter,
-                    const uint16_t *attn, float *h, float *ssq, const uint16_t *norm_w,
-                    float eps, uint16_t *mlp, int batch, void *ws, size_t ws_bytes,
-                    void *stream);
-/* Synchronises the stream and returns Q4NX_ERR_TIMEOUT (clearing the flag) if a
- * multi-stage launch on this workspace gave up waiting since the last check. */
-int q4nx_ws_check(void *ws, void *stream);
+                        size_t ws_bytes, const q4nx_policy *policy, void *stream);
 
 /* ---------------------------------------------------------------- attention
  * GQA flash-decode: one query token per sequence, out[b][h] = softmax(scale * K q) V
@@ -226,26 +225,26 @@ int q4nx_ws_check(void *ws, void *stream);
  * Split-K over the KV length with an exact (m, l, acc) combine. Replaces
  * designs/granite_gemv/granite_attention.h:221-237 (granite_attn_block /
  * granite_attn_finish). head_dim must be 64. q: bf16 [B][Hq][64]; out: bf16 and/or fp32
- * [B][Hq][64]; caches as in q4nx_qkv_rope. n_split = 0 chooses automatically. */
-size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len);
-/* Policy knob: 1 (default) runs q4nx_gqa_decode on the matrix cores (scores and P.V on
- * v_mfma_f32_16x16x32_bf16, P carried as three bf16 terms), 0 on the VALU kernel. Both give
- * fp32-accurate results. Process-wide; returns the previous setting. No reference
- * counterpart. */
-int q4nx_set_attn_mfma(int on);
+ * [B][Hq][64]; caches as in q4nx_qkv_rope. n_split = 0 chooses automatically.
+ * policy->attn_mfma picks the kernel: the matrix cores (scores and P.V on
+ * v_mfma_f32_16x16x32_bf16, P carried as three bf16 terms) or the VALU kernel; both give
+ * fp32-accurate results. */
+size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len,
+                                const q4nx_policy *policy);
 int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                     uint16_t *out, float *out_f32, int batch, int n_q_heads,
                     int n_kv_heads, int head_dim, const int32_t *lens, int max_len,
                     int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
-                    void *ws, size_t ws_bytes, void *stream);
-/* The split count q4nx_gqa_decode chooses for n_split = 0 under the current policy knob
- * (what q4nx_gqa_decode_records and q4nx_gemv_attn_q4 should be given for the same
- * shape); 0 for an invalid shape. */
-int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len);
+                    void *ws, size_t ws_bytes, const q4nx_policy *policy, void *stream);
+/* The split count q4nx_gqa_decode chooses for n_split = 0 under `policy`; 0 for an invalid
+ * shape or policy. */
+int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len,
+                           const q4nx_policy *policy);
 /* The split count to give q4nx_gqa_decode_records when q4nx_gemv_attn_q4 merges the
  * records: q4nx_gqa_decode_splits capped at 12 (every split is a record each o-projection
  * workgroup reads, so the pair runs fastest with fewer, longer splits). */
-int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len);
+int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len,
+                                   const q4nx_policy *policy);
 /* The first half of q4nx_gqa_decode: every split of every (b, kv head) writes its record
  * (fp32 acc[64], m (log2 domain), l, 2 pad; 68 floats per q head) to the workspace at
  * ws + Q4NX_WS_COUNTER_BYTES, laid out [b][kv head][split][head in group][68], and ends;
@@ -259,7 +258,8 @@ int q4nx_gqa_decode_records(const uint16_t *q, const uint16_t *k_cache,
                             const uint16_t *v_cache, int batch, int n_q_heads, int n_kv_heads,
                             int head_dim, const int32_t *lens, int max_len,
                             int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
-                            void *ws, size_t ws_bytes, void *stream);
+                            void *ws, size_t ws_bytes, const q4nx_policy *policy,
+                            void *stream);
 
 /* y[i] = bf16(x[i]), round to nearest even, NaN kept quiet: the device form of the bf16
  * rounding every kernel applies to its outputs (tools/q4nx.py:97-111 rounds the same way
@@ -267,12 +267,14 @@ int q4nx_gqa_decode_records(const uint16_t *q, const uint16_t *k_cache,
 int q4nx_round_bf16(const float *x, uint16_t *y, int64_t n, void *stream);
 
 /* ---------------------------------------------------------------- decode-step helpers
- * h[b][:] = fp32 row tokens[b] of a q8-tiled [vocab][hidden] matrix (a tied lm_head
- * used as the embedding table); ssq_out (optional, [batch][hidden/32]) as in
- * q4nx_gemv_ex. No reference counterpart: the reference has no token loop
- * (README.md:295-311). */
-int q4nx_embed_q8(const uint8_t *w, const int32_t *tokens, float *h, float *ssq_out,
-                  int vocab, int hidden, int batch, void *stream);
+ * h[b][:] = fp32 row tokens[b] of a [vocab][hidden] table: a plain bf16 matrix
+ * (kind Q4NX_KIND_BF16, e.g. a stored model.embed_tokens.weight) or q4 / q8 tiles (a tied
+ * lm_head used as the embedding, dequantised exactly as q4nx_dequant_* does);
+ * ssq_out (optional, [batch][hidden/16]) as in q4nx_gemv_ex. A token outside [0, vocab)
+ * gives a row of NaN, which every later result then shows. No reference counterpart: the reference has no token loop
+ * (README.md:295-311); its Qwen path embeds through transformers. */
+int q4nx_embed(int kind, const void *table, const int32_t *tokens, float *h, float *ssq_out,
+               int vocab, int hidden, int batch, void *stream);
 /* idx[b] = argmax_n logits[b][n] (first maximum), max[b] its value (optional). */
 int q4nx_argmax(const float *logits, int n, int batch, int64_t stride, int32_t *idx,
                 float *max_val, void *stream);

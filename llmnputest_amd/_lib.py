@@ -19,48 +19,75 @@ c_sz = C.c_size_t
 c_f = C.c_float
 c_d = C.c_double
 
+
+class Policy(C.Structure):
+    """q4nx_policy: which kernel family takes a call and how its work is split (passed per
+    call; the library keeps no state). Fields default to q4nx_policy_init's values."""
+    _fields_ = [
+        ("mfma_rows_q4", c_i),          # q4 rows from which the matrix cores take a call; 0 never
+        ("mfma_rows_q8", c_i),          # the same for q8
+        ("rowblock", c_i),              # one-row q4 calls on the row-block kernels
+        ("gemv_ksplit", c_i),           # general VALU GEMV: K parts per group, 0 automatic
+        ("gemv_tiles_per_wave", c_i),   # general VALU GEMV: K-tiles per wave, 0 automatic
+        ("gemm_ksplit", c_i),           # matrix-core contraction: K parts, 0 automatic
+        ("attn_mfma", c_i),             # attention on the matrix cores
+    ]
+
+    def __init__(self, **fields):
+        super().__init__()
+        lib().q4nx_policy_init(C.byref(self))
+        for k, v in fields.items():
+            if k not in dict(self._fields_):
+                raise AttributeError(f"q4nx_policy has no field {k}")
+            setattr(self, k, int(v))
+
+    def replace(self, **fields) -> "Policy":
+        d = {k: getattr(self, k) for k, _ in self._fields_}
+        d.update(fields)
+        return Policy(**d)
+
+    def __repr__(self) -> str:
+        return "Policy(" + ", ".join(f"{k}={getattr(self, k)}" for k, _ in self._fields_) + ")"
+
+
+c_pol = C.POINTER(Policy)
+
 # name -> (restype, argtypes); mirrors include/q4nx_hip.h
 SIGNATURES: dict[str, tuple] = {
     "q4nx_abi_version": (c_i, []),
     "q4nx_last_error": (C.c_char_p, []),
     "q4nx_dequant_q4": (c_i, [c_p, c_p, c_i, c_i, c_i, c_i, c_p]),
     "q4nx_dequant_q8": (c_i, [c_p, c_p, c_i, c_i, c_i, c_i, c_p]),
-    "q4nx_gemv_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
-    "q4nx_gemv_q4": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_p]),
-    "q4nx_gemv_q8": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_p]),
+    "q4nx_policy_init": (None, [c_p]),
+    "q4nx_gemv_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i, c_pol]),
+    "q4nx_gemv_q4": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_pol, c_p]),
+    "q4nx_gemv_q8": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i64, c_i64, c_p, c_p, c_sz, c_pol, c_p]),
     "q4nx_gemv_ex": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p, c_i64, c_p,
-                           c_p, c_p, c_p, c_sz, c_p]),
-    "q4nx_set_split_tiles": (c_i, [c_i]),
-    "q4nx_set_gemv_ksplit": (c_i, [c_i]),
-    "q4nx_gemm_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
-    "q4nx_gemm": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_i, c_p, c_i64, c_p, c_p, c_sz, c_p]),
-    "q4nx_set_gemm_ksplit": (c_i, [c_i]),
-    "q4nx_set_mfma_rows": (c_i, [c_i, c_i]),
+                           c_p, c_p, c_p, c_sz, c_pol, c_p]),
+    "q4nx_gemm_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i, c_pol]),
+    "q4nx_gemm": (c_i, [c_i, c_p, c_i, c_i, c_p, c_i64, c_i, c_p, c_i64, c_p, c_p, c_sz, c_pol,
+                        c_p]),
     "q4nx_rmsnorm": (c_i, [c_p, c_i, c_p, c_p, c_p, c_i, c_i, c_f, c_p]),
     "q4nx_rope": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_i, c_p]),
     "q4nx_rope_table_host": (c_i, [c_p, c_i, c_i, c_d]),
     "q4nx_swiglu": (c_i, [c_p, c_p, c_i, c_p, c_p, c_i, c_i, c_p]),
-    "q4nx_qkv_rope_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
+    "q4nx_qkv_rope_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i, c_pol]),
     "q4nx_qkv_rope": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p,
-                            c_p, c_i, c_p, c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_sz, c_p]),
-    "q4nx_gate_up_ws_bytes": (c_sz, [c_i, c_i, c_i]),
+                            c_p, c_i, c_p, c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_sz, c_pol,
+                            c_p]),
+    "q4nx_gate_up_ws_bytes": (c_sz, [c_i, c_i, c_i, c_pol]),
     "q4nx_gate_up_swiglu": (c_i, [c_p, c_p, c_i, c_i, c_p, c_i64, c_p, c_f, c_p, c_i, c_p,
-                                  c_i64, c_p, c_p, c_p, c_sz, c_p]),
-    "q4nx_layer_tail_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
-    "q4nx_layer_tail": (c_i, [c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_p, c_p, c_f, c_p, c_i,
-                              c_p, c_sz, c_p]),
-    "q4nx_ws_check": (c_i, [c_p, c_p]),
-    "q4nx_gqa_decode_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i]),
-    "q4nx_set_attn_mfma": (c_i, [c_i]),
+                                  c_i64, c_p, c_p, c_p, c_sz, c_pol, c_p]),
+    "q4nx_gqa_decode_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i, c_pol]),
     "q4nx_gqa_decode": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
-                              c_i64, c_f, c_i, c_p, c_sz, c_p]),
-    "q4nx_gqa_decode_splits": (c_i, [c_i, c_i, c_i, c_i]),
-    "q4nx_gqa_decode_records_splits": (c_i, [c_i, c_i, c_i, c_i]),
+                              c_i64, c_f, c_i, c_p, c_sz, c_pol, c_p]),
+    "q4nx_gqa_decode_splits": (c_i, [c_i, c_i, c_i, c_i, c_pol]),
+    "q4nx_gqa_decode_records_splits": (c_i, [c_i, c_i, c_i, c_i, c_pol]),
     "q4nx_gqa_decode_records": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
-                                      c_i64, c_f, c_i, c_p, c_sz, c_p]),
+                                      c_i64, c_f, c_i, c_p, c_sz, c_pol, c_p]),
     "q4nx_gemv_attn_q4": (c_i, [c_p, c_i, c_p, c_i, c_i, c_i, c_p, c_p, c_p, c_p]),
     "q4nx_round_bf16": (c_i, [c_p, c_p, c_i64, c_p]),
-    "q4nx_embed_q8": (c_i, [c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
+    "q4nx_embed": (c_i, [c_i, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
     "q4nx_argmax": (c_i, [c_p, c_i, c_i, c_i64, c_p, c_p, c_p]),
     "q4nx_decode_advance": (c_i, [c_p, c_i, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p]),
 }

@@ -23,6 +23,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "policy.h"
 
 namespace q4nx {
 
@@ -573,10 +574,6 @@ static int auto_split(int batch, int hkv, int max_len, bool mfma) {
   return s < 1 ? 1 : s;
 }
 
-// 1: matrix-core kernel, 0: VALU kernel. Process-wide; a launch reads it once, so its split
-// policy and its kernel always agree.
-static std::atomic<int> g_attn_mfma{1};
-
 template <int G>
 static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) {
   // K/V of 64 MB or more per launch streams past the caches (measured: batch 8 at 32768
@@ -597,13 +594,13 @@ using namespace q4nx;
 
 extern "C" {
 
-int q4nx_set_attn_mfma(int on) {
-  return g_attn_mfma.exchange(on ? 1 : 0);
-}
-
-size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len) {
-  if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1) return 0;
-  const int ns = auto_split(batch, n_kv_heads, max_len, false);   // the larger of the two
+size_t q4nx_gqa_decode_ws_bytes(int batch, int n_q_heads, int n_kv_heads, int max_len,
+                                const q4nx_policy* policy) {
+  Policy P;
+  if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1 ||
+      !resolve_policy_quiet(policy, &P))
+    return 0;
+  const int ns = auto_split(batch, n_kv_heads, max_len, P.attn_mfma != 0);
   if (ns == 1) return 0;
   return (size_t)Q4NX_WS_COUNTER_BYTES +
          partial_bytes(batch, n_kv_heads, ns, n_q_heads / n_kv_heads);
@@ -613,7 +610,10 @@ static int attn_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
                     uint16_t* out, float* out_f32, int batch, int n_q_heads, int n_kv_heads,
                     int head_dim, const int32_t* lens, int max_len, int64_t kv_b_stride,
                     int64_t kv_h_stride, float scale, int n_split, void* ws, size_t ws_bytes,
-                    void* stream, bool publish_only, const char* what) {
+                    const q4nx_policy* policy, void* stream, bool publish_only,
+                    const char* what) {
+  Policy P;
+  if (int rc = resolve_policy(policy, &P, what)) return rc;
   Q4NX_REQUIRE(q && k_cache && v_cache && lens && (publish_only || out || out_f32), Q4NX_ERR_ARG,
                "%s: q, caches, lens and an output are required", what);
   Q4NX_REQUIRE(Q4NX_ALIGNED(q, 16) && Q4NX_ALIGNED(k_cache, 16) && Q4NX_ALIGNED(v_cache, 16),
@@ -643,7 +643,7 @@ static int attn_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   a.scale_l2 = (float)((double)scale * 1.4426950408889634);
   Q4NX_REQUIRE(n_split >= 0 && n_split <= 4096, Q4NX_ERR_ARG, "%s: n_split=%d outside 0..4096",
                what, n_split);
-  const bool mfma = g_attn_mfma.load(std::memory_order_relaxed) != 0;
+  const bool mfma = P.attn_mfma != 0;
   a.n_split = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len, mfma);
   a.chunk = ((max_len + a.n_split - 1) / a.n_split + 7) & ~7;
   a.publish_only = publish_only ? 1 : 0;
@@ -680,15 +680,19 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
                     uint16_t* out, float* out_f32, int batch, int n_q_heads, int n_kv_heads,
                     int head_dim, const int32_t* lens, int max_len, int64_t kv_b_stride,
                     int64_t kv_h_stride, float scale, int n_split, void* ws, size_t ws_bytes,
-                    void* stream) {
+                    const q4nx_policy* policy, void* stream) {
   return attn_run(q, k_cache, v_cache, out, out_f32, batch, n_q_heads, n_kv_heads, head_dim,
-                  lens, max_len, kv_b_stride, kv_h_stride, scale, n_split, ws, ws_bytes, stream,
-                  false, "q4nx_gqa_decode");
+                  lens, max_len, kv_b_stride, kv_h_stride, scale, n_split, ws, ws_bytes, policy,
+                  stream, false, "q4nx_gqa_decode");
 }
 
-int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len) {
-  if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1) return 0;
-  return auto_split(batch, n_kv_heads, max_len, g_attn_mfma.load(std::memory_order_relaxed) != 0);
+int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len,
+                           const q4nx_policy* policy) {
+  Policy P;
+  if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || max_len < 1 ||
+      !resolve_policy_quiet(policy, &P))
+    return 0;
+  return auto_split(batch, n_kv_heads, max_len, P.attn_mfma != 0);
 }
 
 // Splits for records an o-projection merges: the attention policy's count, capped at 12.
@@ -698,8 +702,9 @@ int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len
 // (4000) splits.
 constexpr int kRecordSplitCap = 12;
 
-int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len) {
-  const int ns = q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len);
+int q4nx_gqa_decode_records_splits(int batch, int n_q_heads, int n_kv_heads, int max_len,
+                                   const q4nx_policy* policy) {
+  const int ns = q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len, policy);
   return ns < kRecordSplitCap ? ns : kRecordSplitCap;
 }
 
@@ -707,12 +712,12 @@ int q4nx_gqa_decode_records(const uint16_t* q, const uint16_t* k_cache,
                             const uint16_t* v_cache, int batch, int n_q_heads, int n_kv_heads,
                             int head_dim, const int32_t* lens, int max_len, int64_t kv_b_stride,
                             int64_t kv_h_stride, float scale, int n_split, void* ws,
-                            size_t ws_bytes, void* stream) {
+                            size_t ws_bytes, const q4nx_policy* policy, void* stream) {
   const char* what = "q4nx_gqa_decode_records";
   Q4NX_REQUIRE(n_split >= 1, Q4NX_ERR_ARG, "%s: n_split=%d must be given (>= 1)", what, n_split);
   return attn_run(q, k_cache, v_cache, nullptr, nullptr, batch, n_q_heads, n_kv_heads,
                   head_dim, lens, max_len, kv_b_stride, kv_h_stride, scale, n_split, ws,
-                  ws_bytes, stream, true, what);
+                  ws_bytes, policy, stream, true, what);
 }
 
 }  // extern "C"

@@ -196,6 +196,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
+// RMSNorm from the producer's sums of squares: a row of x has n = K/16 partial sums (one per
+// 16 entries); lane l holds entries l, l + 64, l + 128, ... (loaded clamped into sq) and adds
+// them in that order, and wave_sum of the lane sums is the row's total. Every consumer of the
+// sums uses this order, so all kernel families normalise with the same bits.
+constexpr int kSsqRows = 16;   // entries per partial sum of squares
+template <int NSS>
+__device__ __forceinline__ float ssq_lane_sum(const float (&sq)[NSS], int lane, int n) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NSS; ++j)
+    if (lane + 64 * j < n) s += sq[j];
+  return s;
+}
+
 }  // namespace q4nx
 
 // ---------------------------------------------------------------- host-side error plumbing

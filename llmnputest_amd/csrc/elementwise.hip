@@ -104,30 +104,47 @@ __global__ __launch_bounds__(256) void round_bf16_kernel(const float* __restrict
   if (i < n) y[i] = f32_to_bf16(x[i]);
 }
 
-// ------------------------------------------------------------------ embedding row of a q8 matrix
-__global__ __launch_bounds__(256) void embed_q8_kernel(const uint8_t* __restrict__ w,
-                                                       const int32_t* __restrict__ tokens,
-                                                       float* __restrict__ h,
-                                                       float* __restrict__ ssq_out, int vocab,
-                                                       int hidden) {
+// ------------------------------------------------------------------ embedding rows
+// h[b][c] = row tokens[b] of a [vocab][hidden] table: bf16 (KIND 16), or q4 / q8 tiles
+// dequantised as tools/q4nx.py:127-143 does (q4: code * d + m with one rounding, q8: code * s).
+template <int KIND>
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ w,
+                                                    const int32_t* __restrict__ tokens,
+                                                    float* __restrict__ h,
+                                                    float* __restrict__ ssq_out, int vocab,
+                                                    int hidden) {
   const int b = blockIdx.y;
   const int c = blockIdx.x * 256 + threadIdx.x;   // hidden % 256 == 0: every lane is live
   const int t = tokens[b];
-  float v = __builtin_nanf("");
+  float v = __builtin_nanf("");                   // a token out of range gives a NaN row
   if (t >= 0 && t < vocab) {
-    const int k_t = hidden / 256;
-    const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
-    const int kt = c >> 8, k = c & 255, kb = k >> 5;
-    const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
-    const int g = kb * 32 + rb * 16 + r;
-    const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
-    const int code = (int)(int8_t)tile[kMetaBytes + rb * 4096 + k * 16 + r];
-    v = (float)code * bf16_to_f32(s);
+    if constexpr (KIND == Q4NX_KIND_BF16) {
+      v = bf16_to_f32(((const uint16_t*)w)[(size_t)t * hidden + c]);
+    } else {
+      const int k_t = hidden / 256;
+      const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
+      const int kt = c >> 8, k = c & 255, kb = k >> 5;
+      const int g = kb * 32 + rb * 16 + r;
+      const int i = rb * 4096 + k * 16 + r;        // weight index inside the tile
+      if constexpr (KIND == Q4NX_KIND_Q8) {
+        const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
+        const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
+        v = (float)(int)(int8_t)tile[kMetaBytes + i] * bf16_to_f32(s);
+      } else {
+        const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ4TileBytes;
+        const uint16_t d = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
+        const uint16_t m = (uint16_t)tile[kMetaBytes + 2 * g] |
+                           ((uint16_t)tile[kMetaBytes + 2 * g + 1] << 8);
+        const uint8_t byte = tile[2 * kMetaBytes + (i >> 1)];
+        const int code = (i & 1) ? (byte >> 4) : (byte & 15);   // low nibble = even index
+        v = __fmul_rn((float)code, bf16_to_f32(d)) + bf16_to_f32(m);
+      }
+    }
   }
   h[(size_t)b * hidden + c] = v;
-  if (ssq_out != nullptr) {   // sum of squares per 32 entries, for a following RMSNorm
-    const float s32 = group32_sum(v * v);
-    if ((c & 31) == 0) ssq_out[(size_t)b * (hidden / 32) + (c >> 5)] = s32;
+  if (ssq_out != nullptr) {   // sum of squares per 16 entries, for a following RMSNorm
+    const float s16 = group16_sum(v * v);
+    if ((c & 15) == 0) ssq_out[(size_t)b * (hidden / 16) + (c >> 4)] = s16;
   }
 }
 
@@ -287,14 +304,25 @@ int q4nx_round_bf16(const float* x, uint16_t* y, int64_t n, void* stream) {
   return check_launch("q4nx_round_bf16");
 }
 
-int q4nx_embed_q8(const uint8_t* w, const int32_t* tokens, float* h, float* ssq_out, int vocab,
-                  int hidden, int batch, void* stream) {
-  Q4NX_REQUIRE(w && tokens && h, Q4NX_ERR_ARG, "q4nx_embed_q8: w, tokens and h are required");
-  Q4NX_REQUIRE(vocab > 0 && vocab % 32 == 0 && hidden > 0 && hidden % 256 == 0 && batch > 0,
-               Q4NX_ERR_SHAPE, "q4nx_embed_q8: vocab=%d hidden=%d batch=%d", vocab, hidden, batch);
-  hipLaunchKernelGGL(embed_q8_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0,
-                     (hipStream_t)stream, w, tokens, h, ssq_out, vocab, hidden);
-  return check_launch("q4nx_embed_q8");
+int q4nx_embed(int kind, const void* table, const int32_t* tokens, float* h, float* ssq_out,
+               int vocab, int hidden, int batch, void* stream) {
+  const char* what = "q4nx_embed";
+  Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8 || kind == Q4NX_KIND_BF16,
+               Q4NX_ERR_ARG, "%s: kind must be Q4NX_KIND_Q4, _Q8 or _BF16, got %d", what, kind);
+  Q4NX_REQUIRE(table && tokens && h, Q4NX_ERR_ARG, "%s: table, tokens and h are required", what);
+  Q4NX_REQUIRE(vocab > 0 && (kind == Q4NX_KIND_BF16 || vocab % 32 == 0) && hidden > 0 &&
+                   hidden % 256 == 0 && batch > 0,
+               Q4NX_ERR_SHAPE, "%s: vocab=%d hidden=%d batch=%d", what, vocab, hidden, batch);
+  const dim3 grid(hidden / 256, batch);
+  const uint8_t* w = (const uint8_t*)table;
+  hipStream_t s = (hipStream_t)stream;
+  if (kind == Q4NX_KIND_BF16)
+    hipLaunchKernelGGL(embed_kernel<Q4NX_KIND_BF16>, grid, dim3(256), 0, s, w, tokens, h, ssq_out, vocab, hidden);
+  else if (kind == Q4NX_KIND_Q8)
+    hipLaunchKernelGGL(embed_kernel<Q4NX_KIND_Q8>, grid, dim3(256), 0, s, w, tokens, h, ssq_out, vocab, hidden);
+  else
+    hipLaunchKernelGGL(embed_kernel<Q4NX_KIND_Q4>, grid, dim3(256), 0, s, w, tokens, h, ssq_out, vocab, hidden);
+  return check_launch(what);
 }
 
 int q4nx_argmax(const float* logits, int n, int batch, int64_t stride, int32_t* idx,

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.h"
+#include "policy.h"
 
 namespace q4nx {
 
@@ -15,7 +16,7 @@ struct GemmArgs {
   int n_tr[3];
   int grp_q, grp_k;      // QKV: groups [0, grp_q) are q heads, then k heads, then v heads
   // input: bf16 x, or (norm) fp32 residual h normalised with norm_w and the producer's sums
-  // of squares ssq_in [m][K/32]
+  // of squares ssq_in [m][K/16]
   const uint16_t* x;
   const float* hres;
   const uint16_t* norm_w;
@@ -28,8 +29,8 @@ struct GemmArgs {
   float* y;
   int64_t y_stride;
   const float* residual;
-  float* ssq_out;                    // [m][n_tr] sums of y^2 per tile-row
-  unsigned long long* argmax_keys;   // [m][n_tr] (max, first row) keys per tile-row
+  float* ssq_out;                    // [m][2 n_tr] sums of y^2 per 16-row block
+  unsigned long long* argmax_keys;   // [m][2 n_tr] (max, first row) keys per 16-row block
   // GATEUP / QKV: fp32 values before the epilogue (optional)
   float* raw_out;
   uint16_t* h_out;
@@ -48,14 +49,14 @@ struct GemmArgs {
   unsigned* counters;    // one arrival counter per (group, m-block)
 };
 
-// true when `rows` rows of kind `kind` run on the matrix cores (q4nx_set_mfma_rows)
-bool mfma_use(int kind, int rows);
+// true when `rows` rows of kind `kind` run on the matrix cores under the policy
+bool mfma_use(int kind, int rows, const Policy& P);
 // workspace bytes of a launch of `n_units` tile-rows (PLAIN) or output groups (fused)
-size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows);
+size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows, const Policy& P);
 // whether ws_bytes holds the normalised rows an RMSNorm prologue needs on this path
 bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes);
 // launches `a` (all but the split-K fields filled in); returns Q4NX_OK or an error code
 int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
-                hipStream_t st, const char* what);
+                const Policy& P, hipStream_t st, const char* what);
 
 }  // namespace q4nx

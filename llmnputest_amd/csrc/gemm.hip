@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   static_assert(OP == GOP_PLAIN || RT == 2, "fused epilogues pair two tile-rows");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ int s_last;
-  __shared__ unsigned long long skey[OP == GOP_PLAIN ? MB * RT : 1];
+  __shared__ unsigned long long skey[OP == GOP_PLAIN ? MB * RT * 2 : 1];
 
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int wk = wave % WK, wm = wave / WK;
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int n_tr = a.n_tr[0];
     const int tr0 = group * RT;
     if (a.argmax_keys != nullptr) {
-      for (int e = tid; e < MB * RT; e += 256) skey[e] = 0ull;
+      for (int e = tid; e < MB * RT * 2; e += 256) skey[e] = 0ull;
       __syncthreads();
     }
     for (int e0 = 0; e0 < MB * NW; e0 += 256) {   // MB * NW is a multiple of 256
@@ -327,18 +327,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         v = *outp(m, n);
         if (a.residual != nullptr) v += a.residual[gm * a.y_stride + gn];
         if (a.y != nullptr) a.y[gm * a.y_stride + gn] = v;
-        if (a.argmax_keys != nullptr) atomicMax(&skey[m * RT + n / 32], argmax_key(v, (uint32_t)gn));
+        if (a.argmax_keys != nullptr) atomicMax(&skey[m * RT * 2 + n / 16], argmax_key(v, (uint32_t)gn));
       }
-      if (a.ssq_out != nullptr) {
-        const float sq32 = group32_sum(v * v);
-        if (live && (n & 31) == 0) a.ssq_out[(int64_t)gm * n_tr + tr0 + n / 32] = sq32;
+      if (a.ssq_out != nullptr) {   // per 16-row block
+        const float sq16 = group16_sum(v * v);
+        if (live && (n & 15) == 0) a.ssq_out[(int64_t)gm * n_tr * 2 + tr0 * 2 + n / 16] = sq16;
       }
     }
     if (a.argmax_keys != nullptr) {
       __syncthreads();
-      for (int e = tid; e < MB * RT; e += 256) {
-        const int gm = mblk * MB + e / RT;
-        if (gm < a.m_rows) a.argmax_keys[(int64_t)gm * n_tr + tr0 + e % RT] = skey[e];
+      for (int e = tid; e < MB * RT * 2; e += 256) {
+        const int gm = mblk * MB + e / (RT * 2);
+        if (gm < a.m_rows) a.argmax_keys[(int64_t)gm * n_tr * 2 + tr0 * 2 + e % (RT * 2)] = skey[e];
       }
     }
   } else if constexpr (OP == GOP_GATEUP) {
@@ -396,10 +396,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 }
 
 // RMSNorm of the input rows into bf16, once per launch, before a contraction that needs it:
-// xn[m][k] = bf16((h[m][k] * r_m) * w[k]), r_m = 1/sqrt(sum(ssq[m]) / K + eps) with the sums
-// of squares added in the order of the VALU GEMV's prologue (lane l takes entries l, l+64,
-// l+128, l+192; the wave sums the lanes), so both kernel families see the same input.
-// granite_rmsnorm.h:45-80. One workgroup per row; K % 256 == 0, K / 32 <= 256.
+// xn[m][k] = bf16((h[m][k] * r_m) * w[k]), r_m = 1/sqrt(sum(ssq[m]) / K + eps) with the K/16
+// sums of squares added in the order every GEMV prologue uses (ssq_lane_sum, then
+// wave_sum), so all kernel families see the same input. granite_rmsnorm.h:45-80. One
+// workgroup per row; K % 256 == 0, K <= 8192.
 __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h, int64_t h_stride,
                                                     const float* __restrict__ ssq,
                                                     const uint16_t* __restrict__ w, float eps,
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h,
                                                     int64_t xn_stride) {
   constexpr int kMaxChunks = 4;   // 8-entry chunks per thread: K <= 8192
   const int m = blockIdx.x, tid = threadIdx.x, l = tid & 63;
-  const int n_ss = K / 32, n_ch = K / 8;
+  const int n_ss = K / kSsqRows, n_ch = K / 8;
   const float* hr = h + (int64_t)m * h_stride;
   // the row and the weights are requested before the sums of squares are added up, so the
   // kernel waits on memory once
@@ -423,11 +423,10 @@ __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h,
     }
   }
   const float* srow = ssq + (int64_t)m * n_ss;
-  float part = 0.f;
+  float sq[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (l + 64 * j < n_ss) part += srow[l + 64 * j];
-  const float inv = 1.0f / sqrtf(wave_sum(part) / (float)K + eps);
+  for (int j = 0; j < 8; ++j) sq[j] = srow[min(l + 64 * j, n_ss - 1)];
+  const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<8>(sq, l, n_ss)) / (float)K + eps);
   uint16_t* xr = xn + (int64_t)m * xn_stride;
 #pragma unroll
   for (int i = 0; i < kMaxChunks; ++i) {
@@ -449,14 +448,12 @@ struct GemmPlan {
   int rt, mt, wk, ksplit, kpp, mb, m_blocks, groups;
 };
 
-static std::atomic<int> g_gemm_ksplit{0};   // 0: automatic; process-wide, read once per launch
-
 // Workgroup shape by row count: up to 16 rows the four waves split K; more rows go to more
 // waves and, past 32, two m-tiles per wave. Past 64 rows (prefill) a workgroup takes two
 // tile-rows, halving the x traffic (the fused epilogues always pair two tile-rows); q8 keeps
 // one so the staging stays under 64 KB of LDS.
 // n_units: tile-rows for PLAIN, output groups (of two tile-rows) for GATEUP and QKV.
-static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows) {
+static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows, const Policy& P) {
   GemmPlan p{};
   if (m_rows <= 16) {
     p.mt = 1; p.wk = 4;
@@ -478,7 +475,7 @@ static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows) {
   p.m_blocks = (m_rows + p.mb - 1) / p.mb;
   const int wgs = p.groups * p.m_blocks;
   int ks = 1;
-  const int forced = g_gemm_ksplit.load(std::memory_order_relaxed);
+  const int forced = P.gemm_ksplit;
   if (forced > 0) {
     ks = forced;
   } else if (wgs < 192 && k_t >= 4) {
@@ -526,18 +523,15 @@ static void gemm_launch_op(const GemmArgs& a, const GemmPlan& p, hipStream_t st)
   else if constexpr (OP == GOP_PLAIN) gemm_launch_t<KIND, OP, 1, 2, 1>(a, p, st);
 }
 
-// Rows from which the GEMV entry points run on the matrix cores, per kind (0: never).
-// Measured on MI355X: q4 from 2 rows (one row is as fast on the VALU kernel), q8 from one.
-static std::atomic<int> g_mfma_rows[2] = {{2}, {1}};
-
-bool mfma_use(int kind, int rows) {
-  const int t = g_mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0].load(std::memory_order_relaxed);
+// Whether `rows` rows of `kind` run on the matrix cores under the policy (mfma_rows: 0 never).
+bool mfma_use(int kind, int rows, const Policy& P) {
+  const int t = P.mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0];
   return t > 0 && rows >= t;
 }
 
-size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows) {
+size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows, const Policy& P) {
   // room for the split-K records and for the normalised rows of an RMSNorm prologue
-  const size_t split = split_part_bytes(plan_gemm(kind, op, n_units, k_t, m_rows));
+  const size_t split = split_part_bytes(plan_gemm(kind, op, n_units, k_t, m_rows, P));
   return Q4NX_WS_COUNTER_BYTES + align256(split) + align256((size_t)m_rows * k_t * kTileK * 2);
 }
 
@@ -549,11 +543,11 @@ bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes) {
 // sets the split-K fields from the plan and the workspace. With norm_w set, the rows are
 // normalised once into xn_out (when given) or the workspace, then contracted as bf16.
 int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
-                hipStream_t st, const char* what) {
+                const Policy& P, hipStream_t st, const char* what) {
   Q4NX_REQUIRE(op == GOP_PLAIN || kind == Q4NX_KIND_Q4, Q4NX_ERR_ARG,
                "%s: fused epilogues take q4 tiles", what);
   const int K = a.k_t * kTileK;
-  GemmPlan p = plan_gemm(kind, op, n_units, a.k_t, a.m_rows);
+  GemmPlan p = plan_gemm(kind, op, n_units, a.k_t, a.m_rows, P);
   size_t split = split_part_bytes(p);
   const size_t xn_b = a.norm_w != nullptr && a.xn_out == nullptr
                           ? align256((size_t)a.m_rows * K * 2) : 0;
@@ -566,7 +560,7 @@ int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_
   if (a.norm_w != nullptr) {
     Q4NX_REQUIRE(a.ssq_in != nullptr, Q4NX_ERR_ARG,
                  "%s: the matrix-core RMSNorm prologue needs the sums of squares ssq_in", what);
-    Q4NX_REQUIRE(K / 32 <= 256, Q4NX_ERR_SHAPE, "%s: RMSNorm prologue supports K <= 8192", what);
+    Q4NX_REQUIRE(K / kSsqRows <= 512, Q4NX_ERR_SHAPE, "%s: RMSNorm prologue supports K <= 8192", what);
     uint16_t* xn = a.xn_out;
     int64_t xs = a.x_stride;
     if (xn == nullptr) {
@@ -605,32 +599,21 @@ using namespace q4nx;
 
 extern "C" {
 
-int q4nx_set_gemm_ksplit(int parts) {
-  Q4NX_REQUIRE(parts >= 0 && parts <= 8, Q4NX_ERR_ARG,
-               "K parts per workgroup group must be 0 (automatic) or 1..8, got %d", parts);
-  g_gemm_ksplit = parts;
-  return Q4NX_OK;
-}
-
-size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows) {
+size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows,
+                          const q4nx_policy* policy) {
+  Policy P;
   if ((kind != Q4NX_KIND_Q4 && kind != Q4NX_KIND_Q8) || n_tile_rows < 1 || k_tiles < 1 ||
-      m_rows < 1)
+      m_rows < 1 || !resolve_policy_quiet(policy, &P))
     return 0;
-  return gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, n_tile_rows, k_tiles, m_rows));
-}
-
-int q4nx_set_mfma_rows(int kind, int min_rows) {
-  Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
-               "kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", kind);
-  Q4NX_REQUIRE(min_rows >= 0, Q4NX_ERR_ARG, "min_rows must be >= 0, got %d", min_rows);
-  g_mfma_rows[kind == Q4NX_KIND_Q8 ? 1 : 0] = min_rows;
-  return Q4NX_OK;
+  return gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, n_tile_rows, k_tiles, m_rows, P));
 }
 
 int q4nx_gemm(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const uint16_t* x,
               int64_t x_stride, int m_rows, float* y, int64_t y_stride, const float* residual,
-              void* ws, size_t ws_bytes, void* stream) {
+              void* ws, size_t ws_bytes, const q4nx_policy* policy, void* stream) {
   const char* what = "q4nx_gemm";
+  Policy P;
+  if (int rc = resolve_policy(policy, &P, what)) return rc;
   Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
                "%s: kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", what, kind);
   Q4NX_REQUIRE(w != nullptr && Q4NX_ALIGNED(w, 16), Q4NX_ERR_ARG,
@@ -661,7 +644,7 @@ int q4nx_gemm(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const ui
   a.y_stride = y_stride;
   a.m_rows = m_rows;
   a.k_t = k_tiles;
-  return mfma_launch(kind, GOP_PLAIN, a, n_tile_rows, ws, ws_bytes, (hipStream_t)stream, what);
+  return mfma_launch(kind, GOP_PLAIN, a, n_tile_rows, ws, ws_bytes, P, (hipStream_t)stream, what);
 }
 
 }  // extern "C"

@@ -39,6 +39,8 @@
 #include <atomic>
 #include "common.h"
 #include "gemm.h"
+#include "gemv1.h"
+#include "policy.h"
 
 #include <climits>
 
@@ -59,13 +61,13 @@ struct GemvArgs {
   int64_t x_stride;
   const uint16_t* norm_w;
   float eps;
-  const float* ssq_in;   // optional [batch][K/32] sums of squares of x, per 32 entries
+  const float* ssq_in;   // optional [batch][K/16] sums of squares of x, per 16 entries
   uint16_t* xn_out;
   // plain
   float* y;
   int64_t y_stride;
   const float* residual;
-  float* ssq_out;        // optional [batch][n_tile_rows] sums of squares of y per tile-row
+  float* ssq_out;        // optional [batch][N/16] sums of squares of y per 16-row block
   // qkv
   uint16_t* q_out;
   uint16_t* k_cache;
@@ -79,65 +81,15 @@ struct GemvArgs {
   // gate/up
   uint16_t* h_out;
   int64_t h_stride;
-  // plain: optional argmax keys, uint64 [batch][n_tile_rows] (order-preserving (value, -row))
+  // plain: optional argmax keys, uint64 [batch][N/16] (order-preserving (value, -row) per
+  // 16-row block)
   unsigned long long* argmax_keys;
   // split K: partial sums [group][part][batch][G*32] fp32 and one arrival counter per group
   int ksplit;
   float* part;
   uint32_t part_bytes;
   unsigned* counters;
-  // stage of a multi-stage launch: activations come from an earlier stage of the same
-  // launch (read and written system-coherent), after wait_cnt reaches wait_target
-  int sys_io;
-  const unsigned* wait_cnt;
-  unsigned wait_target;
-  unsigned* err;
-  // o-projection from attention split records (batch 1): x[k] is the bf16 of head k / 64's
-  // output merged from att_split records at att_rec ([kv head][split][head in group][68])
-  const float* att_rec;
-  int att_split, att_g;
 };
-
-// Output stores: plain, or system-coherent when a later stage of the same launch reads them.
-template <typename T>
-__device__ __forceinline__ void put(T* p, T v, int sys) {
-  if (sys) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  else *p = v;
-}
-__device__ __forceinline__ void put4(uint4* p, uint4 v, int sys) {
-  if (sys) {
-    uint32_t* q = (uint32_t*)p;
-    __hip_atomic_store(q, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(q + 1, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(q + 2, v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(q + 3, v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  } else {
-    *p = v;
-  }
-}
-
-constexpr int kCounterReplicas = 8;   // one per XCD (workgroup i runs on XCD i mod 8)
-
-// Waits (one thread, bounded) until an earlier stage has completed `target` items; the
-// rest of the workgroup waits at the barrier. On timeout the error flag is raised and the
-// workgroup goes on (its results are then invalid), so every wave always finishes.
-__device__ __forceinline__ void stage_wait(const unsigned* cnt, unsigned target, unsigned* err) {
-  if (threadIdx.x == 0) {
-    // each XCD's workgroups poll their own replica of the counter (the producers add to
-    // all of them), so no single memory channel serves every poll
-    const unsigned* c = cnt + (blockIdx.x & (kCounterReplicas - 1));
-    unsigned spins = 0;
-    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) < target) {
-      if (++spins > (1u << 22) ||
-          __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != 0u) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(8);
-    }
-  }
-  __syncthreads();
-}
 
 constexpr int kMaxWaves = 16;
 
@@ -167,9 +119,7 @@ __device__ __forceinline__ void transpose_reduce4(const float (&v)[16], float (&
 
 // One work item (an output group, or one K part of it) of a GEMV launch. Returns true when
 // this workgroup ran the epilogue (for a split group, only the last part to arrive does).
-// XNS > 0: the activations are attention split records to merge (see GemvArgs::att_rec),
-// at most XNS of them (one tile-row of one member, a wave per K-tile, no K split).
-template <int KIND, int B, int TPW, bool SYS, int XNS = 0>
+template <int KIND, int B, int TPW>
 __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   constexpr int TB = KIND == 4 ? kQ4TileBytes : kQ8TileBytes;
   constexpr int NCH = KIND == 4 ? 4 : 8;              // 16-byte chunks per lane per tile
@@ -177,7 +127,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   __shared__ float sred[kMaxWaves][B][32];
   __shared__ float sgrp[B][64];
   __shared__ float snorm[kMaxWaves][B];
-  __shared__ unsigned long long skey[B];
+  __shared__ unsigned long long skey[B][2];
   __shared__ int s_last;
 
   // wave-uniform values live in scalar registers: the weight pointer below must be known
@@ -223,30 +173,20 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 
   // ---- 1. activations. Every load is unconditional, from a valid address (clamped row,
   //         or the weights as a stand-in), so nothing waits before the weight stream is
-  //         issued; rows past the batch are masked where the values are used. A stage of a
-  //         multi-stage launch loads them after its weights, once the producer is done, and
-  //         system-coherent (the producer may have run on another XCD).
+  //         issued; rows past the batch are masked where the values are used.
   uint4 ar[B][TPW][2];    // raw activation bytes: 8 bf16 x (first 16 B) or 8 fp32 h (32 B)
   uint4 nw[TPW];
   const bool pre_ssq = norm && a.ssq_in != nullptr;
-  const int n_ss = K / 32;
-  float sq[B][4];
+  const int n_ss = K / kSsqRows;
+  constexpr int kSsqLoads = 8;   // K / 16 <= 512 partial sums per row
+  float sq[B][kSsqLoads];
   constexpr int kSsqIt = 3;
   float4 hs[B][kSsqIt];
   const bool split_norm = norm && ks > 1 && !pre_ssq;
-  // SYS: a stage of a multi-stage launch, whose activations and outputs cross workgroups
-  // of the same launch (system-coherent loads and stores). A compile-time choice: loads in
-  // runtime branches make the compiler wait for them at the join, before the weight stream.
-  constexpr int sys = SYS ? 1 : 0;
-  float ep_res = 0.f;   // epilogue prefetches (see the end of load_acts)
+  float ep_res = 0.f;   // epilogue prefetches (see the end of this block)
   int ep_pos = 0;
-  constexpr bool XREC = XNS > 0;
-  float4 rec_acc[XREC ? XNS : 1];
-  float2 rec_ml[2];
-  auto load_acts = [&]() {
+  {
     const void* xbase = norm ? (const void*)a.hres : (const void*)a.x;
-    const uint32_t xbytes = (uint32_t)((size_t)a.batch * a.x_stride * (norm ? 4 : 2));
-    const __amdgpu_buffer_rsrc_t xr_ = make_rsrc(xbase, xbytes);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int kt = min(kt0 + t, kt_hi - 1);
@@ -255,47 +195,20 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 #pragma unroll
       for (int b = 0; b < B; ++b) {
         const int bb = min(b, a.batch - 1);
-        const uint32_t off = (uint32_t)(((size_t)bb * a.x_stride + k) * (norm ? 4 : 2));
-        if constexpr (SYS) {
-          ar[b][t][0] = ld16_sys(xr_, off);
-          ar[b][t][1] = ld16_sys(xr_, norm ? off + 16 : off);
-        } else if constexpr (!XREC) {
-          const uint4* src = (const uint4*)((const uint8_t*)xbase + off);
-          ar[b][t][0] = src[0];
-          ar[b][t][1] = src[norm ? 1 : 0];
-        }
+        const size_t off = ((size_t)bb * a.x_stride + k) * (norm ? 4 : 2);
+        const uint4* src = (const uint4*)((const uint8_t*)xbase + off);
+        ar[b][t][0] = src[0];
+        ar[b][t][1] = src[norm ? 1 : 0];
       }
     }
-    // attention split records, ahead of the weights: the (m, l) pairs of this wave's four
-    // heads (4 x splits <= 72 pairs, two per lane) and this thread's four activations
-    // 4 tid .. 4 tid + 3 (one head) in every split (clamped: the last split again)
-    if constexpr (XREC) {
-      const int e0 = 4 * tid, h = e0 >> 6, kvh = h / a.att_g, hh = h - kvh * a.att_g;
-      const float* r0 = a.att_rec + ((size_t)kvh * a.att_split * a.att_g + hh) * kAttnRecFloats;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int p = min(lane + 64 * j, 4 * a.att_split - 1);
-        const int ph = 4 * wave + p / a.att_split, pi = p % a.att_split, pk = ph / a.att_g;
-        const size_t rec = ((size_t)pk * a.att_split + pi) * a.att_g + ph - pk * a.att_g;
-        rec_ml[j] = *(const float2*)(a.att_rec + rec * kAttnRecFloats + 64);
-      }
-#pragma unroll
-      for (int i = 0; i < XNS; ++i) {
-        const float* r = r0 + (size_t)min(i, a.att_split - 1) * a.att_g * kAttnRecFloats;
-        rec_acc[i] = *(const float4*)(r + (e0 & 63));
-      }
-    }
-    // RMSNorm sum of squares handed over by the producer of x: K/32 partials per row,
-    // every wave sums them itself (same order everywhere) and needs no other wave
+    // RMSNorm sums of squares handed over by the producer of x: K/16 partials per row,
+    // every wave sums them itself (the order of ssq_lane_sum) and needs no other wave
     if (pre_ssq) {
 #pragma unroll
       for (int b = 0; b < B; ++b)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float* src = a.ssq_in + min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1);
-          if constexpr (SYS) sq[b][j] = load_sys(src);
-          else sq[b][j] = *src;
-        }
+        for (int j = 0; j < kSsqLoads; ++j)
+          sq[b][j] = a.ssq_in[min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1)];
     }
     // with K split and no partials given, this workgroup's tiles see only part of the row:
     // the sum of squares reads the whole row (strided over all threads; three float4 per
@@ -305,34 +218,21 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       for (int it = 0; it < kSsqIt; ++it) {
         const int i = min(tid + it * (int)blockDim.x, K / 4 - 1);
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
-          const uint32_t off = (uint32_t)(((size_t)min(b, a.batch - 1) * a.x_stride + 4 * i) * 4);
-          if constexpr (SYS) {
-            const uint4 u = ld16_sys(xr_, off);
-            hs[b][it] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y),
-                                    __uint_as_float(u.z), __uint_as_float(u.w));
-          } else {
-            hs[b][it] = *(const float4*)((const uint8_t*)a.hres + off);
-          }
-        }
+        for (int b = 0; b < B; ++b)
+          hs[b][it] = *(const float4*)(a.hres + (size_t)min(b, a.batch - 1) * a.x_stride + 4 * i);
       }
     }
     // the epilogue's own inputs for this thread's first output (batch row tid / 32, row
     // tid % 32 of the group): the residual (plain) or the sequence position (q/k/v), in
     // flight with the activations instead of a memory round trip after the reduction.
     // Unconditional loads, from the weights when the launch has no such input.
-    {
-      const int eb = min(tid >> 5, a.batch - 1), er = tid & 31;
-      const bool res = a.op == OP_PLAIN && a.residual != nullptr;
-      const float* rp = res ? a.residual + (int64_t)eb * a.y_stride + (int64_t)tr * 32 + er
-                            : (const float*)a.w[0];
-      if constexpr (SYS) ep_res = load_sys(rp);
-      else ep_res = *rp;
-      ep_pos = *(a.op == OP_QKV ? a.pos + eb : (const int32_t*)a.w[0]);
-    }
-  };
-  const bool staged = SYS && a.wait_cnt != nullptr;
-  if (!staged) load_acts();
+    const int eb = min(tid >> 5, a.batch - 1), er = tid & 31;
+    const bool res = a.op == OP_PLAIN && a.residual != nullptr;
+    const float* rp = res ? a.residual + (int64_t)eb * a.y_stride + (int64_t)tr * 32 + er
+                          : (const float*)a.w[0];
+    ep_res = *rp;
+    ep_pos = *(a.op == OP_QKV ? a.pos + eb : (const int32_t*)a.w[0]);
+  }
 
   // ---- 2. weights and per-group metadata of every tile of this wave
   uint4 wq[TPW][NCH];
@@ -351,59 +251,6 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       mm[t] = make_uint2(0, 0);
       if (KIND == 4) mm[t] = *(const uint2*)(tile + kMetaBytes + 2 * g);
     }
-  }
-
-  if (staged) {
-    stage_wait(a.wait_cnt, a.wait_target, a.err);
-    load_acts();
-  }
-
-  // attention records -> the bf16 activations: wave w owns K-tile w (heads 4w .. 4w + 3),
-  // so each wave merges exactly the 256 activations it uses, and its (m, l) pairs and merged
-  // row pass through its own slice of LDS (in order within the wave: no workgroup barrier).
-  // Each thread merges its four in split order with the operations of the attention
-  // kernel's last workgroup, so the row is the one that kernel would have written.
-  if constexpr (XREC) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_x[kAttnRecMaxKTiles * kTileK];
-    __shared__ float2 s_ml[kAttnRecMaxKTiles][4 * kAttnRecMaxSplits];   // [wave][head][split]
-    const int ns = a.att_split;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)   // past the end: the last pair again, the same value
-      s_ml[wave][min(lane + 64 * j, 4 * ns - 1)] = rec_ml[j];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float2* ml = &s_ml[wave][(lane >> 4) * ns];   // this thread's head
-    float2 mv[XNS];
-#pragma unroll
-    for (int i = 0; i < XNS; ++i) mv[i] = ml[min(i, ns - 1)];
-    float M = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < XNS; ++i)
-      if (i < ns) M = fmaxf(M, mv[i].x);
-    float L = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int i = 0; i < XNS; ++i)
-        if (i < ns) {
-          const float f = __builtin_amdgcn_exp2f(mv[i].x - M);
-          L = fmaf(mv[i].y, f, L);
-          A0 = fmaf(rec_acc[i].x, f, A0);
-          A1 = fmaf(rec_acc[i].y, f, A1);
-          A2 = fmaf(rec_acc[i].z, f, A2);
-          A3 = fmaf(rec_acc[i].w, f, A3);
-        }
-    }
-    const float o0 = L > 0.f ? A0 / L : 0.f, o1 = L > 0.f ? A1 / L : 0.f;
-    const float o2 = L > 0.f ? A2 / L : 0.f, o3 = L > 0.f ? A3 / L : 0.f;
-    *(uint2*)(s_x + 4 * tid) = make_uint2(
-        (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16),
-        (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16));
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    ar[0][0][0] = *(const uint4*)(s_x + kt0 * kTileK + kx);   // kt0 = wave
-    ar[0][0][1] = ar[0][0][0];
   }
 
   // the activations are used from here on (their waits come after the weight stream)
@@ -433,11 +280,13 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   }
   if (pre_ssq) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      float4 v = make_float4(sq[b][0], sq[b][1], sq[b][2], sq[b][3]);
-      pin(v);
-      sq[b][0] = v.x; sq[b][1] = v.y; sq[b][2] = v.z; sq[b][3] = v.w;
-    }
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int j = 0; j < kSsqLoads; j += 4) {
+        float4 v = make_float4(sq[b][j], sq[b][j + 1], sq[b][j + 2], sq[b][j + 3]);
+        pin(v);
+        sq[b][j] = v.x; sq[b][j + 1] = v.y; sq[b][j + 2] = v.z; sq[b][j + 3] = v.w;
+      }
   }
 
   uint4 xr[B][TPW];       // 8 bf16 per lane per tile
@@ -471,9 +320,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       if (b < a.batch)
         for (int i = tid + kSsqIt * (int)blockDim.x; i < K / 4; i += blockDim.x) {
           const float* hp = a.hres + b * a.x_stride + 4 * i;
-          const float4 h = SYS ? make_float4(load_sys(hp), load_sys(hp + 1), load_sys(hp + 2),
-                                             load_sys(hp + 3))
-                               : *(const float4*)hp;
+          const float4 h = *(const float4*)hp;
           ssq[b] = fmaf(h.x, h.x, fmaf(h.y, h.y, fmaf(h.z, h.z, fmaf(h.w, h.w, ssq[b]))));
         }
     }
@@ -481,13 +328,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   float inv_rms[B];
   if (pre_ssq) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (lane + 64 * j < n_ss) s += sq[b][j];
-      inv_rms[b] = 1.0f / sqrtf(wave_sum(s) / (float)K + a.eps);
-    }
+    for (int b = 0; b < B; ++b)
+      inv_rms[b] = 1.0f / sqrtf(wave_sum(ssq_lane_sum<kSsqLoads>(sq[b], lane, n_ss)) / (float)K + a.eps);
   } else if (norm) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
@@ -532,7 +374,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         xr[b][t] = b < a.batch ? make_uint4(o[0], o[1], o[2], o[3]) : make_uint4(0, 0, 0, 0);
         if (a.xn_out != nullptr && group == 0 && member == 0 && rb == 0 && t < ntw &&
             b < a.batch)
-          put4((uint4*)(a.xn_out + b * a.x_stride + (kt0 + t) * kTileK + kx), xr[b][t], sys);
+          *(uint4*)(a.xn_out + b * a.x_stride + (kt0 + t) * kTileK + kx) = xr[b][t];
       }
     }
   }
@@ -748,7 +590,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 
   // ---- 8. epilogue on the whole group
   if (a.op == OP_PLAIN) {
-    if (a.argmax_keys != nullptr && tid < B) skey[tid] = 0ull;
+    if (a.argmax_keys != nullptr && tid < 2 * B) skey[tid >> 1][tid & 1] = 0ull;
     if (a.argmax_keys != nullptr) __syncthreads();
     for (int e0 = 0; e0 < B * 32; e0 += blockDim.x) {   // uniform trip count: 32-lane sums
       const int e = e0 + tid;
@@ -759,17 +601,18 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         const int64_t n = (int64_t)tr * 32 + r;
         v = sgrp[b][r];
         if (a.residual != nullptr) v += e0 == 0 ? ep_res : a.residual[b * a.y_stride + n];
-        if (a.y != nullptr) put(a.y + b * a.y_stride + n, v, sys);
-        if (a.argmax_keys != nullptr) atomicMax(&skey[b], argmax_key(v, (uint32_t)n));
+        if (a.y != nullptr) a.y[b * a.y_stride + n] = v;
+        if (a.argmax_keys != nullptr) atomicMax(&skey[b][r >> 4], argmax_key(v, (uint32_t)n));
       }
-      if (a.ssq_out != nullptr) {   // sum of squares of the tile-row's 32 outputs
-        const float sq32 = group32_sum(v * v);
-        if (live && r == 0) put(a.ssq_out + (int64_t)b * a.n_tr[0] + tr, sq32, sys);
+      if (a.ssq_out != nullptr) {   // sum of squares of each 16-row block's outputs
+        const float sq16 = group16_sum(v * v);
+        if (live && (r & 15) == 0) a.ssq_out[(int64_t)b * a.n_tr[0] * 2 + tr * 2 + (r >> 4)] = sq16;
       }
     }
     if (a.argmax_keys != nullptr) {   // one slot per (batch row, tile-row): no contention
       __syncthreads();
-      if (tid < a.batch) a.argmax_keys[(int64_t)tid * a.n_tr[0] + tr] = skey[tid];
+      if (tid < 2 * a.batch)
+        a.argmax_keys[(int64_t)(tid >> 1) * a.n_tr[0] * 2 + tr * 2 + (tid & 1)] = skey[tid >> 1][tid & 1];
     }
   } else if (a.op == OP_GATEUP) {
     for (int e = tid; e < B * 32; e += blockDim.x) {
@@ -780,11 +623,11 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         const float g = bf16_to_f32(f32_to_bf16(gr));
         const float uu = bf16_to_f32(f32_to_bf16(ur));
         const float h = (g / (1.0f + expf(-g))) * uu;
-        put(a.h_out + b * a.h_stride + n, f32_to_bf16(h), sys);
+        a.h_out[b * a.h_stride + n] = f32_to_bf16(h);
         if (a.raw_out != nullptr) {
           const int64_t N = (int64_t)a.n_tr[0] * 32;
-          put(a.raw_out + b * 2 * N + n, gr, sys);
-          put(a.raw_out + b * 2 * N + N + n, ur, sys);
+          a.raw_out[b * 2 * N + n] = gr;
+          a.raw_out[b * 2 * N + N + n] = ur;
         }
       }
     }
@@ -803,8 +646,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         const float r0 = sgrp[b][d], r1 = sgrp[b][32 + d];
         if (a.raw_out != nullptr) {
           const int64_t Wd = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
-          put(a.raw_out + b * Wd + seg_off + hg * 64 + d, r0, sys);
-          put(a.raw_out + b * Wd + seg_off + hg * 64 + 32 + d, r1, sys);
+          a.raw_out[b * Wd + seg_off + hg * 64 + d] = r0;
+          a.raw_out[b * Wd + seg_off + hg * 64 + 32 + d] = r1;
         }
         const float x0 = bf16_to_f32(f32_to_bf16(r0));
         const float x1 = bf16_to_f32(f32_to_bf16(r1));
@@ -814,8 +657,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
         if (seg == 2) {
           if (pos_ok) {
             uint16_t* dst = a.v_cache + b * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
-            put(dst + d, f32_to_bf16(x0), sys);
-            put(dst + 32 + d, f32_to_bf16(x1), sys);
+            dst[d] = f32_to_bf16(x0);
+            dst[32 + d] = f32_to_bf16(x1);
           }
         } else if (pos_ok) {
           const float c = first ? ep_c : a.rope_tab[(int64_t)p * 64 + d];
@@ -825,8 +668,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
           uint16_t* dst = (seg == 0)
                               ? a.q_out + b * (int64_t)a.n_q_heads * 64 + hg * 64
                               : a.k_cache + b * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
-          put(dst + d, f32_to_bf16(y0), sys);
-          put(dst + 32 + d, f32_to_bf16(y1), sys);
+          dst[d] = f32_to_bf16(y0);
+          dst[32 + d] = f32_to_bf16(y1);
         }
       }
     }
@@ -836,61 +679,18 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 
 template <int KIND, int B, int TPW>
 __global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_kernel(GemvArgs a) {
-  (void)gemv_body<KIND, B, TPW, false>(a, blockIdx.x);
-}
-
-// The o-projection from attention split records: batch 1, one K-tile per wave, at most
-// kAttnRecMaxKTiles waves (the launch bound leaves room for the records in registers), at
-// most XNS splits (loads are issued for XNS; the launch picks the next even bucket).
-template <int XNS>
-__global__ __launch_bounds__(64 * kAttnRecMaxKTiles) void gemv_attn_kernel(GemvArgs a) {
-  (void)gemv_body<4, 1, 1, false, XNS>(a, blockIdx.x);
-}
-
-// A chain of GEMV stages in one launch: stage s owns workgroups [wg_begin[s], wg_begin[s+1])
-// and (after the first) waits until every item of stage s-1 is done before reading its
-// activations; its weights are already streaming by then. Workgroups are dispatched in
-// index order, so a waiting workgroup's producers were all dispatched before it and none
-// of them waits on a later stage: the chain always drains. The last item of the last
-// stage clears the stage counters for the next launch.
-constexpr int kMaxStages = 4;
-struct MultiGemvArgs {
-  GemvArgs st[kMaxStages];
-  int wg_begin[kMaxStages + 1];
-  int n_stages;
-  unsigned* done;      // one completion counter per stage
-  unsigned items[kMaxStages];
-};
-
-template <int KIND, int B, int TPW>
-__global__ __launch_bounds__(B <= 2 ? 1024 : 512) void gemv_multi_kernel(MultiGemvArgs m) {
-  __shared__ int s_final;
-  int s = 0;
-  while (s + 1 < m.n_stages && (int)blockIdx.x >= m.wg_begin[s + 1]) ++s;
-  const bool done_item = gemv_body<KIND, B, TPW, true>(m.st[s], blockIdx.x - m.wg_begin[s]);
-  if (!done_item) return;   // a split part that was not last: the last part signals
-  wait_vm();                // every output store of this item is acknowledged
-  __syncthreads();
-  if (threadIdx.x < (unsigned)kCounterReplicas) {
-    const unsigned prev = atomicAdd(&m.done[s * kCounterReplicas + threadIdx.x], 1u);
-    if (threadIdx.x == 0) s_final = (s == m.n_stages - 1 && prev == m.items[s] - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (s_final && threadIdx.x < (unsigned)(m.n_stages * kCounterReplicas))
-    __hip_atomic_store(&m.done[threadIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  (void)gemv_body<KIND, B, TPW>(a, blockIdx.x);
 }
 
 // ------------------------------------------------------------------ host side
-
-static std::atomic<int> g_tiles_per_wave{0};   // process-wide
 
 static int round_batch(int batch) { return batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : 8; }
 
 // K-tiles per wave: the fewest that fit the group's K into the workgroup's wave budget
 // (16 waves for batch <= 2, 8 above); 1, 2 or 4.
-static int plan_tpw(int G, int k_t, int batch) {
+static int plan_tpw(int G, int k_t, int batch, const Policy& P) {
   const int max_waves = round_batch(batch) <= 2 ? kMaxWaves : kMaxWaves / 2;
-  const int forced = g_tiles_per_wave.load(std::memory_order_relaxed);
+  const int forced = P.gemv_tpw;
   int tpw = forced > 0 ? forced : (G * k_t + max_waves - 1) / max_waves;
   tpw = tpw <= 1 ? 1 : tpw <= 2 ? 2 : tpw <= 4 ? 4 : 0;
   if (tpw && G * ((k_t + tpw - 1) / tpw) > max_waves) tpw = 0;
@@ -911,15 +711,13 @@ static void launch_b(const GemvArgs& a, int tpw, int blocks, int threads, hipStr
   }
 }
 
-static std::atomic<int> g_ksplit{0};   // 0: automatic; process-wide
-
 // Workgroups per group along K: enough groups x parts to fill the GPU (about 240
 // workgroups) when a launch has few output groups of many tiles (a group of 10 tiles
 // finishes sooner whole than split, the merge costs more than it saves), at least 2
 // K-tiles per part, at most 8.
-static int plan_ksplit(int n_groups, int G, int k_t) {
+static int plan_ksplit(int n_groups, int G, int k_t, const Policy& P) {
   int ks;
-  const int forced_ks = g_ksplit.load(std::memory_order_relaxed);
+  const int forced_ks = P.gemv_ksplit;
   if (forced_ks > 0) {
     ks = forced_ks;
   } else {
@@ -939,20 +737,20 @@ static size_t split_bytes(int n_groups, int G, int ks, int batch) {
 
 // K parts per group: plan_ksplit's choice, raised (up to 8) until one part fits in a
 // workgroup at this batch's wave budget (long K with more than two rows).
-static int plan_ksplit_fit(int n_groups, int G, int k_t, int batch) {
-  int ks = plan_ksplit(n_groups, G, k_t);
-  while (ks < 8 && ks < k_t && plan_tpw(G, (k_t + ks - 1) / ks, batch) == 0) ++ks;
+static int plan_ksplit_fit(int n_groups, int G, int k_t, int batch, const Policy& P) {
+  int ks = plan_ksplit(n_groups, G, k_t, P);
+  while (ks < 8 && ks < k_t && plan_tpw(G, (k_t + ks - 1) / ks, batch, P) == 0) ++ks;
   return ks;
 }
 
-static size_t ws_need(int n_groups, int G, int k_t, int batch) {
-  return split_bytes(n_groups, G, plan_ksplit_fit(n_groups, G, k_t, batch), batch);
+static size_t ws_need(int n_groups, int G, int k_t, int batch, const Policy& P) {
+  return split_bytes(n_groups, G, plan_ksplit_fit(n_groups, G, k_t, batch, P), batch);
 }
 
-static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char* what,
-                  void* ws = nullptr, size_t ws_bytes = 0) {
+static int launch(int kind, GemvArgs& a, int n_groups, const Policy& P, hipStream_t s,
+                  const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
   const int B = round_batch(a.batch);
-  int ks = plan_ksplit_fit(n_groups, a.G, a.k_t, a.batch);
+  int ks = plan_ksplit_fit(n_groups, a.G, a.k_t, a.batch, P);
   const size_t need = split_bytes(n_groups, a.G, ks, a.batch);
   if (ks > 1 && (need == 0 || ws == nullptr || ws_bytes < need || !Q4NX_ALIGNED(ws, 256)))
     ks = 1;   // no (or too small a) workspace: one workgroup per group
@@ -963,7 +761,7 @@ static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char
     a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
   }
   const int kpp = (a.k_t + ks - 1) / ks;   // largest part
-  const int tpw = plan_tpw(a.G, kpp, a.batch);
+  const int tpw = plan_tpw(a.G, kpp, a.batch, P);
   Q4NX_REQUIRE(tpw > 0, Q4NX_ERR_SHAPE, "%s: K=%d is longer than one workgroup covers", what,
                a.k_t * 256);
   const int wm = (kpp + tpw - 1) / tpw;
@@ -985,113 +783,6 @@ static int launch(int kind, GemvArgs& a, int n_groups, hipStream_t s, const char
     }
   }
   return check_launch(what);
-}
-
-// Counter region layout for multi-stage launches (inside the workspace's counter region):
-// split-K arrival counters of each stage from index 0, the stage completion counters and
-// the timeout flag at the end.
-constexpr int kStageDoneIdx = Q4NX_WS_COUNTER_BYTES / 4 - 32;   // kMaxStages x 8 replicas
-constexpr int kStageErrIdx = Q4NX_WS_COUNTER_BYTES / 4 - 33;
-// Waves per workgroup of a multi-stage launch (one K-tile per wave in every stage): 10
-// (640 threads) up to batch 2; the kernel's launch bound is 512 threads above that.
-static int multi_waves(int batch) { return round_batch(batch) <= 2 ? 10 : 8; }
-
-static int multi_ksplit(const GemvArgs& a, int n_groups) {
-  const int per_wg = multi_waves(a.batch) / a.G;   // K-tiles one workgroup covers per member
-  int ks = plan_ksplit(n_groups, a.G, a.k_t);
-  const int need = (a.k_t + per_wg - 1) / per_wg;
-  return ks > need ? ks : need;
-}
-
-static size_t multi_ws_bytes(const GemvArgs* st, const int* n_groups, int n) {
-  size_t part = 0;
-  int cnt = 0;
-  for (int i = 0; i < n; ++i) {
-    const int ks = multi_ksplit(st[i], n_groups[i]);
-    if (ks > 1) {
-      part += (size_t)n_groups[i] * ks * st[i].batch * st[i].G * 32 * 4;
-      cnt += n_groups[i];
-    }
-  }
-  if (cnt > kStageErrIdx) return 0;
-  return (size_t)Q4NX_WS_COUNTER_BYTES + part;
-}
-
-// Launches stages st[0..n) as one kernel (see gemv_multi_kernel). Every stage runs with
-// multi_waves(batch) waves and one K-tile per wave; K is split as far as that needs.
-static int launch_multi(int kind, GemvArgs* st, const int* n_groups, int n, void* ws,
-                        size_t ws_bytes, hipStream_t s, const char* what) {
-  Q4NX_REQUIRE(n >= 1 && n <= kMaxStages, Q4NX_ERR_ARG, "%s: %d stages", what, n);
-  const size_t need = multi_ws_bytes(st, n_groups, n);
-  Q4NX_REQUIRE(need > 0 && ws != nullptr && ws_bytes >= need && Q4NX_ALIGNED(ws, 256),
-               Q4NX_ERR_WS, "%s: workspace of %zu bytes (256-aligned) needed, %zu given", what,
-               need, ws_bytes);
-  MultiGemvArgs m{};
-  unsigned* counters = (unsigned*)ws;
-  uint8_t* part = (uint8_t*)ws + Q4NX_WS_COUNTER_BYTES;
-  int cnt = 0, blocks = 0, batch = st[0].batch;
-  for (int i = 0; i < n; ++i) {
-    GemvArgs& a = st[i];
-    Q4NX_REQUIRE(a.batch == batch, Q4NX_ERR_ARG, "%s: stages differ in batch", what);
-    const int ks = multi_ksplit(a, n_groups[i]);
-    Q4NX_REQUIRE(ks <= 8 && ks <= a.k_t, Q4NX_ERR_SHAPE, "%s: stage %d: K=%d too long", what, i,
-                 a.k_t * 256);
-    a.ksplit = ks;
-    if (ks > 1) {
-      const size_t pb = (size_t)n_groups[i] * ks * a.batch * a.G * 32 * 4;
-      a.counters = counters + cnt;
-      a.part = (float*)part;
-      a.part_bytes = (uint32_t)pb;
-      cnt += n_groups[i];
-      part += pb;
-    }
-    a.sys_io = 1;
-    a.err = counters + kStageErrIdx;
-    if (i > 0) {
-      a.wait_cnt = counters + kStageDoneIdx + (i - 1) * kCounterReplicas;
-      a.wait_target = (unsigned)n_groups[i - 1];
-    }
-    m.st[i] = a;
-    m.wg_begin[i] = blocks;
-    m.items[i] = (unsigned)n_groups[i];
-    blocks += n_groups[i] * ks;
-  }
-  m.wg_begin[n] = blocks;
-  m.n_stages = n;
-  m.done = counters + kStageDoneIdx;
-  const dim3 grid(blocks), block(multi_waves(batch) * 64);
-  const int B = round_batch(batch);
-  if (kind == 4) {
-    switch (B) {
-      case 1: hipLaunchKernelGGL((gemv_multi_kernel<4, 1, 1>), grid, block, 0, s, m); break;
-      case 2: hipLaunchKernelGGL((gemv_multi_kernel<4, 2, 1>), grid, block, 0, s, m); break;
-      case 4: hipLaunchKernelGGL((gemv_multi_kernel<4, 4, 1>), grid, block, 0, s, m); break;
-      default: hipLaunchKernelGGL((gemv_multi_kernel<4, 8, 1>), grid, block, 0, s, m); break;
-    }
-  } else {
-    return Q4NX_ERR_ARG;
-  }
-  return check_launch(what);
-}
-
-// The three GEMV stages after attention: o-proj (+ residual, sums of squares), the
-// RMSNorm + [gate, up, SwiGLU] group, and down (+ residual, sums of squares).
-static void tail_stages(GemvArgs* st, int* ng, const uint8_t* wo, const uint8_t* wg,
-                        const uint8_t* wu, const uint8_t* wd, int hidden, int q_dim, int inter,
-                        const uint16_t* attn, float* h, float* ssq, const uint16_t* norm_w,
-                        float eps, uint16_t* mlp, int batch) {
-  GemvArgs o{}, gu{}, dn{};
-  o.w[0] = wo; o.n_tr[0] = hidden / 32; o.op = OP_PLAIN; o.G = 1; o.k_t = q_dim / 256;
-  o.batch = batch; o.x = attn; o.x_stride = q_dim; o.y = h; o.y_stride = hidden;
-  o.residual = h; o.ssq_out = ssq;
-  gu.w[0] = wg; gu.w[1] = wu; gu.n_tr[0] = gu.n_tr[1] = inter / 32; gu.op = OP_GATEUP;
-  gu.G = 2; gu.k_t = hidden / 256; gu.batch = batch; gu.hres = h; gu.x_stride = hidden;
-  gu.norm_w = norm_w; gu.eps = eps; gu.ssq_in = ssq; gu.h_out = mlp; gu.h_stride = inter;
-  dn.w[0] = wd; dn.n_tr[0] = hidden / 32; dn.op = OP_PLAIN; dn.G = 1; dn.k_t = inter / 256;
-  dn.batch = batch; dn.x = mlp; dn.x_stride = inter; dn.y = h; dn.y_stride = hidden;
-  dn.residual = h; dn.ssq_out = ssq;
-  st[0] = o; st[1] = gu; st[2] = dn;
-  ng[0] = hidden / 32; ng[1] = inter / 32; ng[2] = hidden / 32;
 }
 
 static int check_common(const void* w, int n_tile_rows, int k_tiles, int batch, const char* what,
@@ -1125,13 +816,21 @@ static int check_ssq_in(const float* ssq_in, const uint16_t* norm_w, int k_tiles
   return Q4NX_OK;
 }
 
-// Whether a launch of `batch` rows goes to the matrix-core kernels (gemm.hip): the policy
-// of q4nx_set_mfma_rows, and only for what they implement (an RMSNorm prologue there takes
+// Whether a one-row q4 call of G member tile-rows runs on the row-block kernels (gemv1.hip):
+// the policy's choice, for the K they cover, with the producer's sums of squares for a norm.
+static bool take_rowblock(int kind, int batch, int G, int k_tiles, const uint16_t* norm_w,
+                          const float* ssq_in, const Policy& P) {
+  return P.rowblock && kind == Q4NX_KIND_Q4 && batch == 1 &&
+         gemv1_fits(G, k_tiles, norm_w != nullptr) && (norm_w == nullptr || ssq_in != nullptr);
+}
+
+// Whether a launch of `batch` rows goes to the matrix-core kernels (gemm.hip): the policy's
+// mfma_rows, and only for what they implement (an RMSNorm prologue there takes
 // the producer's sums of squares, and room for the normalised rows in xn_out or the
 // workspace).
 static bool take_mfma(int kind, int batch, int k_tiles, const uint16_t* norm_w,
-                      const float* ssq_in, const void* xn_out, size_t ws_bytes) {
-  if (!mfma_use(kind, batch)) return false;
+                      const float* ssq_in, const void* xn_out, size_t ws_bytes, const Policy& P) {
+  if (!mfma_use(kind, batch, P)) return false;
   if (norm_w == nullptr) return true;
   return ssq_in != nullptr && (xn_out != nullptr || mfma_norm_fits(k_tiles, batch, ws_bytes));
 }
@@ -1140,8 +839,10 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
                       float eps, const float* ssq_in, float* y, int n_tile_rows, int k_tiles,
                       int batch, int64_t x_stride, int64_t y_stride, const float* residual,
                       float* ssq_out, unsigned long long* argmax_keys, void* stream,
-                      const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
-  const bool mf = take_mfma(kind, batch, k_tiles, norm_w, ssq_in, nullptr, ws ? ws_bytes : 0);
+                      const char* what, void* ws, size_t ws_bytes, const q4nx_policy* policy) {
+  Policy P;
+  if (int rc = resolve_policy(policy, &P, what)) return rc;
+  const bool mf = take_mfma(kind, batch, k_tiles, norm_w, ssq_in, nullptr, ws ? ws_bytes : 0, P);
   int rc = check_common(w, n_tile_rows, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
   if (rc) return rc;
   rc = check_x(x, x_stride, k_tiles, what);
@@ -1180,7 +881,27 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
     g.residual = residual;
     g.ssq_out = ssq_out;
     g.argmax_keys = argmax_keys;
-    return mfma_launch(kind, GOP_PLAIN, g, n_tile_rows, ws, ws_bytes, (hipStream_t)stream, what);
+    return mfma_launch(kind, GOP_PLAIN, g, n_tile_rows, ws, ws_bytes, P, (hipStream_t)stream,
+                       what);
+  }
+  if (take_rowblock(kind, batch, 1, k_tiles, norm_w, ssq_in, P)) {
+    Gemv1Args g{};
+    g.w0 = w;
+    g.k_t = k_tiles;
+    g.n_groups = n_tile_rows;
+    if (norm_w) {
+      g.hres = (const float*)x;
+      g.norm_w = norm_w;
+      g.eps = eps;
+      g.ssq_in = ssq_in;
+    } else {
+      g.x = (const uint16_t*)x;
+    }
+    g.y = y;
+    g.residual = residual;
+    g.ssq_out = ssq_out;
+    g.keys = argmax_keys;
+    return gemv1_launch(G1_PLAIN, g, (hipStream_t)stream, what);
   }
   GemvArgs a{};
   a.w[0] = w;
@@ -1203,7 +924,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
   a.residual = residual;
   a.ssq_out = ssq_out;
   a.argmax_keys = argmax_keys;
-  return launch(kind, a, n_tile_rows, (hipStream_t)stream, what, ws, ws_bytes);
+  return launch(kind, a, n_tile_rows, P, (hipStream_t)stream, what, ws, ws_bytes);
 }
 
 }  // namespace q4nx
@@ -1212,53 +933,45 @@ using namespace q4nx;
 
 extern "C" {
 
-int q4nx_set_gemv_ksplit(int parts) {
-  Q4NX_REQUIRE(parts >= 0 && parts <= 8, Q4NX_ERR_ARG,
-               "K parts per group must be 0 (automatic) or 1..8, got %d", parts);
-  g_ksplit = parts;
-  return Q4NX_OK;
-}
-
-int q4nx_set_split_tiles(int tiles) {
-  Q4NX_REQUIRE(tiles == 0 || tiles == 1 || tiles == 2 || tiles == 4, Q4NX_ERR_ARG,
-               "tiles per wave must be 0 (automatic), 1, 2 or 4, got %d", tiles);
-  g_tiles_per_wave = tiles;
-  return Q4NX_OK;
-}
-
-// Workspace of a split-K launch (0 when the launch has enough groups to fill the GPU).
-// Without it the launches still run, one workgroup per group.
-size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch) {
-  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1) return 0;
+// Workspace of a split-K launch (0 when the launch has enough groups to fill the GPU, or runs
+// on the row-block kernels). Without it the launches still run, one workgroup per group.
+size_t q4nx_gemv_ws_bytes(int kind, int n_tile_rows, int k_tiles, int batch,
+                          const q4nx_policy* policy) {
+  Policy P;
+  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1 || !resolve_policy_quiet(policy, &P)) return 0;
   // either kernel may take the launch (the VALU one when the matrix-core one cannot)
-  const size_t v = batch <= Q4NX_MAX_BATCH ? ws_need(n_tile_rows, 1, k_tiles, batch) : 0;
-  const size_t m = mfma_use(kind, batch) ? mfma_ws_bytes(kind, GOP_PLAIN, n_tile_rows, k_tiles, batch) : 0;
+  const bool rowblock = take_rowblock(kind, batch, 1, k_tiles, nullptr, nullptr, P);
+  const size_t v = batch <= Q4NX_MAX_BATCH && !rowblock ? ws_need(n_tile_rows, 1, k_tiles, batch, P) : 0;
+  const size_t m = mfma_use(kind, batch, P) ? mfma_ws_bytes(kind, GOP_PLAIN, n_tile_rows, k_tiles, batch, P) : 0;
   return v > m ? v : m;
 }
 
 int q4nx_gemv_q4(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
-                 size_t ws_bytes, void* stream) {
+                 size_t ws_bytes, const q4nx_policy* policy, void* stream) {
   return gemv_plain(4, w, x, nullptr, 0.f, nullptr, y, n_tile_rows, k_tiles, batch, x_stride,
-                    y_stride, residual, nullptr, nullptr, stream, "q4nx_gemv_q4", ws, ws_bytes);
+                    y_stride, residual, nullptr, nullptr, stream, "q4nx_gemv_q4", ws, ws_bytes,
+                    policy);
 }
 
 int q4nx_gemv_q8(const uint8_t* w, const uint16_t* x, float* y, int n_tile_rows, int k_tiles,
                  int batch, int64_t x_stride, int64_t y_stride, const float* residual, void* ws,
-                 size_t ws_bytes, void* stream) {
+                 size_t ws_bytes, const q4nx_policy* policy, void* stream) {
   return gemv_plain(8, w, x, nullptr, 0.f, nullptr, y, n_tile_rows, k_tiles, batch, x_stride,
-                    y_stride, residual, nullptr, nullptr, stream, "q4nx_gemv_q8", ws, ws_bytes);
+                    y_stride, residual, nullptr, nullptr, stream, "q4nx_gemv_q8", ws, ws_bytes,
+                    policy);
 }
 
 int q4nx_gemv_ex(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const void* x,
                  int64_t x_stride, const uint16_t* norm_w, float eps, const float* ssq_in,
                  int batch, float* y, int64_t y_stride, const float* residual, float* ssq_out,
-                 uint64_t* argmax_keys, void* ws, size_t ws_bytes, void* stream) {
+                 uint64_t* argmax_keys, void* ws, size_t ws_bytes, const q4nx_policy* policy,
+                 void* stream) {
   Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8, Q4NX_ERR_ARG,
                "q4nx_gemv_ex: kind must be Q4NX_KIND_Q4 or Q4NX_KIND_Q8, got %d", kind);
   return gemv_plain(kind, w, x, norm_w, eps, ssq_in, y, n_tile_rows, k_tiles, batch, x_stride,
                     y_stride, residual, ssq_out, (unsigned long long*)argmax_keys, stream,
-                    "q4nx_gemv_ex", ws, ws_bytes);
+                    "q4nx_gemv_ex", ws, ws_bytes, policy);
 }
 
 int q4nx_gemv_attn_q4(const uint8_t* w, int n_tile_rows, const float* att_rec, int n_split,
@@ -1271,7 +984,7 @@ int q4nx_gemv_attn_q4(const uint8_t* w, int n_tile_rows, const float* att_rec, i
                what, n_q_heads, n_kv_heads);
   const int k_tiles = n_q_heads / 4;   // K = 64 per head
   Q4NX_REQUIRE(k_tiles <= kAttnRecMaxKTiles, Q4NX_ERR_SHAPE,
-               "%s: %d query heads, at most %d (the merged row stays in one workgroup)", what,
+               "%s: %d query heads, at most %d (a wave per four heads, one workgroup)", what,
                n_q_heads, 4 * kAttnRecMaxKTiles);
   int rc = check_common(w, n_tile_rows, k_tiles, 1, what);
   if (rc) return rc;
@@ -1283,44 +996,31 @@ int q4nx_gemv_attn_q4(const uint8_t* w, int n_tile_rows, const float* att_rec, i
                "%s: y must be a 4-byte aligned device pointer", what);
   Q4NX_REQUIRE(ssq_out == nullptr || Q4NX_ALIGNED(ssq_out, 4), Q4NX_ERR_ARG,
                "%s: ssq_out must be 4-byte aligned", what);
-  GemvArgs a{};
-  a.w[0] = w;
-  a.n_tr[0] = n_tile_rows;
-  a.op = OP_PLAIN;
-  a.G = 1;
-  a.k_t = k_tiles;
-  a.batch = 1;
-  a.x = (const uint16_t*)att_rec;   // not read: the row is merged from the records
-  a.x_stride = k_tiles * kTileK;
-  a.y = y;
-  a.y_stride = n_tile_rows * 32;
-  a.residual = residual;
-  a.ssq_out = ssq_out;
-  a.ksplit = 1;
-  a.att_rec = att_rec;
-  a.att_split = n_split;
-  a.att_g = n_q_heads / n_kv_heads;
-  const dim3 grid(n_tile_rows), block(64 * k_tiles);
-  hipStream_t st = (hipStream_t)stream;
-  switch ((n_split + 1) / 2) {   // record loads for the next even count of splits
-    case 1: hipLaunchKernelGGL(gemv_attn_kernel<2>, grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(gemv_attn_kernel<4>, grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL(gemv_attn_kernel<6>, grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL(gemv_attn_kernel<8>, grid, block, 0, st, a); break;
-    case 5: hipLaunchKernelGGL(gemv_attn_kernel<10>, grid, block, 0, st, a); break;
-    case 6: hipLaunchKernelGGL(gemv_attn_kernel<12>, grid, block, 0, st, a); break;
-    case 7: hipLaunchKernelGGL(gemv_attn_kernel<14>, grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL(gemv_attn_kernel<16>, grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL(gemv_attn_kernel<18>, grid, block, 0, st, a); break;
-  }
-  return check_launch(what);
+  Gemv1Args g{};
+  g.w0 = w;
+  g.k_t = k_tiles;
+  g.n_groups = n_tile_rows;
+  g.att_rec = att_rec;
+  g.att_split = n_split;
+  g.att_g = n_q_heads / n_kv_heads;
+  g.y = y;
+  g.residual = residual;
+  g.ssq_out = ssq_out;
+  return gemv1_attn_launch(g, (hipStream_t)stream, what);
 }
 
-size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch) {
-  if (n_q_heads < 1 || n_kv_heads < 1 || k_tiles < 1 || batch < 1) return 0;
+size_t q4nx_qkv_rope_ws_bytes(int n_q_heads, int n_kv_heads, int k_tiles, int batch,
+                              const q4nx_policy* policy) {
+  Policy P;
+  if (n_q_heads < 1 || n_kv_heads < 1 || k_tiles < 1 || batch < 1 ||
+      !resolve_policy_quiet(policy, &P))
+    return 0;
   const int g = n_q_heads + 2 * n_kv_heads;
-  const size_t v = batch <= Q4NX_MAX_BATCH ? ws_need(g, 2, k_tiles, batch) : 0;
-  const size_t m = mfma_use(Q4NX_KIND_Q4, batch) ? mfma_ws_bytes(Q4NX_KIND_Q4, GOP_QKV, g, k_tiles, batch) : 0;
+  // a call with a norm prologue needs ssq_in on the row-block kernels: size for the general
+  // kernel too unless the shape fits them either way
+  const bool rowblock = take_rowblock(Q4NX_KIND_Q4, batch, 2, k_tiles, nullptr, nullptr, P);
+  const size_t v = batch <= Q4NX_MAX_BATCH && !rowblock ? ws_need(g, 2, k_tiles, batch, P) : 0;
+  const size_t m = mfma_use(Q4NX_KIND_Q4, batch, P) ? mfma_ws_bytes(Q4NX_KIND_Q4, GOP_QKV, g, k_tiles, batch, P) : 0;
   return v > m ? v : m;
 }
 
@@ -1330,9 +1030,12 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
                   const int32_t* positions,
                   const float* rope_tab, int max_pos, uint16_t* q_out, uint16_t* k_cache,
                   uint16_t* v_cache, int64_t kv_b_stride, int64_t kv_h_stride, float* raw_out,
-                  uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
+                  uint16_t* xn_out, void* ws, size_t ws_bytes, const q4nx_policy* policy,
+                  void* stream) {
   const char* what = "q4nx_qkv_rope";
-  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, k_tiles, norm_w, ssq_in, xn_out, ws ? ws_bytes : 0);
+  Policy P;
+  if (int rc = resolve_policy(policy, &P, what)) return rc;
+  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, k_tiles, norm_w, ssq_in, xn_out, ws ? ws_bytes : 0, P);
   for (const void* p : {(const void*)wq, (const void*)wk, (const void*)wv}) {
     int rc = check_common(p, 2, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
     if (rc) return rc;
@@ -1386,8 +1089,38 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
     g.n_q_heads = n_q_heads;
     g.n_kv_heads = n_kv_heads;
     g.raw_out = raw_out;
-    return mfma_launch(Q4NX_KIND_Q4, GOP_QKV, g, n_q_heads + 2 * n_kv_heads, ws, ws_bytes,
+    return mfma_launch(Q4NX_KIND_Q4, GOP_QKV, g, n_q_heads + 2 * n_kv_heads, ws, ws_bytes, P,
                        (hipStream_t)stream, what);
+  }
+  if (take_rowblock(Q4NX_KIND_Q4, batch, 2, k_tiles, norm_w, ssq_in, P)) {
+    Gemv1Args g{};
+    g.w0 = wq;
+    g.w1 = wk;
+    g.w2 = wv;
+    g.k_t = k_tiles;
+    g.n_groups = n_q_heads + 2 * n_kv_heads;
+    g.grp_q = n_q_heads;
+    g.grp_k = n_kv_heads;
+    if (norm_w) {
+      g.hres = (const float*)x;
+      g.norm_w = norm_w;
+      g.eps = eps;
+      g.ssq_in = ssq_in;
+      g.xn_out = xn_out;
+    } else {
+      g.x = (const uint16_t*)x;
+    }
+    g.q_out = q_out;
+    g.k_cache = k_cache;
+    g.v_cache = v_cache;
+    g.kv_h_stride = kv_h_stride;
+    g.pos = positions;
+    g.rope_tab = rope_tab;
+    g.max_pos = max_pos;
+    g.n_q_heads = n_q_heads;
+    g.n_kv_heads = n_kv_heads;
+    g.raw_out = raw_out;
+    return gemv1_launch(G1_QKV, g, (hipStream_t)stream, what);
   }
   GemvArgs a{};
   a.w[0] = wq;
@@ -1423,22 +1156,27 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
   a.n_q_heads = n_q_heads;
   a.n_kv_heads = n_kv_heads;
   a.raw_out = raw_out;
-  return launch(4, a, n_q_heads + 2 * n_kv_heads, (hipStream_t)stream, what, ws, ws_bytes);
+  return launch(4, a, n_q_heads + 2 * n_kv_heads, P, (hipStream_t)stream, what, ws, ws_bytes);
 }
 
-size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch) {
-  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1) return 0;
-  const size_t v = batch <= Q4NX_MAX_BATCH ? ws_need(n_tile_rows, 2, k_tiles, batch) : 0;
-  const size_t m = mfma_use(Q4NX_KIND_Q4, batch) ? mfma_ws_bytes(Q4NX_KIND_Q4, GOP_GATEUP, n_tile_rows, k_tiles, batch) : 0;
+size_t q4nx_gate_up_ws_bytes(int n_tile_rows, int k_tiles, int batch, const q4nx_policy* policy) {
+  Policy P;
+  if (n_tile_rows < 1 || k_tiles < 1 || batch < 1 || !resolve_policy_quiet(policy, &P)) return 0;
+  const bool rowblock = take_rowblock(Q4NX_KIND_Q4, batch, 2, k_tiles, nullptr, nullptr, P);
+  const size_t v = batch <= Q4NX_MAX_BATCH && !rowblock ? ws_need(n_tile_rows, 2, k_tiles, batch, P) : 0;
+  const size_t m = mfma_use(Q4NX_KIND_Q4, batch, P) ? mfma_ws_bytes(Q4NX_KIND_Q4, GOP_GATEUP, n_tile_rows, k_tiles, batch, P) : 0;
   return v > m ? v : m;
 }
 
 int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, int k_tiles,
                         const void* x, int64_t x_stride, const uint16_t* norm_w, float eps,
-                        const float* ssq_in, int batch, uint16_t* h_out, int64_t h_stride, float* raw_out,
-                        uint16_t* xn_out, void* ws, size_t ws_bytes, void* stream) {
+                        const float* ssq_in, int batch, uint16_t* h_out, int64_t h_stride,
+                        float* raw_out, uint16_t* xn_out, void* ws, size_t ws_bytes,
+                        const q4nx_policy* policy, void* stream) {
   const char* what = "q4nx_gate_up_swiglu";
-  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, k_tiles, norm_w, ssq_in, xn_out, ws ? ws_bytes : 0);
+  Policy P;
+  if (int rc = resolve_policy(policy, &P, what)) return rc;
+  const bool mf = take_mfma(Q4NX_KIND_Q4, batch, k_tiles, norm_w, ssq_in, xn_out, ws ? ws_bytes : 0, P);
   for (const void* p : {(const void*)wg, (const void*)wu}) {
     int rc = check_common(p, n_tile_rows, k_tiles, batch, what, mf ? INT_MAX : Q4NX_MAX_BATCH);
     if (rc) return rc;
@@ -1474,8 +1212,27 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
     g.h_out = h_out;
     g.h_stride = h_stride;
     g.raw_out = raw_out;
-    return mfma_launch(Q4NX_KIND_Q4, GOP_GATEUP, g, n_tile_rows, ws, ws_bytes,
+    return mfma_launch(Q4NX_KIND_Q4, GOP_GATEUP, g, n_tile_rows, ws, ws_bytes, P,
                        (hipStream_t)stream, what);
+  }
+  if (take_rowblock(Q4NX_KIND_Q4, batch, 2, k_tiles, norm_w, ssq_in, P)) {
+    Gemv1Args g{};
+    g.w0 = wg;
+    g.w1 = wu;
+    g.k_t = k_tiles;
+    g.n_groups = n_tile_rows;
+    if (norm_w) {
+      g.hres = (const float*)x;
+      g.norm_w = norm_w;
+      g.eps = eps;
+      g.ssq_in = ssq_in;
+      g.xn_out = xn_out;
+    } else {
+      g.x = (const uint16_t*)x;
+    }
+    g.h_out = h_out;
+    g.raw_out = raw_out;
+    return gemv1_launch(G1_GATEUP, g, (hipStream_t)stream, what);
   }
   GemvArgs a{};
   a.w[0] = wg;
@@ -1499,59 +1256,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
   a.h_out = h_out;
   a.h_stride = h_stride;
   a.raw_out = raw_out;
-  return launch(4, a, n_tile_rows, (hipStream_t)stream, what, ws, ws_bytes);
-}
-
-size_t q4nx_layer_tail_ws_bytes(int hidden, int q_dim, int inter, int batch) {
-  if (hidden < 256 || q_dim < 256 || inter < 256 || batch < 1 || batch > Q4NX_MAX_BATCH) return 0;
-  GemvArgs st[3];
-  int ng[3];
-  tail_stages(st, ng, nullptr, nullptr, nullptr, nullptr, hidden, q_dim, inter, nullptr, nullptr,
-              nullptr, nullptr, 0.f, nullptr, batch);
-  return multi_ws_bytes(st, ng, 3);
-}
-
-int q4nx_layer_tail(const uint8_t* wo, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
-                    int hidden, int q_dim, int inter, const uint16_t* attn, float* h, float* ssq,
-                    const uint16_t* norm_w, float eps, uint16_t* mlp, int batch, void* ws,
-                    size_t ws_bytes, void* stream) {
-  const char* what = "q4nx_layer_tail";
-  Q4NX_REQUIRE(hidden % 256 == 0 && q_dim % 256 == 0 && inter % 256 == 0 && hidden > 0 &&
-                   q_dim > 0 && inter > 0 && hidden <= 8192,
-               Q4NX_ERR_SHAPE, "%s: hidden=%d q_dim=%d inter=%d must be multiples of 256 "
-               "(hidden <= 8192)", what, hidden, q_dim, inter);
-  int rc = check_common(wo, hidden / 32, q_dim / 256, batch, what);
-  if (rc) return rc;
-  for (const void* p : {(const void*)wg, (const void*)wu})
-    if ((rc = check_common(p, inter / 32, hidden / 256, batch, what))) return rc;
-  if ((rc = check_common(wd, hidden / 32, inter / 256, batch, what))) return rc;
-  Q4NX_REQUIRE(attn && h && ssq && norm_w && mlp && Q4NX_ALIGNED(attn, 16) &&
-                   Q4NX_ALIGNED(h, 16) && Q4NX_ALIGNED(mlp, 16) && Q4NX_ALIGNED(norm_w, 16) &&
-                   Q4NX_ALIGNED(ssq, 4),
-               Q4NX_ERR_ARG, "%s: attn, h, ssq, norm_w and mlp are required (16-byte aligned)",
-               what);
-  GemvArgs st[3];
-  int ng[3];
-  tail_stages(st, ng, wo, wg, wu, wd, hidden, q_dim, inter, attn, h, ssq, norm_w, eps, mlp, batch);
-  return launch_multi(4, st, ng, 3, ws, ws_bytes, (hipStream_t)stream, what);
-}
-
-int q4nx_ws_check(void* ws, void* stream) {
-  Q4NX_REQUIRE(ws != nullptr, Q4NX_ERR_ARG, "q4nx_ws_check: ws is required");
-  unsigned flag = 0;
-  unsigned* dev = (unsigned*)ws + kStageErrIdx;
-  hipStream_t s = (hipStream_t)stream;
-  if (hipMemcpyAsync(&flag, dev, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
-      hipStreamSynchronize(s) != hipSuccess) {
-    set_error("q4nx_ws_check: reading the flag failed");
-    return Q4NX_ERR_LAUNCH;
-  }
-  if (flag == 0) return Q4NX_OK;
-  // a stage gave up: counters may be left mid-count, so the whole region starts over
-  (void)hipMemsetAsync(ws, 0, Q4NX_WS_COUNTER_BYTES, s);
-  (void)hipStreamSynchronize(s);
-  set_error("a multi-stage launch timed out waiting for an earlier stage (results invalid)");
-  return Q4NX_ERR_TIMEOUT;
+  return launch(4, a, n_tile_rows, P, (hipStream_t)stream, what, ws, ws_bytes);
 }
 
 }  // extern "C"

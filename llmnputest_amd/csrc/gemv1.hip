@@ -1,0 +1,455 @@
+// Batch-1 q4 GEMV family for gfx950: y = W x for one token, W read in the q4nx tile layout.
+//
+// Replaces, for a single token, the per-core AIE kernels of
+// designs/granite_gemv/granite_gemv.h:109-300 (Q4_1 GEMV) and the fused epilogues of
+// granite_qkv_rope.h:30-71 and granite_swiglu_f32.h:27-51, with the RMSNorm of
+// granite_rmsnorm.h:45-80 as a prologue and attention's split merge
+// (granite_attention.h:193-212) as an alternative prologue of the o-projection.
+//
+// Work decomposition
+//   A q4nx tile stores two 16-row blocks (rb) of 2048 code bytes each. One workgroup owns
+//   one output group (one tile-row for a plain GEMV, the two tile-rows of an attention
+//   head for [q,k,v,RoPE], the same tile-row of gate and up for SwiGLU) and ONE row block
+//   of it: 16 (or 2 x 16) complete output rows, so no two workgroups ever share an output
+//   and nothing is merged across workgroups. The two row blocks of a group go to
+//   workgroups 8 apart, which the dispatcher places on the same XCD, so the tile metadata
+//   both read is fetched into one L2. Each wave owns TPW consecutive K-tiles of one member
+//   tile-row; the waves combine once through LDS, in wave order.
+//
+// Data path
+//   Lane l of a wave reads the 32 contiguous code bytes at rb * 2048 + 32 l of each of its
+//   tiles: 4 K values x 16 rows (K-group l / 8, K offset 4 (l % 8)). Every load of a wave
+//   (activations, codes, scales, the epilogue's inputs) is issued before the first wait,
+//   and nothing is loaded under a branch, so the weight stream starts at once.
+//
+// Arithmetic (exact products, fp32 sums)
+//   x is converted to fp16 with one power-of-two scale per wave (bf16 values are exact in
+//   fp16's range after scaling). A 4-bit code placed in bits 4-7 of an fp16 is the
+//   subnormal c * 2^-20, and v_dot2_f32_f16 multiplies two of them by two x values exactly;
+//   one v_perm_b32 builds [c(k), c(k+1)] for a row. The 16 row sums of a lane are reduced
+//   over the 8 lanes of its K-group (bits 2, 1, 0 of the lane: 14 adds), leaving each lane
+//   two rows of one group, to which that group's scale and minimum are applied:
+//   y_r += d_r * sum(c x) + m_r * sum(x) (the Q4_1 factoring, granite_gemv.h:19-29).
+
+#include "common.h"
+#include "gemv1.h"
+
+namespace q4nx {
+
+__device__ __forceinline__ constexpr uint32_t sel_pair(int i) {
+  return 0x0c040c00u + (uint32_t)i * 0x00010001u;   // [s1.b_i, 0, s0.b_i, 0]
+}
+
+// 64-bit max over aligned groups of 16 lanes (every lane of the group gets it).
+__device__ __forceinline__ unsigned long long key_max16(unsigned long long k) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    const unsigned long long t = __shfl_xor(k, o);
+    k = t > k ? t : k;
+  }
+  return k;
+}
+
+template <int OP, int G, int TPW, int NSS, int XNS>
+__global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
+  constexpr bool NORM = NSS > 0;
+  constexpr bool XREC = XNS > 0;
+  __shared__ float sred[16][16];
+
+  // every argument read before the weight stream, in one round of scalar loads (the empty
+  // asm consumes them all at once, so the compiler cannot spread them over dependent rounds)
+  const uint8_t* const w0 = a.w0;
+  const uint8_t* const w1 = a.w1;
+  const uint8_t* const w2 = a.w2;
+  const void* const xin = XREC ? (const void*)a.att_rec : NORM ? (const void*)a.hres : (const void*)a.x;
+  const uint16_t* const norm_w = a.norm_w;
+  const float* const ssq_in = a.ssq_in;
+  const float* const residual = a.residual;
+  const int32_t* const posp = a.pos;
+  const int k_t = a.k_t, n_groups = a.n_groups, grp_q = a.grp_q, grp_k = a.grp_k;
+  const int att_split = a.att_split, att_g = a.att_g;
+  asm volatile("" ::"s"(w0), "s"(w1), "s"(w2), "s"(xin), "s"(norm_w), "s"(ssq_in), "s"(residual),
+               "s"(posp), "s"(k_t), "s"(n_groups), "s"(grp_q), "s"(grp_k), "s"(att_split),
+               "s"(att_g));
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int WM = (k_t + TPW - 1) / TPW;   // waves per member (the launch gives G * WM)
+  const int member = (G == 2 && wave >= WM) ? 1 : 0, chunk = wave - member * WM;
+  const int bi = blockIdx.x;
+  int group, rb;
+  if ((n_groups & 7) == 0) {
+    group = (bi >> 4) * 8 + (bi & 7);
+    rb = (bi >> 3) & 1;
+  } else {
+    group = bi >> 1;
+    rb = bi & 1;
+  }
+  // member tile-row and its tensor
+  int tr, seg = 0, hg = group;
+  const uint8_t* wseg;
+  if constexpr (OP == G1_PLAIN) {
+    tr = group;
+    wseg = w0;
+  } else if constexpr (OP == G1_GATEUP) {
+    tr = group;
+    wseg = member ? w1 : w0;
+  } else {
+    seg = group < grp_q ? 0 : group < grp_q + grp_k ? 1 : 2;
+    hg = group - (seg == 0 ? 0 : seg == 1 ? grp_q : grp_q + grp_k);
+    tr = 2 * hg + member;
+    wseg = seg == 0 ? w0 : seg == 1 ? w1 : w2;
+  }
+  const int K = k_t * kTileK;
+  const int qq = lane & 7, gk = lane >> 3;
+  const int k0 = gk * 32 + qq * 4;                 // this lane's first K inside a tile
+  const int mi = gk * 32 + rb * 16 + 2 * qq;       // meta index of the lane's two rows
+  const int kt0 = chunk * TPW;
+
+  // ---- 1. every load of the wave
+  uint2 xv[TPW];          // bf16 x[k .. k+3]
+  float4 hv[TPW];         // fp32 h[k .. k+3] (RMSNorm prologue)
+  uint2 nv[TPW];          // bf16 norm_w[k .. k+3]
+  float sq[NORM ? NSS : 1];
+  float4 racc[XREC ? XNS : 1];
+  float2 rml[XREC ? XNS : 1];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int k = min(kt0 + t, k_t - 1) * kTileK + k0;
+    if constexpr (XREC) {
+      // attention records of this lane's head (k / 64) and its four dims (k % 64 ..)
+      const int h = k >> 6, kvh = h / att_g, hh = h - kvh * att_g;
+#pragma unroll
+      for (int i = 0; i < XNS; ++i) {
+        const int s = min(i, att_split - 1);
+        const float* r = (const float*)xin + ((size_t)(kvh * att_split + s) * att_g + hh) * kAttnRecFloats;
+        racc[i] = *(const float4*)(r + (k & 63));
+        rml[i] = *(const float2*)(r + 64);
+      }
+    } else if constexpr (NORM) {
+      hv[t] = *(const float4*)((const float*)xin + k);
+      nv[t] = *(const uint2*)(norm_w + k);
+    } else {
+      xv[t] = *(const uint2*)((const uint16_t*)xin + k);
+    }
+  }
+  if constexpr (NORM) {
+    const int n_ss = K / 16;
+#pragma unroll
+    for (int j = 0; j < NSS; ++j) sq[j] = ssq_in[min(lane + 64 * j, n_ss - 1)];
+  }
+  uint4 wq[TPW][2];
+  uint32_t md[TPW], mm[TPW];
+  {
+    const uint8_t* rowp = wseg + (size_t)tr * k_t * kQ4TileBytes;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const uint8_t* tile = rowp + (size_t)min(kt0 + t, k_t - 1) * kQ4TileBytes;
+      const uint4* src = (const uint4*)(tile + 1024 + rb * 2048 + lane * 32);
+      wq[t][0] = src[0];
+      wq[t][1] = src[1];
+      md[t] = *(const uint32_t*)(tile + 2 * mi);
+      mm[t] = *(const uint32_t*)(tile + kMetaBytes + 2 * mi);
+    }
+  }
+  // the epilogue's own inputs, in flight with the weights (thread r < 16 owns output row r
+  // of each member): the residual (plain), the sequence position (q/k/v)
+  const int er = tid & 15;
+  float ep_res = 0.f;
+  int ep_pos = 0;
+  if constexpr (OP == G1_PLAIN) {
+    const float* rp = residual != nullptr ? residual + (int64_t)tr * 32 + rb * 16 + er
+                                            : (const float*)w0;
+    ep_res = *rp;
+  }
+  if constexpr (OP == G1_QKV) ep_pos = *posp;
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. activations: as given, RMSNorm of h, or merged attention records; bf16 bits
+  uint2 xr[TPW];
+  if constexpr (XREC) {
+    const int ns = a.att_split;
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < XNS; ++i)
+      if (i < ns) M = fmaxf(M, rml[i].x);
+    float L = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < XNS; ++i)
+        if (i < ns) {
+          const float f = __builtin_amdgcn_exp2f(rml[i].x - M);
+          L = fmaf(rml[i].y, f, L);
+          A0 = fmaf(racc[i].x, f, A0);
+          A1 = fmaf(racc[i].y, f, A1);
+          A2 = fmaf(racc[i].z, f, A2);
+          A3 = fmaf(racc[i].w, f, A3);
+        }
+    }
+    const float o0 = L > 0.f ? A0 / L : 0.f, o1 = L > 0.f ? A1 / L : 0.f;
+    const float o2 = L > 0.f ? A2 / L : 0.f, o3 = L > 0.f ? A3 / L : 0.f;
+    xr[0] = make_uint2((uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16),
+                       (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16));
+  } else if constexpr (NORM) {
+    const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / 16)) / (float)K + a.eps);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      xr[t].x = pack_bf16x2((hv[t].x * inv) * bf16lo(nv[t].x), (hv[t].y * inv) * bf16hi(nv[t].x));
+      xr[t].y = pack_bf16x2((hv[t].z * inv) * bf16lo(nv[t].y), (hv[t].w * inv) * bf16hi(nv[t].y));
+      if (a.xn_out != nullptr && group == 0 && rb == 0 && member == 0 && kt0 + t < a.k_t)
+        *(uint2*)(a.xn_out + (kt0 + t) * kTileK + k0) = xr[t];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) xr[t] = xv[t];
+  }
+  // RoPE cos/sin of this thread's output dim, now that the position is here
+  float ep_c = 0.f, ep_s = 0.f;
+  if constexpr (OP == G1_QKV) {
+    const bool ok = ep_pos >= 0 && ep_pos < a.max_pos;
+    const float* tb = ok ? a.rope_tab + (int64_t)ep_pos * 64 + rb * 16 + er : a.rope_tab;
+    ep_c = tb[0];
+    ep_s = tb[32];
+  }
+
+  // ---- 3. fp16 conversion with one power-of-two scale per wave (its live tiles)
+  float xm = 0.f;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+    if (kt0 + t < a.k_t) {
+      xm = fmaxf(xm, fmaxf(fabsf(bf16lo(xr[t].x)), fabsf(bf16hi(xr[t].x))));
+      xm = fmaxf(xm, fmaxf(fabsf(bf16lo(xr[t].y)), fabsf(bf16hi(xr[t].y))));
+    }
+  xm = wave_max(xm);
+  int e = 0;
+  if (xm > 0.f && xm <= 3.0e38f) {
+    (void)frexpf(xm, &e);   // xm < 2^e
+    e -= 15;                // scaled max < 2^15 < fp16 max
+    e = e < -120 ? -120 : e;
+  }
+  const float xs = ldexpf(1.0f, -e);
+  uint32_t xp[TPW][2];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    half2_t h;
+    h.x = (_Float16)(bf16lo(xr[t].x) * xs);
+    h.y = (_Float16)(bf16hi(xr[t].x) * xs);
+    xp[t][0] = h2_bits(h);
+    h.x = (_Float16)(bf16lo(xr[t].y) * xs);
+    h.y = (_Float16)(bf16hi(xr[t].y) * xs);
+    xp[t][1] = h2_bits(h);
+  }
+
+  // ---- 4. tiles
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const bool live = kt0 + t < a.k_t;
+    float pv[16], X = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pv[i] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      // dwords: rows 0-7 at k, rows 8-15 at k, rows 0-7 at k+1, rows 8-15 at k+1; the low
+      // nibble of byte i is row 2i, the high nibble row 2i + 1. Both go to bits 4-7.
+      const uint4 w = wq[t][c];
+      const uint32_t Lx = (w.x << 4) & 0xF0F0F0F0u, Ly = (w.y << 4) & 0xF0F0F0F0u;
+      const uint32_t Lz = (w.z << 4) & 0xF0F0F0F0u, Lw = (w.w << 4) & 0xF0F0F0F0u;
+      const uint32_t Hx = w.x & 0xF0F0F0F0u, Hy = w.y & 0xF0F0F0F0u;
+      const uint32_t Hz = w.z & 0xF0F0F0F0u, Hw = w.w & 0xF0F0F0F0u;
+      const uint32_t xc = xp[t][c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[2 * i] = dot2(perm(Lz, Lx, sel_pair(i)), xc, pv[2 * i]);
+        pv[2 * i + 1] = dot2(perm(Hz, Hx, sel_pair(i)), xc, pv[2 * i + 1]);
+        pv[8 + 2 * i] = dot2(perm(Lw, Ly, sel_pair(i)), xc, pv[8 + 2 * i]);
+        pv[8 + 2 * i + 1] = dot2(perm(Hw, Hy, sel_pair(i)), xc, pv[8 + 2 * i + 1]);
+      }
+      X = dot2(xc, 0x3C003C00u, X);
+    }
+    // 16 rows over the 8 lanes of the K-group: lane bit 2 (half mirror), bit 1, bit 0
+    float t8[8], t4[4], r2[2];
+    const bool u2 = (lane & 4) != 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float keep = u2 ? pv[i + 8] : pv[i], send = u2 ? pv[i] : pv[i + 8];
+      t8[i] = keep + dpp<kDppHalfMirror>(send);
+    }
+    const bool u1 = (lane & 2) != 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float keep = u1 ? t8[i + 4] : t8[i], send = u1 ? t8[i] : t8[i + 4];
+      t4[i] = keep + dpp<kDppXor2>(send);
+    }
+    const bool u0 = (lane & 1) != 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float keep = u0 ? t4[i + 2] : t4[i], send = u0 ? t4[i] : t4[i + 2];
+      r2[i] = keep + dpp<kDppXor1>(send);
+    }
+    X += dpp<kDppHalfMirror>(X);
+    X += dpp<kDppXor2>(X);
+    X += dpp<kDppXor1>(X);
+    constexpr float kC = 1048576.0f;   // undo the 2^-20 of the codes
+    const float c0 = fmaf(bf16lo(md[t]), r2[0] * kC, bf16lo(mm[t]) * X);
+    const float c1 = fmaf(bf16hi(md[t]), r2[1] * kC, bf16hi(mm[t]) * X);
+    acc0 += live ? c0 : 0.f;
+    acc1 += live ? c1 : 0.f;
+  }
+
+  // ---- 5. sum over the 8 K-groups (lane bits 3..5), undo the activation scale
+  {
+    const float sc = ldexpf(1.0f, e);
+    float v0 = acc0, v1 = acc1;
+    v0 += dpp<kDppRor8>(v0);
+    v1 += dpp<kDppRor8>(v1);
+    v0 = xor32_sum(xor16_sum(v0));
+    v1 = xor32_sum(xor16_sum(v1));
+    if (lane < 8) {
+      sred[wave][2 * lane] = v0 * sc;
+      sred[wave][2 * lane + 1] = v1 * sc;
+    }
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+
+  // ---- 6. waves of each member in order; thread r < 16 holds row r of each member
+  float s[G];
+#pragma unroll
+  for (int m = 0; m < G; ++m) {
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) v[c] = sred[min(m * WM + c, 15)][er];
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c < WM) acc += v[c];
+    s[m] = acc;
+  }
+
+  // ---- 7. epilogue
+  if constexpr (OP == G1_PLAIN) {
+    const int64_t n = (int64_t)tr * 32 + rb * 16 + er;
+    float v = s[0];
+    if (a.residual != nullptr) v += ep_res;
+    if (tid < 16 && a.y != nullptr) a.y[n] = v;
+    if (a.ssq_out != nullptr) {   // sum of squares of the block's 16 outputs
+      const float q = group16_sum(tid < 16 ? v * v : 0.f);
+      if (tid == 0) a.ssq_out[(int64_t)tr * 2 + rb] = q;
+    }
+    if (a.keys != nullptr) {      // (max, first row) of the block, order-preserving
+      const unsigned long long kk = key_max16(tid < 16 ? argmax_key(v, (uint32_t)n) : 0ull);
+      if (tid == 0) a.keys[(int64_t)tr * 2 + rb] = kk;
+    }
+  } else if constexpr (OP == G1_GATEUP) {
+    if (tid < 16) {
+      const int64_t n = (int64_t)group * 32 + rb * 16 + er;
+      const float g = bf16_to_f32(f32_to_bf16(s[0]));
+      const float u = bf16_to_f32(f32_to_bf16(s[1]));
+      a.h_out[n] = f32_to_bf16((g / (1.0f + expf(-g))) * u);
+      if (a.raw_out != nullptr) {
+        const int64_t N = (int64_t)a.n_groups * 32;
+        a.raw_out[n] = s[0];
+        a.raw_out[N + n] = s[1];
+      }
+    }
+  } else {   // QKV: dims d and d + 32 of one head, d = rb * 16 + r
+    if (tid < 16) {
+      const int d = rb * 16 + er;
+      const int seg_off = seg == 0 ? 0 : seg == 1 ? a.n_q_heads * 64 : (a.n_q_heads + a.n_kv_heads) * 64;
+      if (a.raw_out != nullptr) {
+        a.raw_out[seg_off + hg * 64 + d] = s[0];
+        a.raw_out[seg_off + hg * 64 + 32 + d] = s[1];
+      }
+      const float x0 = bf16_to_f32(f32_to_bf16(s[0]));
+      const float x1 = bf16_to_f32(f32_to_bf16(s[1]));
+      const int p = ep_pos;
+      if (p >= 0 && p < a.max_pos) {
+        if (seg == 2) {
+          uint16_t* dst = a.v_cache + hg * a.kv_h_stride + (int64_t)p * 64;
+          dst[d] = f32_to_bf16(x0);
+          dst[32 + d] = f32_to_bf16(x1);
+        } else {
+          const float y0 = fmaf(x0, ep_c, -(x1 * ep_s));
+          const float y1 = fmaf(x1, ep_c, x0 * ep_s);
+          uint16_t* dst = seg == 0 ? a.q_out + hg * 64
+                                   : a.k_cache + hg * a.kv_h_stride + (int64_t)p * 64;
+          dst[d] = f32_to_bf16(y0);
+          dst[32 + d] = f32_to_bf16(y1);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+// K-tiles per wave: the fewest (1, 2 or 4) that fit the group's K into 16 waves; 0 if none.
+int gemv1_tpw(int G, int k_t) {
+  for (int tpw = 1; tpw <= 4; tpw *= 2)
+    if (G * ((k_t + tpw - 1) / tpw) <= 16) return tpw;
+  return 0;
+}
+
+bool gemv1_fits(int G, int k_t, bool norm) {
+  if (k_t < 1 || gemv1_tpw(G, k_t) == 0) return false;
+  return !norm || k_t * kTileK / 16 <= 512;
+}
+
+template <int OP, int G, int TPW, int NSS, int XNS>
+static void go(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
+  hipLaunchKernelGGL((gemv1_kernel<OP, G, TPW, NSS, XNS>), dim3(blocks), dim3(threads), 0, s, a);
+}
+
+template <int OP, int G, int TPW>
+static void go_norm(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
+  if (a.norm_w == nullptr) go<OP, G, TPW, 0, 0>(a, blocks, threads, s);
+  else if (a.k_t * kTileK / 16 <= 256) go<OP, G, TPW, 4, 0>(a, blocks, threads, s);
+  else go<OP, G, TPW, 8, 0>(a, blocks, threads, s);
+}
+
+template <int OP, int G>
+static void go_tpw(const Gemv1Args& a, int tpw, int blocks, int threads, hipStream_t s) {
+  switch (tpw) {
+    case 1: go_norm<OP, G, 1>(a, blocks, threads, s); break;
+    case 2: go_norm<OP, G, 2>(a, blocks, threads, s); break;
+    default: go_norm<OP, G, 4>(a, blocks, threads, s); break;
+  }
+}
+
+int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what) {
+  const int G = op == G1_PLAIN ? 1 : 2;
+  const int tpw = gemv1_tpw(G, a.k_t);
+  Q4NX_REQUIRE(tpw > 0, Q4NX_ERR_SHAPE, "%s: K=%d is longer than one workgroup covers", what,
+               a.k_t * kTileK);
+  const int threads = G * ((a.k_t + tpw - 1) / tpw) * 64;
+  const int blocks = 2 * a.n_groups;
+  if (op == G1_PLAIN) go_tpw<G1_PLAIN, 1>(a, tpw, blocks, threads, s);
+  else if (op == G1_GATEUP) go_tpw<G1_GATEUP, 2>(a, tpw, blocks, threads, s);
+  else go_tpw<G1_QKV, 2>(a, tpw, blocks, threads, s);
+  return check_launch(what);
+}
+
+// The o-projection from attention records: one K-tile (four heads) per wave.
+int gemv1_attn_launch(const Gemv1Args& a, hipStream_t s, const char* what) {
+  Q4NX_REQUIRE(a.k_t >= 1 && a.k_t <= kAttnRecMaxKTiles, Q4NX_ERR_SHAPE,
+               "%s: %d K-tiles (at most %d)", what, a.k_t, kAttnRecMaxKTiles);
+  Q4NX_REQUIRE(a.att_split >= 1 && a.att_split <= kAttnRecMaxSplits, Q4NX_ERR_SHAPE,
+               "%s: %d splits (1..%d)", what, a.att_split, kAttnRecMaxSplits);
+  const int blocks = 2 * a.n_groups, threads = a.k_t * 64;
+  switch ((a.att_split + 1) / 2) {
+    case 1: go<G1_PLAIN, 1, 1, 0, 2>(a, blocks, threads, s); break;
+    case 2: go<G1_PLAIN, 1, 1, 0, 4>(a, blocks, threads, s); break;
+    case 3: go<G1_PLAIN, 1, 1, 0, 6>(a, blocks, threads, s); break;
+    case 4: go<G1_PLAIN, 1, 1, 0, 8>(a, blocks, threads, s); break;
+    case 5: go<G1_PLAIN, 1, 1, 0, 10>(a, blocks, threads, s); break;
+    case 6: go<G1_PLAIN, 1, 1, 0, 12>(a, blocks, threads, s); break;
+    case 7: go<G1_PLAIN, 1, 1, 0, 14>(a, blocks, threads, s); break;
+    case 8: go<G1_PLAIN, 1, 1, 0, 16>(a, blocks, threads, s); break;
+    default: go<G1_PLAIN, 1, 1, 0, 18>(a, blocks, threads, s); break;
+  }
+  return check_launch(what);
+}
+
+}  // namespace q4nx

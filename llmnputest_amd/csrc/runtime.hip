@@ -4,6 +4,7 @@
 #include <stdio.h>
 
 #include "common.h"
+#include "policy.h"
 
 namespace q4nx {
 
@@ -25,9 +26,64 @@ int check_launch(const char* what) {
   return Q4NX_OK;
 }
 
+static void policy_defaults(q4nx_policy* p) {
+  p->mfma_rows_q4 = 2;   // one q4 row is faster on the row-block kernels, two and more on MFMA
+  p->mfma_rows_q8 = 1;   // a q8 row is faster on the matrix cores (lm_head 100352 x 2560)
+  p->rowblock = 1;
+  p->gemv_ksplit = 0;
+  p->gemv_tiles_per_wave = 0;
+  p->gemm_ksplit = 0;
+  p->attn_mfma = 1;
+}
+
+static const char* policy_problem(const q4nx_policy* p) {
+  if (p->mfma_rows_q4 < 0 || p->mfma_rows_q8 < 0) return "mfma_rows must be >= 0";
+  if (p->rowblock != 0 && p->rowblock != 1) return "rowblock must be 0 or 1";
+  if (p->gemv_ksplit < 0 || p->gemv_ksplit > 8) return "gemv_ksplit must be 0..8";
+  if (p->gemv_tiles_per_wave != 0 && p->gemv_tiles_per_wave != 1 &&
+      p->gemv_tiles_per_wave != 2 && p->gemv_tiles_per_wave != 4)
+    return "gemv_tiles_per_wave must be 0, 1, 2 or 4";
+  if (p->gemm_ksplit < 0 || p->gemm_ksplit > 8) return "gemm_ksplit must be 0..8";
+  if (p->attn_mfma != 0 && p->attn_mfma != 1) return "attn_mfma must be 0 or 1";
+  return nullptr;
+}
+
+static void policy_copy(const q4nx_policy& p, Policy* out) {
+  out->mfma_rows[0] = p.mfma_rows_q4;
+  out->mfma_rows[1] = p.mfma_rows_q8;
+  out->rowblock = p.rowblock;
+  out->gemv_ksplit = p.gemv_ksplit;
+  out->gemv_tpw = p.gemv_tiles_per_wave;
+  out->gemm_ksplit = p.gemm_ksplit;
+  out->attn_mfma = p.attn_mfma;
+}
+
+bool resolve_policy_quiet(const q4nx_policy* p, Policy* out) {
+  q4nx_policy d;
+  policy_defaults(&d);
+  if (p == nullptr) p = &d;
+  if (policy_problem(p) != nullptr) return false;
+  policy_copy(*p, out);
+  return true;
+}
+
+int resolve_policy(const q4nx_policy* p, Policy* out, const char* what) {
+  q4nx_policy d;
+  policy_defaults(&d);
+  if (p == nullptr) p = &d;
+  const char* bad = policy_problem(p);
+  Q4NX_REQUIRE(bad == nullptr, Q4NX_ERR_ARG, "%s: invalid policy: %s", what, bad);
+  policy_copy(*p, out);
+  return Q4NX_OK;
+}
+
 }  // namespace q4nx
 
 extern "C" {
+
+void q4nx_policy_init(q4nx_policy* p) {
+  if (p != nullptr) q4nx::policy_defaults(p);
+}
 
 int q4nx_abi_version(void) { return Q4NX_ABI_VERSION; }
 

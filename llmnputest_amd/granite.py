@@ -13,15 +13,16 @@ groups the projections by shared input:
 
 At one sequence the attention launch only publishes its split records
 (q4nx_gqa_decode_records) and the o-projection merges them in its prologue
-(q4nx_gemv_attn_q4), which gives the same bits sooner. Then one q8 lm_head launch (final
-RMSNorm fused as its prologue, one order-preserving (max, row) key per tile-row in its
-epilogue) and one bookkeeping launch that reduces the keys to the next token and advances
-positions. A whole step is captured once in a HIP graph
-and replayed; the greedy loop never leaves the device.
+(q4nx_gemv_attn_q4), which gives the same bits sooner. Then one lm_head launch (q8 or q4;
+final RMSNorm fused as its prologue, one order-preserving (max, row) key per 16-row block in
+its epilogue) and one bookkeeping launch that reduces the keys to the next token and
+advances positions. A whole step is captured once in a HIP graph and replayed; the greedy
+loop never leaves the device. Every launch carries the decoder's own launch policy.
 
 Conventions (the reference fixes none of them): fp32 residual stream, pre-norm
-Llama/Granite order, final RMSNorm, tied q8 lm_head whose dequantised row t is the
-embedding of token t, KV cache bf16 [B][Hkv][L][64] per layer.
+Llama/Granite order, final RMSNorm; the embedding of token t is row t of the stored
+model.embed_tokens.weight when the weights have one, else row t of the dequantised (tied)
+lm_head; KV cache bf16 [B][Hkv][L][64] per layer.
 """
 
 from __future__ import annotations
@@ -33,7 +34,8 @@ import numpy as np
 import torch
 
 from . import ops
-from .q4nx import Q4_TILE_BYTES, Q8_TILE_BYTES, Q4NX, check_stored_shape, projection_shape
+from .ops import Policy
+from .q4nx import Q4_TILE_BYTES, Q8_TILE_BYTES, Q4NX, TILE_BYTES, check_stored_shape, projection_shape
 
 
 @dataclass(frozen=True)
@@ -64,27 +66,35 @@ class GraniteConfig:
         elems = q * h + 2 * kv * h + h * q + 3 * h * i
         return elems // 2 + elems // 32 * 4     # 4 bits per weight + bf16 d, m per 32
 
-    def lm_head_bytes(self) -> int:
-        return (self.vocab // 32) * (self.hidden // 256) * Q8_TILE_BYTES
+    def lm_head_bytes(self, kind: str = "q8") -> int:
+        return (self.vocab // 32) * (self.hidden // 256) * TILE_BYTES[kind]
 
 
 @dataclass
 class GraniteWeights:
-    """Device tensors: raw q4nx tiles (uint8) per projection, bf16 norm weights."""
+    """Device tensors: raw q4nx tiles (uint8) per projection, bf16 norm weights, the
+    lm_head's tiles (q8 or q4) and, when the model stores one, a bf16 embedding matrix."""
     cfg: GraniteConfig
     layers: list = field(default_factory=list)   # dicts: q k v o gate up down norm_in norm_post
     norm_final: torch.Tensor | None = None
-    lm_head: torch.Tensor | None = None           # q8 tiles, [vocab, hidden]
+    lm_head: torch.Tensor | None = None           # tiles of [vocab, hidden]
+    lm_head_kind: str = "q8"
+    embed: torch.Tensor | None = None             # bf16 [vocab, hidden]; None: tied lm_head
+
+    def lm_head_bytes(self) -> int:
+        return self.cfg.lm_head_bytes(self.lm_head_kind)
 
     # ------------------------------------------------------------ synthetic
     @staticmethod
-    def synthetic(cfg: GraniteConfig, seed: int = 0, device="cuda") -> "GraniteWeights":
+    def synthetic(cfg: GraniteConfig, seed: int = 0, device="cuda", lm_head_kind: str = "q8",
+                  stored_embed: bool = False) -> "GraniteWeights":
         """Random-init weights of the granite architecture in q4nx tiles, generated on the
-        device from a seeded generator (Q4_1 with d = bf16(|N|*0.02), m = -8d; q8 lm_head
-        with s = bf16(|N|*0.01); norm weights bf16(1 + 0.1 N))."""
+        device from a seeded generator (Q4_1 with d = bf16(|N|*0.02), m = -8d; a q8 lm_head
+        with s = bf16(|N|*0.01) or a q4 one; norm weights bf16(1 + 0.1 N); optionally a bf16
+        N(0,1) embedding matrix)."""
         g = torch.Generator(device=device)
         g.manual_seed(seed)
-        w = GraniteWeights(cfg)
+        w = GraniteWeights(cfg, lm_head_kind=lm_head_kind)
         h, i = cfg.hidden, cfg.inter
         for _ in range(cfg.n_layers):
             w.layers.append({
@@ -99,26 +109,33 @@ class GraniteWeights:
                 "norm_post": random_norm(h, g, device),
             })
         w.norm_final = random_norm(h, g, device)
-        w.lm_head = random_q8_tiles(cfg.vocab, h, g, device)
+        w.lm_head = (random_q8_tiles(cfg.vocab, h, g, device) if lm_head_kind == "q8"
+                     else random_q4_tiles(cfg.vocab, h, g, device))
+        if stored_embed:
+            w.embed = torch.randn((cfg.vocab, h), device=device, generator=g).to(torch.bfloat16)
         return w
 
     # ------------------------------------------------------------ real files
     @staticmethod
     def from_q4nx(path, cfg: GraniteConfig, device="cuda") -> "GraniteWeights":
         """Load a granite `.q4nx` file: raw tiles straight to the device, (N, K) from the
-        config and checked against the stored shape (granite_gemv.py:90-102, 282-288)."""
+        config and checked against the stored shape (granite_gemv.py:90-102, 282-288).
+        The projections are q4; the lm_head is q4 in granite's file
+        (designs/granite_gemv/granite_gemv.h:4-7) and q8 in others, either is taken; the
+        embedding is model.embed_tokens.weight when the file stores it (bf16, as
+        tools/q4nx.py:182-184 reads plain tensors), else the tied lm_head's rows."""
         f = Q4NX(path)
         hf_cfg = {"hidden_size": cfg.hidden, "intermediate_size": cfg.inter,
                   "num_attention_heads": cfg.n_q, "num_key_value_heads": cfg.n_kv,
                   "head_dim": cfg.head_dim, "vocab_size": cfg.vocab}
 
-        def tiles(name, want_kind):
+        def tiles(name, want_kind=None):
             n, k = projection_shape(name, hf_cfg)
             check_stored_shape(f.header[name]["shape"], n, k)
             kind, b = f.tiles(name)
-            if kind != want_kind:
+            if want_kind is not None and kind != want_kind:
                 raise ValueError(f"{name}: stored as {kind}, this decoder expects {want_kind}")
-            return torch.from_numpy(np.ascontiguousarray(b).reshape(-1)).to(device)
+            return kind, torch.from_numpy(np.array(b, copy=True).reshape(-1)).to(device)
 
         def norm(name):
             return torch.from_numpy(f.plain(name).astype(np.uint16).view(np.int16).copy()).to(device).view(torch.bfloat16)
@@ -127,18 +144,26 @@ class GraniteWeights:
         for li in range(cfg.n_layers):
             p = f"model.layers.{li}."
             w.layers.append({
-                "q": tiles(p + "self_attn.q_proj.weight", "q4"),
-                "k": tiles(p + "self_attn.k_proj.weight", "q4"),
-                "v": tiles(p + "self_attn.v_proj.weight", "q4"),
-                "o": tiles(p + "self_attn.o_proj.weight", "q4"),
-                "gate": tiles(p + "mlp.gate_proj.weight", "q4"),
-                "up": tiles(p + "mlp.up_proj.weight", "q4"),
-                "down": tiles(p + "mlp.down_proj.weight", "q4"),
+                "q": tiles(p + "self_attn.q_proj.weight", "q4")[1],
+                "k": tiles(p + "self_attn.k_proj.weight", "q4")[1],
+                "v": tiles(p + "self_attn.v_proj.weight", "q4")[1],
+                "o": tiles(p + "self_attn.o_proj.weight", "q4")[1],
+                "gate": tiles(p + "mlp.gate_proj.weight", "q4")[1],
+                "up": tiles(p + "mlp.up_proj.weight", "q4")[1],
+                "down": tiles(p + "mlp.down_proj.weight", "q4")[1],
                 "norm_in": norm(p + "input_layernorm.weight"),
                 "norm_post": norm(p + "post_attention_layernorm.weight"),
             })
         w.norm_final = norm("model.norm.weight")
-        w.lm_head = tiles("lm_head.weight", "q8")
+        w.lm_head_kind, w.lm_head = tiles("lm_head.weight")
+        name = "model.embed_tokens.weight"
+        if name in f:
+            e = f.plain(name)
+            if f.header[name]["dtype"] != "BF16" or tuple(e.shape) != (cfg.vocab, cfg.hidden):
+                raise ValueError(f"{name}: expected BF16 [{cfg.vocab}, {cfg.hidden}], file has "
+                                 f"{f.header[name]['dtype']} {list(e.shape)}")
+            w.embed = torch.from_numpy(e.astype(np.uint16).view(np.int16).copy()).to(device).view(
+                torch.bfloat16)
         return w
 
 
@@ -175,18 +200,17 @@ class GraniteDecoder:
     greedy loop on the device from a HIP graph of one step."""
 
     def __init__(self, weights: GraniteWeights, max_batch: int = 1, max_len: int = 4096,
-                 device="cuda", fused_tail: bool = False, fused_attn_o: bool = True,
-                 attn_splits: int = 0):
+                 device="cuda", fused_attn_o: bool = True, attn_splits: int = 0,
+                 policy: Policy | None = None):
         c = weights.cfg
         self.cfg, self.w = c, weights
-        # o-proj + MLP of a layer as one three-stage launch (q4nx_layer_tail) instead of three.
-        # Off by default: measured slower on MI355X (the stages' cross-XCD hand-offs cost
-        # more than the weight streams they overlap).
-        self.fused_tail = fused_tail
+        # the launch policy of every kernel this decoder issues (its own copy: other
+        # decoders and callers in the process keep theirs)
+        self.policy = Policy() if policy is None else policy.replace()
         # batch 1: attention only publishes its split records and the o-projection merges
         # them in its prologue (q4nx_gemv_attn_q4), saving attention's cross-workgroup merge
         self.fused_attn_o = fused_attn_o
-        self.attn_splits = attn_splits   # 0: the library's policy for the path taken
+        self.attn_splits = attn_splits   # 0: the library's choice for the path taken
         self.dev = torch.device(device)
         self.max_batch = max_batch
         self.max_len = (max_len + 63) // 64 * 64
@@ -196,8 +220,8 @@ class GraniteDecoder:
         self.v_cache = [torch.zeros(kv_shape, dtype=torch.bfloat16, device=dev) for _ in range(c.n_layers)]
         self.rope = ops.rope_table(self.max_len, c.head_dim, c.theta, device=dev)
         self.h = torch.zeros((b, c.hidden), dtype=torch.float32, device=dev)
-        # sums of h^2 per 32 entries, written by each producer of h for the next RMSNorm
-        self.ssq = torch.zeros((b, c.hidden // 32), dtype=torch.float32, device=dev)
+        # sums of h^2 per 16 entries, written by each producer of h for the next RMSNorm
+        self.ssq = torch.zeros((b, c.hidden // 16), dtype=torch.float32, device=dev)
         self.q = torch.zeros((b, c.q_dim), dtype=torch.bfloat16, device=dev)
         self.attn = torch.zeros((b, c.n_q, c.head_dim), dtype=torch.bfloat16, device=dev)
         self.mlp = torch.zeros((b, c.inter), dtype=torch.bfloat16, device=dev)
@@ -205,7 +229,7 @@ class GraniteDecoder:
         self.tokens = torch.zeros(b, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(b, dtype=torch.int32, device=dev)
         self.lens = torch.ones(b, dtype=torch.int32, device=dev)
-        self.keys = torch.zeros((b, c.vocab // 32), dtype=torch.int64, device=dev)  # argmax keys
+        self.keys = torch.zeros((b, c.vocab // 16), dtype=torch.int64, device=dev)  # argmax keys
         self.history = torch.zeros((self.max_len, b), dtype=torch.int32, device=dev)
         self.step_ctr = torch.zeros(1, dtype=torch.int32, device=dev)
         self.ws = ops.Workspace(ops.WS_COUNTER_BYTES + (64 << 20), device=dev)
@@ -219,7 +243,7 @@ class GraniteDecoder:
         (q4nx_gemv_attn_q4: one sequence, at most 18 splits, the attention row of at most 40
         heads held by one workgroup)."""
         c = self.cfg
-        return (self.fused_attn_o and not self.fused_tail and b == 1 and 1 <= n_split <= 18
+        return (self.fused_attn_o and b == 1 and 1 <= n_split <= 18
                 and c.n_q % 4 == 0 and c.n_q <= 40)
 
     # ------------------------------------------------------------ one step, eager
@@ -229,38 +253,40 @@ class GraniteDecoder:
         kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
         h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
         ssq = self.ssq[:b]
+        pol = self.policy
         n_split = self.attn_splits or ops.gqa_decode_records_splits(b, c.n_q, c.n_kv,
-                                                                    self.max_len)
+                                                                    self.max_len, policy=pol)
         fuse_o = self.fuses_attn_o(b, n_split)
-        ops.embed_q8(w.lm_head, self.tokens[:b], c.vocab, c.hidden, out=h, ssq_out=ssq)
+        if w.embed is not None:
+            ops.embed(w.embed, "bf16", self.tokens[:b], c.vocab, c.hidden, out=h, ssq_out=ssq)
+        else:
+            ops.embed(w.lm_head, w.lm_head_kind, self.tokens[:b], c.vocab, c.hidden, out=h,
+                      ssq_out=ssq)
         for li, L in enumerate(w.layers):
             kc, vc = self.k_cache[li], self.v_cache[li]
             ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
                          kc, vc, q_out=q, norm_w=L["norm_in"], eps=c.eps, ws=self.ws,
-                         ssq_in=ssq)
+                         ssq_in=ssq, policy=pol)
             if fuse_o:
                 rec = ops.gqa_decode_records(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b],
-                                             n_split, c.scale, max_len=self.max_len, ws=self.ws)
+                                             n_split, c.scale, max_len=self.max_len, ws=self.ws,
+                                             policy=pol)
                 ops.gemv_attn_q4(L["o"], c.hidden // 32, rec, residual=h, out=h, ssq_out=ssq)
             else:
                 ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
                                max_len=self.max_len, n_split=self.attn_splits, out=attn,
-                               ws=self.ws)
-            if self.fused_tail:   # o-proj, norm + gate/up + SwiGLU, down: one launch
-                ops.layer_tail(L["o"], L["gate"], L["up"], L["down"], c.hidden, c.q_dim, c.inter,
-                               attn.view(b, c.q_dim), h, ssq, L["norm_post"], c.eps, mlp,
-                               ws=self.ws)
-                continue
-            if not fuse_o:
+                               ws=self.ws, policy=pol)
                 ops.gemv_ex(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q,
-                            residual=h, out=h, ssq_out=ssq, ws=self.ws)
+                            residual=h, out=h, ssq_out=ssq, ws=self.ws, policy=pol)
             ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
-                               norm_w=L["norm_post"], eps=c.eps, ws=self.ws, ssq_in=ssq)
+                               norm_w=L["norm_post"], eps=c.eps, ws=self.ws, ssq_in=ssq,
+                               policy=pol)
             ops.gemv_ex(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h,
-                        ssq_out=ssq, ws=self.ws)
+                        ssq_out=ssq, ws=self.ws, policy=pol)
         # final RMSNorm fused into the lm_head prologue, greedy argmax into its epilogue
-        ops.gemv_ex(w.lm_head, "q8", h, c.vocab // 32, kt_h, norm_w=w.norm_final, eps=c.eps,
-                    out=self.logits[:b], argmax_keys=self.keys[:b], ssq_in=ssq, ws=self.ws)
+        ops.gemv_ex(w.lm_head, w.lm_head_kind, h, c.vocab // 32, kt_h, norm_w=w.norm_final,
+                    eps=c.eps, out=self.logits[:b], argmax_keys=self.keys[:b], ssq_in=ssq,
+                    ws=self.ws, policy=pol)
 
     def step(self, tokens, positions) -> torch.Tensor:
         """One decode step, eager: tokens/positions for B sequences -> fp32 logits [B, V]."""
@@ -275,12 +301,11 @@ class GraniteDecoder:
         self.pos[:b].copy_(positions)
         self.lens[:b].copy_(positions + 1)
         self._launch_step(b)
-        ops.ws_check(self.ws)
         return self.logits[:b]
 
     # ------------------------------------------------------------ graph + greedy loop
     def _advance(self, b: int) -> None:
-        ops.decode_advance(self.keys[:b], self.cfg.vocab // 32, self.tokens[:b], self.pos[:b],
+        ops.decode_advance(self.keys[:b], self.cfg.vocab // 16, self.tokens[:b], self.pos[:b],
                            self.lens[:b], self.step_ctr,
                            self.history[:, :b] if b == self.max_batch else None)
 
@@ -327,7 +352,6 @@ class GraniteDecoder:
                 logs.append(self.logits[:b].clone())
         torch.cuda.synchronize()
         self.seconds += time.perf_counter() - t0
-        ops.ws_check(self.ws)   # raises if a multi-stage launch gave up waiting
         self.calls += n_new
         return self.history[:n_new, :b].t().contiguous().cpu().numpy(), logs
 

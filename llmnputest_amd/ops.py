@@ -3,24 +3,58 @@ all arithmetic runs in libq4nx_hip.so.
 
 Tensor conventions: tile bytes are torch.uint8 (raw q4nx bytes), bf16 values are
 torch.bfloat16 (bit-identical to the uint16 patterns of the C ABI), positions/lengths are
-torch.int32. Every tensor must live on the current CUDA (HIP) device.
+torch.int32. Every tensor must live on the current CUDA (HIP) device. Sums of squares and
+argmax keys are kept per 16-row block ([B, N/16]).
+
+Launch policy: every op that chooses between kernel families takes `policy=` (a `Policy`,
+the C ABI's q4nx_policy). When it is omitted, the policy of the innermost `policy_scope`
+of the calling context applies, else the library's defaults. The scope is a context
+variable (per thread / task), so callers that pass their own policy never see another's.
 """
 
 from __future__ import annotations
+
+import contextlib
+import contextvars
 
 import numpy as np
 import torch
 
 from . import _lib
+from ._lib import Policy
 from .q4nx import Q4_TILE_BYTES, Q8_TILE_BYTES, Q4NXFormatError
 
-KIND = {"q4": 4, "q8": 8}
+KIND = {"q4": 4, "q8": 8, "bf16": 16}
 WS_COUNTER_BYTES = 65536   # Q4NX_WS_COUNTER_BYTES
 TILE_BYTES = {"q4": Q4_TILE_BYTES, "q8": Q8_TILE_BYTES}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+_POLICY: contextvars.ContextVar = contextvars.ContextVar("q4nx_policy", default=None)
+
+
+@contextlib.contextmanager
+def policy_scope(policy: Policy | None):
+    """Ops called inside the block without an explicit `policy=` use this one."""
+    tok = _POLICY.set(policy)
+    try:
+        yield policy
+    finally:
+        _POLICY.reset(tok)
+
+
+def current_policy() -> Policy:
+    """The policy an op called here without `policy=` would use."""
+    p = _POLICY.get()
+    return p if p is not None else Policy()
+
+
+def _pol(policy: Policy | None):
+    p = policy if policy is not None else _POLICY.get()
+    return None if p is None else _lib.C.byref(p)
 
 
 def _stream() -> int:
@@ -92,9 +126,9 @@ def dequant(tiles: torch.Tensor, kind: str, n_tile_rows: int, k_tiles: int,
 
 def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
          residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
-         ws: Workspace | None = None) -> torch.Tensor:
-    """y = residual + W @ x, fp32. x: bf16 [K] or [B, K]; B <= 8 on the VALU kernel, any B on
-    the matrix-core one (`set_mfma_rows` chooses). Returns [N] or [B, N]."""
+         ws: Workspace | None = None, policy: Policy | None = None) -> torch.Tensor:
+    """y = residual + W @ x, fp32. x: bf16 [K] or [B, K]; B <= 8 on the VALU kernels, any B on
+    the matrix-core ones (the policy's mfma_rows choose). Returns [N] or [B, N]."""
     _tiles(tiles, kind, n_tile_rows, k_tiles)
     _dev(x, "x", torch.bfloat16)
     squeeze = x.dim() == 1
@@ -111,15 +145,16 @@ def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_ti
         if residual.numel() != b * n:
             raise ValueError("residual must have the shape of the output")
     ws = ws or default_workspace()
-    wp, wn = ws.get(_lib.lib().q4nx_gemv_ws_bytes(KIND[kind], n_tile_rows, k_tiles, b))
+    pol = _pol(policy)
+    wp, wn = ws.get(_lib.lib().q4nx_gemv_ws_bytes(KIND[kind], n_tile_rows, k_tiles, b, pol))
     _lib.call(f"q4nx_gemv_{kind}", _ptr(tiles), _ptr(x2), _ptr(out), n_tile_rows, k_tiles, b,
-              k, n, _ptr(residual), wp, wn, _stream())
+              k, n, _ptr(residual), wp, wn, pol, _stream())
     return out.reshape(n) if squeeze else out
 
 
 def gemm(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
          residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
-         ws: Workspace | None = None) -> torch.Tensor:
+         ws: Workspace | None = None, policy: Policy | None = None) -> torch.Tensor:
     """Y = residual + X @ W^T on the matrix cores, fp32, for any number of rows.
     x: bf16 [M, K] (row stride a multiple of 8) or [K]. Returns [M, N] (or [N])."""
     _tiles(tiles, kind, n_tile_rows, k_tiles)
@@ -143,20 +178,11 @@ def gemm(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_ti
         if residual.numel() != m * n:
             raise ValueError("residual must have the shape of the output")
     ws = ws or default_workspace()
-    wp, wn = ws.get(_lib.lib().q4nx_gemm_ws_bytes(KIND[kind], n_tile_rows, k_tiles, m))
+    pol = _pol(policy)
+    wp, wn = ws.get(_lib.lib().q4nx_gemm_ws_bytes(KIND[kind], n_tile_rows, k_tiles, m, pol))
     _lib.call("q4nx_gemm", KIND[kind], _ptr(tiles), n_tile_rows, k_tiles, _ptr(x2), x2.stride(0),
-              m, _ptr(out), n, _ptr(residual), wp, wn, _stream())
+              m, _ptr(out), n, _ptr(residual), wp, wn, pol, _stream())
     return out.reshape(n) if squeeze else out
-
-
-def set_gemm_ksplit(parts: int) -> None:
-    """Workgroups along K for `gemm` (0 = automatic)."""
-    _lib.call("q4nx_set_gemm_ksplit", int(parts))
-
-
-def set_mfma_rows(kind: str, min_rows: int) -> None:
-    """Rows from which the GEMV / fused ops of `kind` run on the matrix cores (0 = never)."""
-    _lib.call("q4nx_set_mfma_rows", KIND[kind], int(min_rows))
 
 
 def _ssq(t, name, b, n):
@@ -171,12 +197,12 @@ def gemv_ex(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k
             residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
             argmax_keys: torch.Tensor | None = None, want_y: bool = True,
             ssq_in: torch.Tensor | None = None, ssq_out: torch.Tensor | None = None,
-            ws: Workspace | None = None):
+            ws: Workspace | None = None, policy: Policy | None = None):
     """General GEMV: y = residual + W f(x), f = RMSNorm(x; norm_w) when norm_w is given
-    (x fp32 [B, K]) else identity (x bf16). argmax_keys: int64 [B, n_tile_rows] receives one
-    order-preserving (max, first row) key per tile-row -- reduced by `decode_advance`.
-    ssq_out: fp32 [B, n_tile_rows] sums of y^2 per tile-row; ssq_in: the same for x
-    ([B, K/32], written by x's producer) so the norm needs no cross-wave reduction."""
+    (x fp32 [B, K]) else identity (x bf16). argmax_keys: int64 [B, N/16] receives one
+    order-preserving (max, first row) key per 16-row block -- reduced by `decode_advance`.
+    ssq_out: fp32 [B, N/16] sums of y^2 per 16-row block; ssq_in: the same for x
+    ([B, K/16], written by x's producer) so the norm needs no cross-wave reduction."""
     _tiles(tiles, kind, n_tile_rows, k_tiles)
     _dev(x, "x", torch.float32 if norm_w is not None else torch.bfloat16)
     x2 = x.reshape(1, -1) if x.dim() == 1 else x
@@ -188,15 +214,16 @@ def gemv_ex(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k
         out = torch.empty((b, n), dtype=torch.float32, device=x.device)
     if argmax_keys is not None:
         _dev(argmax_keys, "argmax_keys", torch.int64)
-        if argmax_keys.numel() < b * n_tile_rows:
-            raise ValueError("argmax_keys needs batch * n_tile_rows entries")
-    _ssq(ssq_in, "ssq_in", b, k_tiles * 8)
-    _ssq(ssq_out, "ssq_out", b, n_tile_rows)
+        if argmax_keys.numel() < b * n_tile_rows * 2:
+            raise ValueError("argmax_keys needs batch * N/16 entries")
+    _ssq(ssq_in, "ssq_in", b, k_tiles * 16)
+    _ssq(ssq_out, "ssq_out", b, n_tile_rows * 2)
     ws = ws or default_workspace()
-    wp, wn = ws.get(_lib.lib().q4nx_gemv_ws_bytes(KIND[kind], n_tile_rows, k_tiles, b))
+    pol = _pol(policy)
+    wp, wn = ws.get(_lib.lib().q4nx_gemv_ws_bytes(KIND[kind], n_tile_rows, k_tiles, b, pol))
     _lib.call("q4nx_gemv_ex", KIND[kind], _ptr(tiles), n_tile_rows, k_tiles, _ptr(x2),
               x2.shape[1], _ptr(norm_w), float(eps), _ptr(ssq_in), b, _ptr(out), n,
-              _ptr(residual), _ptr(ssq_out), _ptr(argmax_keys), wp, wn, _stream())
+              _ptr(residual), _ptr(ssq_out), _ptr(argmax_keys), wp, wn, pol, _stream())
     return out
 
 
@@ -216,16 +243,6 @@ def round_bf16(x: torch.Tensor) -> torch.Tensor:
     y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
     _lib.call("q4nx_round_bf16", _ptr(x), _ptr(y), x.numel(), _stream())
     return y
-
-
-def set_split_tiles(tiles_per_wave: int) -> None:
-    """Tuning: K-tiles per wave for all GEMVs (0 = automatic, else 1, 2 or 4)."""
-    _lib.call("q4nx_set_split_tiles", int(tiles_per_wave))
-
-
-def set_gemv_ksplit(parts: int) -> None:
-    """Tuning: workgroups per output group along K (0 = automatic, else 1..8)."""
-    _lib.call("q4nx_set_gemv_ksplit", int(parts))
 
 
 # ---------------------------------------------------------------- elementwise
@@ -293,9 +310,10 @@ def qkv_rope(wq, wk, wv, n_q_heads: int, n_kv_heads: int, k_tiles: int, x: torch
              positions: torch.Tensor, table: torch.Tensor, k_cache: torch.Tensor,
              v_cache: torch.Tensor, q_out: torch.Tensor | None = None,
              norm_w: torch.Tensor | None = None, eps: float = 1e-5, raw_out=None, xn_out=None,
-             ws: Workspace | None = None, ssq_in: torch.Tensor | None = None) -> torch.Tensor:
+             ws: Workspace | None = None, ssq_in: torch.Tensor | None = None,
+             policy: Policy | None = None) -> torch.Tensor:
     """[q,k,v,RoPE] in one launch. x: bf16 [B, K], or fp32 residual [B, K] with norm_w
-    (and optionally its per-32 sums of squares ssq_in [B, K/32]).
+    (and its per-16 sums of squares ssq_in [B, K/16], which the one-row kernels need).
     Caches: bf16 [B, Hkv, Lmax, 64]. Returns q_out bf16 [B, Hq*64]."""
     for t, n, kk in ((wq, "wq", n_q_heads), (wk, "wk", n_kv_heads), (wv, "wv", n_kv_heads)):
         _tiles(t, "q4", kk * 2, k_tiles, n)
@@ -312,14 +330,16 @@ def qkv_rope(wq, wk, wv, n_q_heads: int, n_kv_heads: int, k_tiles: int, x: torch
     if norm_w is not None:
         _dev(norm_w, "norm_w", torch.bfloat16)
     ws = ws or default_workspace()
-    wp, wn = ws.get(_lib.lib().q4nx_qkv_rope_ws_bytes(n_q_heads, n_kv_heads, k_tiles, b))
+    pol = _pol(policy)
+    wp, wn = ws.get(_lib.lib().q4nx_qkv_rope_ws_bytes(n_q_heads, n_kv_heads, k_tiles, b, pol))
+    _ssq(ssq_in, "ssq_in", b, k_tiles * 16)
     lmax = k_cache.shape[2]
     _lib.call("q4nx_qkv_rope", _ptr(wq), _ptr(wk), _ptr(wv), n_q_heads, n_kv_heads, k_tiles,
               _ptr(x), x.shape[1], _ptr(norm_w), float(eps), _ptr(ssq_in), b, _ptr(positions),
               _ptr(table),
               table.shape[0] if table.shape[0] < lmax else lmax, _ptr(q_out), _ptr(k_cache),
               _ptr(v_cache), k_cache.stride(0), k_cache.stride(1), _ptr(raw_out), _ptr(xn_out),
-              wp, wn, _stream())
+              wp, wn, pol, _stream())
     return q_out
 
 
@@ -327,7 +347,8 @@ def gate_up_swiglu(wg, wu, n_tile_rows: int, k_tiles: int, x: torch.Tensor,
                    h_out: torch.Tensor | None = None, norm_w: torch.Tensor | None = None,
                    eps: float = 1e-5, raw_out=None, xn_out=None,
                    ws: Workspace | None = None,
-                   ssq_in: torch.Tensor | None = None) -> torch.Tensor:
+                   ssq_in: torch.Tensor | None = None,
+                   policy: Policy | None = None) -> torch.Tensor:
     """[gate, up, SwiGLU] in one launch; returns bf16 h [B, N]."""
     _tiles(wg, "q4", n_tile_rows, k_tiles, "wg")
     _tiles(wu, "q4", n_tile_rows, k_tiles, "wu")
@@ -337,57 +358,24 @@ def gate_up_swiglu(wg, wu, n_tile_rows: int, k_tiles: int, x: torch.Tensor,
     if h_out is None:
         h_out = torch.empty((b, n), dtype=torch.bfloat16, device=x.device)
     ws = ws or default_workspace()
-    wp, wn = ws.get(_lib.lib().q4nx_gate_up_ws_bytes(n_tile_rows, k_tiles, b))
+    pol = _pol(policy)
+    wp, wn = ws.get(_lib.lib().q4nx_gate_up_ws_bytes(n_tile_rows, k_tiles, b, pol))
+    _ssq(ssq_in, "ssq_in", b, k_tiles * 16)
     _lib.call("q4nx_gate_up_swiglu", _ptr(wg), _ptr(wu), n_tile_rows, k_tiles, _ptr(x),
               x.shape[1], _ptr(norm_w), float(eps), _ptr(ssq_in), b, _ptr(h_out), h_out.stride(0),
-              _ptr(raw_out), _ptr(xn_out), wp, wn, _stream())
+              _ptr(raw_out), _ptr(xn_out), wp, wn, pol, _stream())
     return h_out
-
-
-def layer_tail(wo, wg, wu, wd, hidden: int, q_dim: int, inter: int, attn: torch.Tensor,
-               h: torch.Tensor, ssq: torch.Tensor, norm_w: torch.Tensor, eps: float,
-               mlp: torch.Tensor, ws: Workspace | None = None) -> None:
-    """o-proj + RMSNorm/[gate,up,SwiGLU] + down in one launch (three dependent stages):
-    h += Wo attn; mlp = SwiGLU(RMSNorm(h)); h += Wd mlp; ssq = per-32 sums of h^2."""
-    _tiles(wo, "q4", hidden // 32, q_dim // 256, "wo")
-    _tiles(wg, "q4", inter // 32, hidden // 256, "wg")
-    _tiles(wu, "q4", inter // 32, hidden // 256, "wu")
-    _tiles(wd, "q4", hidden // 32, inter // 256, "wd")
-    _dev(attn, "attn", torch.bfloat16)
-    _dev(h, "h", torch.float32)
-    _dev(mlp, "mlp", torch.bfloat16)
-    _dev(norm_w, "norm_w", torch.bfloat16)
-    b = h.shape[0]
-    _ssq(ssq, "ssq", b, hidden // 32)
-    if attn.numel() < b * q_dim or mlp.numel() < b * inter or h.numel() < b * hidden:
-        raise ValueError("attn, h or mlp too small for the batch")
-    ws = ws or default_workspace()
-    wp, wn = ws.get(_lib.lib().q4nx_layer_tail_ws_bytes(hidden, q_dim, inter, b))
-    _lib.call("q4nx_layer_tail", _ptr(wo), _ptr(wg), _ptr(wu), _ptr(wd), hidden, q_dim, inter,
-              _ptr(attn), _ptr(h), _ptr(ssq), _ptr(norm_w), float(eps), _ptr(mlp), b, wp, wn,
-              _stream())
-
-
-def ws_check(ws: Workspace | None = None) -> None:
-    """Synchronise and raise if a multi-stage launch on this workspace timed out."""
-    ws = ws or default_workspace()
-    _lib.call("q4nx_ws_check", ws.buf.data_ptr(), _stream())
 
 
 # ---------------------------------------------------------------- attention
 
-def set_attn_mfma(on: bool) -> bool:
-    """Run attention on the matrix-core kernel (True, the default) or the VALU kernel.
-    Returns the previous setting."""
-    return bool(_lib.lib().q4nx_set_attn_mfma(1 if on else 0))
-
-
 def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                lens: torch.Tensor, scale: float = 0.125, max_len: int | None = None,
                n_split: int = 0, out: torch.Tensor | None = None, want_f32: bool = False,
-               ws: Workspace | None = None):
+               ws: Workspace | None = None, policy: Policy | None = None):
     """GQA flash-decode. q: bf16 [B, Hq, 64]; caches bf16 [B, Hkv, Lmax, 64]; lens int32 [B].
-    Returns bf16 [B, Hq, 64] (and the fp32 copy when want_f32)."""
+    Returns bf16 [B, Hq, 64] (and the fp32 copy when want_f32). policy.attn_mfma picks the
+    matrix-core (default) or the VALU kernel."""
     _dev(q, "q", torch.bfloat16)
     _dev(lens, "lens", torch.int32)
     for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
@@ -401,31 +389,36 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
     of = torch.empty((b, hq, d), dtype=torch.float32, device=q.device) if want_f32 else None
     ws = ws or default_workspace()
-    need = _lib.lib().q4nx_gqa_decode_ws_bytes(b, hq, hkv, max_len)
+    pol = _pol(policy)
+    need = _lib.lib().q4nx_gqa_decode_ws_bytes(b, hq, hkv, max_len, pol)
     if n_split:
         need = max(need, WS_COUNTER_BYTES + b * hkv * n_split * (hq // hkv) * 68 * 4)
     wp, wn = ws.get(need)
     _lib.call("q4nx_gqa_decode", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(of), b,
               hq, hkv, d, _ptr(lens), max_len, k_cache.stride(0), k_cache.stride(1),
-              float(scale), int(n_split), wp, wn, _stream())
+              float(scale), int(n_split), wp, wn, pol, _stream())
     return (out, of) if want_f32 else out
 
 
-def gqa_decode_splits(batch: int, n_q_heads: int, n_kv_heads: int, max_len: int) -> int:
-    """The split count `gqa_decode` chooses for n_split=0 under the current kernel policy."""
-    return int(_lib.lib().q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len))
+def gqa_decode_splits(batch: int, n_q_heads: int, n_kv_heads: int, max_len: int,
+                      policy: Policy | None = None) -> int:
+    """The split count `gqa_decode` chooses for n_split=0 under the policy."""
+    return int(_lib.lib().q4nx_gqa_decode_splits(batch, n_q_heads, n_kv_heads, max_len,
+                                                 _pol(policy)))
 
 
 def gqa_decode_records_splits(batch: int, n_q_heads: int, n_kv_heads: int,
-                              max_len: int) -> int:
+                              max_len: int, policy: Policy | None = None) -> int:
     """The split count for records that `gemv_attn_q4` merges (the attention policy's, capped
     at 12: fewer, longer splits make the pair faster)."""
-    return int(_lib.lib().q4nx_gqa_decode_records_splits(batch, n_q_heads, n_kv_heads, max_len))
+    return int(_lib.lib().q4nx_gqa_decode_records_splits(batch, n_q_heads, n_kv_heads, max_len,
+                                                         _pol(policy)))
 
 
 def gqa_decode_records(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        lens: torch.Tensor, n_split: int, scale: float = 0.125,
-                       max_len: int | None = None, ws: Workspace | None = None) -> torch.Tensor:
+                       max_len: int | None = None, ws: Workspace | None = None,
+                       policy: Policy | None = None) -> torch.Tensor:
     """The publishing half of `gqa_decode`: every split writes its (acc[64], m, l) record and
     nothing is merged. Returns the records, an fp32 view of the workspace shaped
     [B, Hkv, n_split, Hq/Hkv, 68] (valid until the workspace is next used)."""
@@ -446,7 +439,7 @@ def gqa_decode_records(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
     wp, wn = ws.get(WS_COUNTER_BYTES + pb)
     _lib.call("q4nx_gqa_decode_records", _ptr(q), _ptr(k_cache), _ptr(v_cache), b, hq, hkv, d,
               _ptr(lens), max_len, k_cache.stride(0), k_cache.stride(1), float(scale),
-              int(n_split), wp, wn, _stream())
+              int(n_split), wp, wn, _pol(policy), _stream())
     return ws.buf[WS_COUNTER_BYTES:WS_COUNTER_BYTES + pb].view(torch.float32).view(
         b, hkv, n_split, g, 68)
 
@@ -466,7 +459,7 @@ def gemv_attn_q4(tiles: torch.Tensor, n_tile_rows: int, records: torch.Tensor,
     n = n_tile_rows * 32
     if out is None:
         out = torch.empty((1, n), dtype=torch.float32, device=records.device)
-    _ssq(ssq_out, "ssq_out", 1, n_tile_rows)
+    _ssq(ssq_out, "ssq_out", 1, n_tile_rows * 2)
     _lib.call("q4nx_gemv_attn_q4", _ptr(tiles), n_tile_rows, _ptr(records), ns, hq, hkv,
               _ptr(out), _ptr(residual), _ptr(ssq_out), _stream())
     return out
@@ -474,18 +467,33 @@ def gemv_attn_q4(tiles: torch.Tensor, n_tile_rows: int, records: torch.Tensor,
 
 # ---------------------------------------------------------------- decode helpers
 
-def embed_q8(tiles: torch.Tensor, tokens: torch.Tensor, vocab: int, hidden: int,
-             out: torch.Tensor | None = None,
-             ssq_out: torch.Tensor | None = None) -> torch.Tensor:
-    _tiles(tiles, "q8", vocab // 32, hidden // 256, "tiles")
+def embed(table: torch.Tensor, kind: str, tokens: torch.Tensor, vocab: int, hidden: int,
+          out: torch.Tensor | None = None,
+          ssq_out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 rows `tokens` of a [vocab, hidden] table: kind "bf16" (a stored embedding
+    matrix) or "q4" / "q8" tiles (a tied lm_head, dequantised exactly). ssq_out: fp32
+    [B, hidden/16] sums of squares for a following RMSNorm."""
+    if kind == "bf16":
+        _dev(table, "table", torch.bfloat16)
+        if table.numel() != vocab * hidden:
+            raise ValueError(f"table has {table.numel()} values, expected {vocab}x{hidden}")
+    else:
+        _tiles(table, kind, vocab // 32, hidden // 256, "table")
     _dev(tokens, "tokens", torch.int32)
     b = tokens.numel()
     if out is None:
-        out = torch.empty((b, hidden), dtype=torch.float32, device=tiles.device)
-    _ssq(ssq_out, "ssq_out", b, hidden // 32)
-    _lib.call("q4nx_embed_q8", _ptr(tiles), _ptr(tokens), _ptr(out), _ptr(ssq_out), vocab, hidden,
-              b, _stream())
+        out = torch.empty((b, hidden), dtype=torch.float32, device=table.device)
+    _ssq(ssq_out, "ssq_out", b, hidden // 16)
+    _lib.call("q4nx_embed", KIND[kind], _ptr(table), _ptr(tokens), _ptr(out), _ptr(ssq_out),
+              vocab, hidden, b, _stream())
     return out
+
+
+def embed_q8(tiles: torch.Tensor, tokens: torch.Tensor, vocab: int, hidden: int,
+             out: torch.Tensor | None = None,
+             ssq_out: torch.Tensor | None = None) -> torch.Tensor:
+    """`embed` of a q8-tiled table."""
+    return embed(tiles, "q8", tokens, vocab, hidden, out=out, ssq_out=ssq_out)
 
 
 def argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

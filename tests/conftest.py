@@ -38,43 +38,60 @@ def dev():
     return torch.device("cuda:0")
 
 
-def _set_kernel_path(path: str) -> None:
-    """Which kernels the GEMV / fused entry points use: the VALU GEMV only, the matrix-core
-    kernels for every row count, or the library's default policy."""
+# Launch policies of the kernel families: "valu" the VALU kernels (the row-block kernels at
+# one row, the general GEMV for 2-8), "general" the general VALU GEMV at every row count,
+# "mfma" the matrix-core kernels for every row count, "default" the library's defaults.
+PATHS = {
+    "valu": dict(mfma_rows_q4=0, mfma_rows_q8=0),
+    "general": dict(mfma_rows_q4=0, mfma_rows_q8=0, rowblock=0),
+    "mfma": dict(mfma_rows_q4=1, mfma_rows_q8=1),
+    "default": {},
+}
+
+
+def _scope(path: str):
     from llmnputest_amd import ops
-    q4, q8 = {"valu": (0, 0), "mfma": (1, 1), "default": (2, 1)}[path]
-    ops.set_mfma_rows("q4", q4)
-    ops.set_mfma_rows("q8", q8)
+    return ops.policy_scope(ops.Policy(**PATHS[path]))
 
 
-@pytest.fixture(params=["valu", "mfma"])
+@pytest.fixture(params=["valu", "general", "mfma"])
 def kpath(request, dev):
     """Run the test once on each kernel family."""
-    _set_kernel_path(request.param)
-    yield request.param
-    _set_kernel_path("default")
+    with _scope(request.param):
+        yield request.param
+
+
+@pytest.fixture(params=["valu", "general"])
+def vpath(request, dev):
+    """Run the test on each VALU kernel family (row-block at one row, and the general one)."""
+    with _scope(request.param):
+        yield request.param
 
 
 @pytest.fixture
 def valu(dev):
-    """Pin the VALU GEMV (for tests of its own knobs)."""
-    _set_kernel_path("valu")
-    yield
-    _set_kernel_path("default")
+    """Pin the VALU kernels (row-block at one row)."""
+    with _scope("valu"):
+        yield
+
+
+@pytest.fixture
+def general(dev):
+    """Pin the general VALU GEMV (for tests of its own splits)."""
+    with _scope("general"):
+        yield
 
 
 @pytest.fixture
 def mfma(dev):
     """Pin the matrix-core kernels for every row count."""
-    _set_kernel_path("mfma")
-    yield
-    _set_kernel_path("default")
+    with _scope("mfma"):
+        yield
 
 
 @pytest.fixture(params=["mfma", "valu"])
 def apath(request, dev):
     """Run an attention test on each attention kernel (matrix-core and VALU)."""
     from llmnputest_amd import ops
-    ops.set_attn_mfma(request.param == "mfma")
-    yield request.param
-    ops.set_attn_mfma(True)
+    with ops.policy_scope(ops.Policy(attn_mfma=int(request.param == "mfma"))):
+        yield request.param

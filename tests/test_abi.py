@@ -29,7 +29,7 @@ def test_header_symbols_exported():
     missing = [n for n in names if not hasattr(h, n)]
     assert not missing, missing
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
-    assert _lib.lib().q4nx_abi_version() == 1
+    assert _lib.lib().q4nx_abi_version() == 2
 
 
 def rc_msg(name, *args):
@@ -37,52 +37,67 @@ def rc_msg(name, *args):
     return rc, _lib.lib().q4nx_last_error().decode()
 
 
+def pol(**kw):
+    return C.byref(_lib.Policy(**kw))
+
+
+def test_policy_defaults_and_validation():
+    p = _lib.Policy()
+    assert (p.mfma_rows_q4, p.mfma_rows_q8, p.rowblock, p.gemv_ksplit, p.gemv_tiles_per_wave,
+            p.gemm_ksplit, p.attn_mfma) == (2, 1, 1, 0, 0, 0, 1)
+    fake = C.c_void_p(0x10000)
+    for bad in ({"gemv_ksplit": 9}, {"gemv_tiles_per_wave": 3}, {"gemm_ksplit": -1},
+                {"attn_mfma": 2}, {"rowblock": 5}, {"mfma_rows_q4": -1}):
+        rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 8, 10, 1, 2560, 256, None, None, 0,
+                         pol(**bad), None)
+        assert rc == ERR_ARG and "policy" in msg, bad
+        assert _lib.lib().q4nx_gemv_ws_bytes(4, 80, 32, 1, pol(**bad)) == 0   # queries: 0
+        assert _lib.lib().q4nx_gqa_decode_splits(1, 40, 8, 2048, pol(**bad)) == 0
+
+
 def test_gemv_argument_errors():
     fake = C.c_void_p(0x10000)       # aligned, never dereferenced: validation fails first
-    rc, msg = rc_msg("q4nx_gemv_q4", None, fake, fake, 8, 10, 1, 2560, 256, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemv_q4", None, fake, fake, 8, 10, 1, 2560, 256, None, None, 0, None,
+                     None)
     assert rc == ERR_ARG and "weights" in msg
     rc, msg = rc_msg("q4nx_gemv_q4", C.c_void_p(0x10001), fake, fake, 8, 10, 1, 2560, 256,
-                     None, None, 0, None)
+                     None, None, 0, None, None)
     assert rc == ERR_ARG                                   # misaligned tiles
-    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 0, 10, 1, 2560, 256, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 0, 10, 1, 2560, 256, None, None, 0, None,
+                     None)
     assert rc == ERR_SHAPE and "n_tile_rows" in msg
-    _lib.lib().q4nx_set_mfma_rows(8, 0)                   # VALU kernel only: batch <= 8
-    try:
-        rc, msg = rc_msg("q4nx_gemv_q8", fake, fake, fake, 8, 4, 9, 1024, 256, None, None, 0,
-                         None)
-    finally:
-        _lib.lib().q4nx_set_mfma_rows(8, 1)
+    rc, msg = rc_msg("q4nx_gemv_q8", fake, fake, fake, 8, 4, 9, 1024, 256, None, None, 0,
+                     pol(mfma_rows_q8=0), None)                 # VALU kernel only: batch <= 8
     assert rc == ERR_SHAPE and "batch" in msg
-    rc, msg = rc_msg("q4nx_set_mfma_rows", 5, 1)
-    assert rc == ERR_ARG
-    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 8, 10, 1, 2000, 256, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 8, 10, 1, 2000, 256, None, None, 0, None,
+                     None)
     assert rc == ERR_SHAPE and "x_stride" in msg           # K = 2560 does not fit a 2000 row
     rc, msg = rc_msg("q4nx_gemv_ex", 5, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), None, 1,
-                     fake, 256, None, None, None, None, 0, None)
+                     fake, 256, None, None, None, None, 0, None, None)
     assert rc == ERR_ARG and "kind" in msg
     rc, msg = rc_msg("q4nx_gemv_ex", 4, fake, 8, 10, fake, 2560, None, C.c_float(1e-5), fake, 1,
-                     fake, 256, None, None, None, None, 0, None)
+                     fake, 256, None, None, None, None, 0, None, None)
     assert rc == ERR_ARG and "ssq_in" in msg               # partial sums without a norm
-    rc, msg = rc_msg("q4nx_set_gemv_ksplit", 9)
-    assert rc == ERR_ARG
-    rc, msg = rc_msg("q4nx_set_split_tiles", 3)
-    assert rc == ERR_ARG
 
 
 def test_fused_and_attention_argument_errors():
     fake = C.c_void_p(0x10000)
     rc, msg = rc_msg("q4nx_qkv_rope", fake, fake, fake, 40, 7, 10, fake, 2560, None,
                      C.c_float(1e-5), None, 1, fake, fake, 512, fake, fake, fake, 8 * 512 * 64,
-                     512 * 64, None, None, None, 0, None)
+                     512 * 64, None, None, None, 0, None, None)
     assert rc == ERR_SHAPE and "n_kv_heads" in msg         # 40 % 7 != 0
     rc, msg = rc_msg("q4nx_gqa_decode", fake, fake, fake, fake, None, 1, 40, 8, 128, fake, 512,
-                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 0, None, 0, None)
+                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 0, None, 0, None, None)
     assert rc == ERR_SHAPE and "head_dim" in msg
     rc, msg = rc_msg("q4nx_gqa_decode", fake, fake, fake, fake, None, 1, 40, 8, 64, fake, 4096,
-                     8 * 4096 * 64, 4096 * 64, C.c_float(0.125), 8, None, 0, None)
+                     8 * 4096 * 64, 4096 * 64, C.c_float(0.125), 8, None, 0, None, None)
     assert rc == ERR_WS and "workspace" in msg
-    rc, msg = rc_msg("q4nx_embed_q8", fake, fake, fake, None, 100, 2560, 1, None)
-    assert rc == ERR_SHAPE                                 # vocab not a multiple of 32
+    rc, msg = rc_msg("q4nx_embed", 8, fake, fake, fake, None, 100, 2560, 1, None)
+    assert rc == ERR_SHAPE                                 # q8 tiles: vocab not a multiple of 32
+    rc, msg = rc_msg("q4nx_embed", 16, fake, fake, fake, None, 100, 2500, 1, None)
+    assert rc == ERR_SHAPE                                 # hidden not a multiple of 256
+    rc, msg = rc_msg("q4nx_embed", 5, fake, fake, fake, None, 128, 2560, 1, None)
+    assert rc == ERR_ARG and "kind" in msg
     rc, msg = rc_msg("q4nx_dequant_q4", fake, None, 1, 1, 0, 0, None)
     assert rc == ERR_ARG
 
@@ -93,22 +108,19 @@ def test_attention_record_splits_and_errors():
     lib = _lib.lib()
     fake = C.c_void_p(0x10000)
     for lmax, auto in ((640, 5), (2176, 9), (4160, 16)):   # the 3B decode shapes
-        assert lib.q4nx_gqa_decode_splits(1, 40, 8, lmax) == auto
-        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, lmax) == min(auto, 12)
-    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 32
-    prev = lib.q4nx_set_attn_mfma(0)
-    try:                                                     # VALU policy: up to 64 splits
-        assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 64
-        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, 32768) == 12
-    finally:
-        lib.q4nx_set_attn_mfma(prev)
-    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 0) == 0       # invalid shapes: 0
-    assert lib.q4nx_gqa_decode_records_splits(0, 40, 8, 64) == 0
+        assert lib.q4nx_gqa_decode_splits(1, 40, 8, lmax, None) == auto
+        assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, lmax, None) == min(auto, 12)
+    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768, None) == 32
+    valu = pol(attn_mfma=0)                                  # VALU policy: up to 64 splits
+    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768, valu) == 64
+    assert lib.q4nx_gqa_decode_records_splits(1, 40, 8, 32768, valu) == 12
+    assert lib.q4nx_gqa_decode_splits(1, 40, 8, 0, None) == 0       # invalid shapes: 0
+    assert lib.q4nx_gqa_decode_records_splits(0, 40, 8, 64, None) == 0
     rc, msg = rc_msg("q4nx_gqa_decode_records", fake, fake, fake, 1, 40, 8, 64, fake, 512,
-                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 0, fake, 1 << 20, None)
+                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 0, fake, 1 << 20, None, None)
     assert rc == ERR_ARG and "n_split" in msg               # the count must be given
     rc, msg = rc_msg("q4nx_gqa_decode_records", fake, fake, fake, 1, 40, 8, 64, fake, 512,
-                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 4, fake, 4096, None)
+                     8 * 512 * 64, 512 * 64, C.c_float(0.125), 4, fake, 4096, None, None)
     assert rc == ERR_WS and "workspace" in msg              # 4 splits need 64 KB + 43,520 B
     rc, msg = rc_msg("q4nx_gemv_attn_q4", fake, 80, fake, 10, 44, 4, fake, None, None, None)
     assert rc == ERR_SHAPE and "query heads" in msg         # 11 K-tiles
@@ -121,85 +133,85 @@ def test_attention_record_splits_and_errors():
     assert rc == ERR_ARG and "16-byte" in msg               # misaligned records
 
 
-def test_attn_policy_knob_is_atomic():
-    """q4nx_set_attn_mfma exchanges the process-wide setting and returns the one it replaced;
-    setters and split queries racing from several threads (ctypes drops the GIL in the call)
-    leave every query with one policy whole: 32 (matrix cores) or 64 (VALU) splits at 32768
-    positions. Host-only calls, no launch."""
+def test_policies_are_per_call():
+    """Two policies used side by side, also from racing threads (ctypes drops the GIL in the
+    call), each get their own answer: the library keeps no setting between calls."""
     import threading
     lib = _lib.lib()
-    prev = lib.q4nx_set_attn_mfma(1)
-    try:
-        assert lib.q4nx_set_attn_mfma(0) == 1
-        assert lib.q4nx_set_attn_mfma(0) == 0
-        assert lib.q4nx_set_attn_mfma(7) == 0                  # any nonzero value means on
-        assert lib.q4nx_set_attn_mfma(1) == 1
-        seen = set()
+    pm, pv = _lib.Policy(), _lib.Policy(attn_mfma=0)
+    bad = []
 
-        def worker(i):
-            for n in range(2000):
-                if (i + n) % 2:
-                    lib.q4nx_set_attn_mfma(n & 1)
-                else:
-                    seen.add(lib.q4nx_gqa_decode_splits(1, 40, 8, 32768))
+    def worker(i):
+        for n in range(2000):
+            p = pm if (i + n) % 2 else pv
+            want = 32 if p is pm else 64
+            if lib.q4nx_gqa_decode_splits(1, 40, 8, 32768, C.byref(p)) != want:
+                bad.append((i, n))
+            ws = lib.q4nx_gemv_ws_bytes(4, 80, 32, 1, C.byref(p))
+            if ws != 0:                       # one row of q4 on the row-block kernels
+                bad.append(("ws", ws))
 
-        threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
-        for t in threads:
-            t.start()
-        for t in threads:
-            t.join()
-        assert seen and seen <= {32, 64}
-        lib.q4nx_set_attn_mfma(1)
-        assert lib.q4nx_gqa_decode_splits(1, 40, 8, 32768) == 32
-    finally:
-        lib.q4nx_set_attn_mfma(prev)
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not bad, bad[:5]
+    # the general VALU kernel's split needs a workspace; the row-block one does not
+    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1, pol(rowblock=0)) == 65536 + 80 * 3 * 32 * 4
+    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1, None) == 0
 
 
 def test_gemm_argument_errors():
     fake = C.c_void_p(0x10000)
-    rc, msg = rc_msg("q4nx_gemm", 3, fake, 8, 10, fake, 2560, 4, fake, 256, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemm", 3, fake, 8, 10, fake, 2560, 4, fake, 256, None, None, 0, None,
+                     None)
     assert rc == ERR_ARG and "kind" in msg
-    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 0, fake, 256, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 0, fake, 256, None, None, 0, None,
+                     None)
     assert rc == ERR_SHAPE and "m_rows" in msg
-    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2564, 4, fake, 256, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2564, 4, fake, 256, None, None, 0, None,
+                     None)
     assert rc == ERR_SHAPE and "x_stride" in msg            # not a multiple of 8
-    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 4, fake, 128, None, None, 0, None)
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 4, fake, 128, None, None, 0, None,
+                     None)
     assert rc == ERR_SHAPE and "y_stride" in msg            # N = 256 does not fit
     rc, msg = rc_msg("q4nx_gemm", 8, fake, 8, 10, fake, 2560, 4, C.c_void_p(0x10004), 256,
-                     None, None, 0, None)
+                     None, None, 0, None, None)
     assert rc == ERR_ARG and "y" in msg                     # misaligned output
-    rc, msg = rc_msg("q4nx_set_gemm_ksplit", 9)
-    assert rc == ERR_ARG
+    rc, msg = rc_msg("q4nx_gemm", 4, fake, 8, 10, fake, 2560, 4, fake, 256, None, None, 0,
+                     pol(gemm_ksplit=9), None)
+    assert rc == ERR_ARG and "policy" in msg
 
 
 def test_ws_queries():
     lib = _lib.lib()
-    # 80 tile-rows do not fill the GPU: K is split 3 ways, partials [80][3][1][32] fp32
-    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1) == 65536 + 80 * 3 * 32 * 4
-    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 1) == 0      # enough tile-rows: no split
+    general = pol(rowblock=0)
+    # 80 tile-rows do not fill the GPU: the general VALU kernel splits K 3 ways, partials
+    # [80][3][1][32] fp32; the row-block kernels (the default at one row) need nothing
+    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1, general) == 65536 + 80 * 3 * 32 * 4
+    assert lib.q4nx_gemv_ws_bytes(4, 80, 32, 1, None) == 0
+    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 1, general) == 0   # enough tile-rows: no split
     # batch 9 runs on the matrix cores: no split, room for 9 normalised rows
-    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9) == 65536 + 9 * 2560 * 2
+    assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9, None) == 65536 + 9 * 2560 * 2
     # 56 heads of 2 tile-rows, batch 2 on the VALU kernel: 5 parts of 2 K-tiles,
     # [56][5][batch 2][64]; on the matrix cores (the default from 2 rows): 5 parts of
     # [16 rows][64] per head, then room for 2 normalised rows of 2560 bf16
-    lib.q4nx_set_mfma_rows(4, 0)
-    try:
-        assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2) == 65536 + 56 * 5 * 2 * 64 * 4
-    finally:
-        lib.q4nx_set_mfma_rows(4, 2)
-    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2) == 65536 + 56 * 5 * 16 * 64 * 4 + 2 * 2560 * 2
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, pol(mfma_rows_q4=0)) == 65536 + 56 * 5 * 2 * 64 * 4
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, None) == 65536 + 56 * 5 * 16 * 64 * 4 + 2 * 2560 * 2
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 1, None) == 0     # one row: row-block kernel
     # q8 lm_head at one row (matrix cores): 3136 workgroups, no split, one normalised row
-    assert lib.q4nx_gemv_ws_bytes(8, 3136, 10, 1) == 65536 + 2560 * 2
-    assert lib.q4nx_gate_up_ws_bytes(256, 10, 1) == 0
-    assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64) == 0  # one split: no workspace
-    big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768)    # 64 splits of (acc[64], m, l, pad)
+    assert lib.q4nx_gemv_ws_bytes(8, 3136, 10, 1, None) == 65536 + 2560 * 2
+    assert lib.q4nx_gate_up_ws_bytes(256, 10, 1, None) == 0
+    assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64, None) == 0  # one split: no workspace
+    big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768, pol(attn_mfma=0))   # 64 splits
     assert big == 65536 + 8 * 64 * 5 * 68 * 4
     # batched contraction: 80 tile-rows x 1 block of 16 rows split 3 ways along K
-    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 8) == 65536 + 80 * 3 * 16 * 32 * 4
-    assert lib.q4nx_gemm_ws_bytes(4, 256, 10, 8) == 0      # 256 workgroups: no split
+    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 8, None) == 65536 + 80 * 3 * 16 * 32 * 4
+    assert lib.q4nx_gemm_ws_bytes(4, 256, 10, 8, None) == 0      # 256 workgroups: no split
     # 512 rows: 40 pairs of tile-rows x 4 blocks of 128 rows, split 2 ways
-    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 512) == 65536 + 160 * 2 * 128 * 64 * 4
-    assert lib.q4nx_gemm_ws_bytes(5, 80, 32, 8) == 0
+    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 512, None) == 65536 + 160 * 2 * 128 * 64 * 4
+    assert lib.q4nx_gemm_ws_bytes(5, 80, 32, 8, None) == 0
 
 
 @pytest.mark.parametrize("max_pos,theta", [(4096, 10000.0), (64, 500000.0)])

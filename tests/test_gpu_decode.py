@@ -1,12 +1,13 @@
 """The granite-shaped decode step on the GPU against the oracle, per step.
 
-Full widths (hidden 2560, intermediate 8192, 40q/8kv heads, d=64, vocab 100352, q8
-lm_head); reduced layer counts and contexts keep the float64 CPU oracle to seconds. The
-GPU runs its own greedy loop from a HIP graph; the oracle replays the same tokens
-(teacher-forced on the GPU's choices) and every step's logits are compared. bf16
+Full widths (hidden 2560, intermediate 8192, 40q/8kv heads, d=64); reduced layer counts,
+vocabularies and contexts keep the float64 CPU oracle to seconds, and the full 40-layer,
+100352-vocab step at context 2048 is checked over all 128 greedy tokens of the benchmark's
+workload. The GPU runs its own greedy loop from a HIP graph; the oracle replays the same
+tokens (teacher-forced on the GPU's choices) and every step's logits are compared. bf16
 narrowing inside the step makes rare 1-ulp flips unavoidable between two correct
-implementations, so the per-step gate is cosine >= 0.9999 with max|Δ|/max|ref| < 5e-3, and
-the GPU's greedy token must be the oracle's argmax unless the oracle's top two logits lie
+implementations; the per-step gate is cosine >= 0.9999 with max|Δ|/max|ref| < REL, and the
+GPU's greedy token must be the oracle's argmax unless the oracle's top two logits lie
 within that tolerance.
 """
 
@@ -14,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from llmnputest_amd import ops
+from llmnputest_amd import ops, q4nx, synth
 from llmnputest_amd.granite import GraniteConfig, GraniteDecoder, GraniteWeights
 from oracle import cpu_oracle
 from oracle import decode_oracle as do
@@ -23,7 +24,10 @@ from oracle import q4nx_oracle as qo
 pytestmark = pytest.mark.gpu
 
 COS = 0.9999
-REL = 5e-3
+# The north star's bar for bf16 outputs. Over the 128 steps of the 40-layer step (a chain of
+# 40 layers of bf16 narrowings) the largest per-step value measured is 6.6e-4, cosine
+# >= 0.99999989; the per-step values are printed.
+REL = 1e-3
 
 
 def host_bits(t: torch.Tensor) -> np.ndarray:
@@ -42,7 +46,9 @@ def host_copy(w: GraniteWeights) -> do.DecodeWeights:
         hw.norm_in.append(host_bits(L["norm_in"]))
         hw.norm_post.append(host_bits(L["norm_post"]))
     hw.norm_final = host_bits(w.norm_final)
-    hw.lm_head = w.lm_head.cpu().numpy().reshape(-1, 8704)
+    hw.lm_head_kind = w.lm_head_kind
+    hw.lm_head = w.lm_head.cpu().numpy().reshape(-1, q4nx.TILE_BYTES[w.lm_head_kind])
+    hw.embed = None if w.embed is None else host_bits(w.embed)
     return hw
 
 
@@ -55,52 +61,101 @@ def check_step(got, ref, token):
     return rel, cos
 
 
-@pytest.mark.parametrize("n_layers,batch,ctx,n_new,fused", [(2, 1, 256, 6, False),
-                                                            (1, 3, 100, 3, False),
-                                                            (2, 1, 200, 3, True),
-                                                            (2, 1, 2100, 2, False)])
-def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new, fused):
-    cfg = GraniteConfig(n_layers=n_layers)
-    w = GraniteWeights.synthetic(cfg, seed=11, device=dev)
-    dec = GraniteDecoder(w, max_batch=batch, max_len=ctx + n_new, device=dev, fused_tail=fused)
-    dec.seed_cache(ctx, seed=12)
+def run_and_check(w, batch, ctx, n_new, policy=None, seed=12):
+    """Greedy decode on the GPU, then the oracle teacher-forced on its tokens, every step and
+    sequence compared. Returns the per-step (rel, cos) of sequence 0."""
+    dec = GraniteDecoder(w, max_batch=batch, max_len=ctx + n_new, device=w.lm_head.device,
+                         policy=policy)
+    dec.seed_cache(ctx, seed=seed)
     kc = [host_bits(t) for t in dec.k_cache]
     vc = [host_bits(t) for t in dec.v_cache]
     rng = np.random.default_rng(13)
-    first = rng.integers(0, cfg.vocab, batch).astype(np.int32)
+    first = rng.integers(0, w.cfg.vocab, batch).astype(np.int32)
     start = np.full(batch, ctx, np.int32) - np.arange(batch, dtype=np.int32) * 7   # ragged
     toks, logits = dec.generate(first, start, n_new, record_logits=True)
     oracle = do.DecodeOracle(host_copy(w), kc, vc, dec.max_len, gemv=cpu_oracle.gemv)
-    prev = first
+    prev, stats = first, []
     for i in range(n_new):
         ref = oracle.step(prev, start + i)
         got = logits[i].cpu().numpy()
         for b in range(batch):
-            check_step(got[b], ref[b], int(toks[b, i]))
+            s = check_step(got[b], ref[b], int(toks[b, i]))
+            if b == 0:
+                stats.append(s)
         prev = toks[:, i]
+    return stats
 
 
-def test_full_granite_step_vs_oracle(dev):
-    """The full granite-3B-shaped decode (40 layers, q8 lm_head 2560->100352, batch 1, context
-    2048, the default kernels and fusions) against the CPU oracle for two greedy tokens."""
+@pytest.mark.parametrize("n_layers,batch,ctx,n_new", [(2, 1, 256, 6), (1, 3, 100, 3),
+                                                      (2, 1, 2100, 2), (2, 8, 300, 4)])
+def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new):
+    cfg = GraniteConfig(n_layers=n_layers)
+    w = GraniteWeights.synthetic(cfg, seed=11, device=dev)
+    run_and_check(w, batch, ctx, n_new, policy=ops.current_policy())
+
+
+@pytest.mark.parametrize("lm_kind,stored_embed", [("q4", True), ("q4", False), ("q8", True)])
+def test_decode_lm_head_kinds_and_embeddings(dev, lm_kind, stored_embed):
+    """A q4 lm_head (granite's file: designs/granite_gemv/granite_gemv.h:4-7) or a q8 one, with
+    a stored embedding matrix or the tied lm_head's rows, at batch 1 and 2."""
+    cfg = GraniteConfig(n_layers=2, vocab=8192)
+    w = GraniteWeights.synthetic(cfg, seed=17, device=dev, lm_head_kind=lm_kind,
+                                 stored_embed=stored_embed)
+    for batch in (1, 2):
+        run_and_check(w, batch, 200, 3)
+
+
+# ------------------------------------------------------------------ the full workload
+
+FULL_CTX, FULL_NEW, CHUNK = 2048, 128, 32
+
+
+@pytest.fixture(scope="module")
+def full_run(dev):
+    """The benchmark's decode workload (40 layers, q8 lm_head 2560->100352, batch 1, context
+    2048, 128 greedy tokens, the default kernels and fusions) decoded once on the GPU; the
+    oracle replays it in chunks."""
     cfg = GraniteConfig()
     assert cfg.n_layers == 40
     w = GraniteWeights.synthetic(cfg, seed=91, device=dev)
-    ctx, n_new = 2048, 2
-    dec = GraniteDecoder(w, max_batch=1, max_len=ctx + n_new, device=dev)
-    dec.seed_cache(ctx, seed=92)
+    dec = GraniteDecoder(w, max_batch=1, max_len=FULL_CTX + FULL_NEW, device=dev)
+    dec.seed_cache(FULL_CTX, seed=92)
     kc = [host_bits(t) for t in dec.k_cache]
     vc = [host_bits(t) for t in dec.v_cache]
     first = np.array([4242], np.int32)
-    start = np.array([ctx], np.int32)
-    toks, logits = dec.generate(first, start, n_new, record_logits=True)
-    oracle = do.DecodeOracle(host_copy(w), kc, vc, dec.max_len, gemv=cpu_oracle.gemv)
-    prev = first
-    for i in range(n_new):
-        ref = oracle.step(prev, start + i)
-        check_step(logits[i].cpu().numpy()[0], ref[0], int(toks[0, i]))
-        prev = toks[:, i]
+    toks, logits = dec.generate(first, [FULL_CTX], FULL_NEW, record_logits=True)
+    state = {
+        "oracle": do.DecodeOracle(host_copy(w), kc, vc, dec.max_len, gemv=cpu_oracle.gemv),
+        "tokens": toks[0].copy(),
+        "logits": [l.cpu().numpy()[0] for l in logits],
+        "prev": int(first[0]),
+        "next": 0,
+        "stats": [],
+    }
+    del dec, w
+    torch.cuda.empty_cache()
+    return state
 
+
+@pytest.mark.parametrize("chunk", range(FULL_NEW // CHUNK))
+def test_full_granite_128_steps_vs_oracle(full_run, chunk):
+    """All 128 greedy steps of the full granite-3B-shaped decode, CHUNK steps per test (run
+    in order), each step's logits against the oracle; the per-step rel/cos are printed."""
+    st = full_run
+    assert st["next"] == chunk * CHUNK, "chunks run in order"
+    for i in range(chunk * CHUNK, (chunk + 1) * CHUNK):
+        ref = st["oracle"].step([st["prev"]], [FULL_CTX + i])[0]
+        rel, cos = check_step(st["logits"][i], ref, int(st["tokens"][i]))
+        st["stats"].append((rel, cos))
+        st["prev"] = int(st["tokens"][i])
+        st["next"] = i + 1
+    rels = [r for r, _ in st["stats"][chunk * CHUNK:]]
+    coss = [c for _, c in st["stats"][chunk * CHUNK:]]
+    print(f"steps {chunk * CHUNK}..{(chunk + 1) * CHUNK - 1}: max rel {max(rels):.3e}, "
+          f"min cos {min(coss):.9f}")
+
+
+# ------------------------------------------------------------------ fusions, graphs, policies
 
 @pytest.mark.parametrize("ctx", [300, 2100])
 def test_fused_attn_o_equals_unfused(dev, apath, ctx):
@@ -108,12 +163,13 @@ def test_fused_attn_o_equals_unfused(dev, apath, ctx):
     bit-identical logits as attention merging on its own at the same split count."""
     cfg = GraniteConfig(n_layers=2)
     w = GraniteWeights.synthetic(cfg, seed=41, device=dev)
-    n_split = ops.gqa_decode_records_splits(1, cfg.n_q, cfg.n_kv, ctx + 64)
-    assert 1 <= n_split <= ops.gqa_decode_splits(1, cfg.n_q, cfg.n_kv, ctx + 64)
+    pol = ops.current_policy()
+    n_split = ops.gqa_decode_records_splits(1, cfg.n_q, cfg.n_kv, ctx + 64, policy=pol)
+    assert 1 <= n_split <= ops.gqa_decode_splits(1, cfg.n_q, cfg.n_kv, ctx + 64, policy=pol)
     out = []
     for fused in (True, False):   # the same split count on both paths
         dec = GraniteDecoder(w, max_batch=1, max_len=ctx + 64, device=dev, fused_attn_o=fused,
-                             attn_splits=n_split)
+                             attn_splits=n_split, policy=pol)
         assert dec.fuses_attn_o(1, n_split) == fused
         dec.seed_cache(ctx, seed=42)
         out.append(dec.generate([77], [ctx], 3, record_logits=True))
@@ -123,12 +179,11 @@ def test_fused_attn_o_equals_unfused(dev, apath, ctx):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_graph_equals_eager(dev, kpath, fused):
+def test_graph_equals_eager(dev, kpath):
     """A graph replay computes bit-identical logits to the eager step."""
     cfg = GraniteConfig(n_layers=2)
     w = GraniteWeights.synthetic(cfg, seed=21, device=dev)
-    dec = GraniteDecoder(w, max_batch=1, max_len=320, device=dev, fused_tail=fused)
+    dec = GraniteDecoder(w, max_batch=1, max_len=320, device=dev, policy=ops.current_policy())
     dec.seed_cache(300, seed=22)
     snap_k = [t.clone() for t in dec.k_cache]
     snap_v = [t.clone() for t in dec.v_cache]
@@ -138,3 +193,78 @@ def test_graph_equals_eager(dev, kpath, fused):
     e0 = dec.step([123], [300]).clone()
     e1 = dec.step([int(toks[0, 0])], [301]).clone()
     assert torch.equal(e0, logits[0]) and torch.equal(e1, logits[1])
+
+
+def test_two_decoders_keep_their_policies(dev):
+    """Two decoders with different launch policies in one process, stepped alternately, each
+    reproduce bit for bit what they compute alone: the library holds no policy state."""
+    cfg = GraniteConfig(n_layers=2)
+    w = GraniteWeights.synthetic(cfg, seed=51, device=dev)
+    pols = (ops.Policy(), ops.Policy(rowblock=0, attn_mfma=0, gemv_ksplit=2))
+
+    def decoder(p):
+        d = GraniteDecoder(w, max_batch=1, max_len=384, device=dev, policy=p)
+        d.seed_cache(300, seed=52)
+        return d
+
+    alone = []
+    for p in pols:
+        d = decoder(p)
+        alone.append([d.step([9 + i], [300 + i]).clone() for i in range(3)])
+    a, b = decoder(pols[0]), decoder(pols[1])
+    for i in range(3):
+        la = a.step([9 + i], [300 + i]).clone()
+        lb = b.step([9 + i], [300 + i]).clone()
+        assert torch.equal(la, alone[0][i]) and torch.equal(lb, alone[1][i])
+    # the two policies really take different kernels (same answer to the tolerance only)
+    assert not torch.equal(alone[0][0], alone[1][0])
+    rel, cos = qo.metrics(alone[0][2].cpu().numpy(), alone[1][2].cpu().numpy())
+    assert rel < REL and cos >= COS
+
+
+# ------------------------------------------------------------------ a real-layout file
+
+def test_decode_from_q4nx_file(dev, tmp_path):
+    """A granite-layout .q4nx file (q4 projections and lm_head stored as [tiles, 5120] the
+    way granite's file stores them, bf16 norms and embed_tokens) written with write_q4nx,
+    loaded through GraniteWeights.from_q4nx and decoded, against the oracle on the same
+    bytes; then the same file without embed_tokens (tied) and with a q8 lm_head."""
+    cfg = GraniteConfig(n_layers=2, vocab=4096)
+    rng = np.random.default_rng(61)
+    hid, inter, q, kv = cfg.hidden, cfg.inter, cfg.q_dim, cfg.kv_dim
+    t = {}
+    for li in range(cfg.n_layers):
+        p = f"model.layers.{li}."
+        for name, (n, k) in (("self_attn.q_proj", (q, hid)), ("self_attn.k_proj", (kv, hid)),
+                             ("self_attn.v_proj", (kv, hid)), ("self_attn.o_proj", (hid, q)),
+                             ("mlp.gate_proj", (inter, hid)), ("mlp.up_proj", (inter, hid)),
+                             ("mlp.down_proj", (hid, inter))):
+            t[p + name + ".weight"] = ("q4", synth.q4_tiles(rng, n, k).reshape(-1, 5120))
+        t[p + "input_layernorm.weight"] = synth.f32_to_bf16_bits(
+            1 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+        t[p + "post_attention_layernorm.weight"] = synth.f32_to_bf16_bits(
+            1 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+    t["model.norm.weight"] = synth.f32_to_bf16_bits(1 + 0.1 * rng.standard_normal(hid).astype(np.float32))
+    t["lm_head.weight"] = ("q4", synth.q4_tiles(rng, cfg.vocab, hid).reshape(-1, 5120))
+    t["model.embed_tokens.weight"] = synth.random_bf16(rng, (cfg.vocab, hid))
+    path = tmp_path / "granite2.q4nx"
+    q4nx.write_q4nx(path, t)
+    w = GraniteWeights.from_q4nx(path, cfg, device=dev)
+    assert w.lm_head_kind == "q4" and w.embed is not None
+    assert np.array_equal(host_bits(w.embed), t["model.embed_tokens.weight"])
+    assert np.array_equal(w.layers[1]["down"].cpu().numpy(), t["model.layers.1.mlp.down_proj.weight"][1].reshape(-1))
+    run_and_check(w, 1, 200, 4)
+    # tied embeddings (no embed_tokens), and a q8 lm_head
+    del t["model.embed_tokens.weight"]
+    t["lm_head.weight"] = ("q8", synth.q8_tiles(rng, cfg.vocab, hid).reshape(-1, 8704))
+    path2 = tmp_path / "granite2_tied_q8.q4nx"
+    q4nx.write_q4nx(path2, t)
+    w2 = GraniteWeights.from_q4nx(path2, cfg, device=dev)
+    assert w2.lm_head_kind == "q8" and w2.embed is None
+    run_and_check(w2, 1, 200, 3)
+    # a stored shape that disagrees with the config is refused (a k-shaped q_proj; gate and
+    # down cannot be told apart this way, both are 2560 tiles: granite_gemv.py:11-16)
+    t["model.layers.0.self_attn.q_proj.weight"] = ("q4", synth.q4_tiles(rng, kv, hid).reshape(-1, 5120))
+    q4nx.write_q4nx(tmp_path / "bad.q4nx", t)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        GraniteWeights.from_q4nx(tmp_path / "bad.q4nx", cfg, device=dev)

@@ -123,12 +123,9 @@ def test_gemm_ksplit_deterministic(dev, parts, m):
     w = _dev_u8(raw, dev)
     x = synth.random_bf16(rng, (m, k))
     xd = _dev_bf16(x, dev)
-    ops.set_gemm_ksplit(parts)
-    try:
-        y1 = ops.gemm(w, "q4", xd, n // 32, k // 256).cpu().numpy()
-        y2 = ops.gemm(w, "q4", xd, n // 32, k // 256).cpu().numpy()
-    finally:
-        ops.set_gemm_ksplit(0)
+    pol = ops.Policy(gemm_ksplit=parts)
+    y1 = ops.gemm(w, "q4", xd, n // 32, k // 256, policy=pol).cpu().numpy()
+    y2 = ops.gemm(w, "q4", xd, n // 32, k // 256, policy=pol).cpu().numpy()
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
     ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
     _check_rows(y1, ref)

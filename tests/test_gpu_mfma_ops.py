@@ -1,4 +1,4 @@
-"""The GEMV and fused entry points on their matrix-core path (q4nx_set_mfma_rows): RMSNorm
+"""The GEMV and fused entry points on their matrix-core path (policy mfma_rows): RMSNorm
 prologue from the producer's sums of squares, the plain epilogue (residual, sums of squares,
 argmax keys), [gate, up, SwiGLU] and [q, k, v, RoPE + cache append], for batches inside and
 beyond the VALU kernel's 8 rows.
@@ -46,17 +46,17 @@ def assert_bf16_close(got_bits, ref_f64, max_frac=1e-3):
     assert (diff > 0).mean() <= max_frac, float((diff > 0).mean())
 
 
-def ssq32(y):
+def ssq16(y):
     y = np.asarray(y, np.float64)
-    return (y.reshape(y.shape[0], -1, 32) ** 2).sum(-1)
+    return (y.reshape(y.shape[0], -1, 16) ** 2).sum(-1)
 
 
 def normed_input(rng, batch, k, dev, scale=20.0):
-    """fp32 residual rows, their per-32 sums of squares, bf16 norm weights, and the oracle's
+    """fp32 residual rows, their per-16 sums of squares, bf16 norm weights, and the oracle's
     normalised input (float64, before the bf16 rounding)."""
     h = (rng.standard_normal((batch, k)) * scale).astype(np.float32)
     nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(k).astype(np.float32))
-    return (torch.from_numpy(h).to(dev), torch.from_numpy(ssq32(h).astype(np.float32)).to(dev),
+    return (torch.from_numpy(h).to(dev), torch.from_numpy(ssq16(h).astype(np.float32)).to(dev),
             bf16_dev(nw, dev), do.rmsnorm(h, nw, 1e-5))
 
 
@@ -97,19 +97,19 @@ def test_mfma_gemv_ex_norm_ssq_keys(dev, mfma, kind, batch):
     w = torch.from_numpy(raw.reshape(-1)).to(dev)
     hd, ss_in, nwd, x64 = normed_input(rng, batch, k, dev)
     res = rng.standard_normal((batch, n)).astype(np.float32)
-    ss_out = torch.empty((batch, n // 32), dtype=torch.float32, device=dev)
-    keys = torch.zeros((batch, n // 32), dtype=torch.int64, device=dev)
+    ss_out = torch.empty((batch, n // 16), dtype=torch.float32, device=dev)
+    keys = torch.zeros((batch, n // 16), dtype=torch.int64, device=dev)
     y = ops.gemv_ex(w, kind, hd, n // 32, k // 256, norm_w=nwd, eps=1e-5,
                     residual=torch.from_numpy(res).to(dev), ssq_in=ss_in, ssq_out=ss_out,
                     argmax_keys=keys).cpu().numpy()
     assert_close_norm(y, raw, kind, x64, n // 32, k // 256, res)
-    sref = ssq32(y)
+    sref = ssq16(y)
     assert np.abs(ss_out.cpu().numpy() - sref).max() <= 1e-6 * sref.max()
     tok = torch.zeros(batch, dtype=torch.int32, device=dev)
     pos = torch.zeros(batch, dtype=torch.int32, device=dev)
     lens = torch.zeros(batch, dtype=torch.int32, device=dev)
     step = torch.zeros(1, dtype=torch.int32, device=dev)
-    ops.decode_advance(keys, n // 32, tok, pos, lens, step)
+    ops.decode_advance(keys, n // 16, tok, pos, lens, step)
     assert tok.cpu().numpy().tolist() == np.argmax(y, axis=1).tolist()
 
 
@@ -120,13 +120,13 @@ def test_mfma_gemv_plain_keys_only(dev, mfma, batch):
     n, k = 4096, 1024
     raw = synth.q8_tiles(rng, n, k).reshape(-1, 8704)
     x = synth.random_bf16(rng, (batch, k))
-    keys = torch.zeros((batch, n // 32), dtype=torch.int64, device=dev)
+    keys = torch.zeros((batch, n // 16), dtype=torch.int64, device=dev)
     ops.gemv_ex(torch.from_numpy(raw.reshape(-1)).to(dev), "q8", bf16_dev(x, dev), n // 32,
                 k // 256, argmax_keys=keys, want_y=False)
     ref = qo.gemv(raw, "q8", x, n // 32, k // 256, acc=np.float64).reshape(batch, n)
     tok = torch.zeros(batch, dtype=torch.int32, device=dev)
     z = lambda: torch.zeros(batch, dtype=torch.int32, device=dev)
-    ops.decode_advance(keys, n // 32, tok, z(), z(), torch.zeros(1, dtype=torch.int32, device=dev))
+    ops.decode_advance(keys, n // 16, tok, z(), z(), torch.zeros(1, dtype=torch.int32, device=dev))
     got = tok.cpu().numpy()
     for b in range(batch):
         top = np.sort(ref[b])[-2:]
@@ -217,14 +217,11 @@ def test_mfma_and_valu_agree(dev):
     x = synth.random_bf16(rng, (3, hid))
     d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
     outs = {}
-    try:
-        for path, rows in (("valu", 0), ("mfma", 1)):
-            ops.set_mfma_rows("q4", rows)
-            raw = torch.empty((3, 2 * inter), dtype=torch.float32, device=dev)
-            h = ops.gate_up_swiglu(d(wg), d(wu), inter // 32, kt, bf16_dev(x, dev), raw_out=raw)
-            outs[path] = (raw.cpu().numpy(), bits(h))
-    finally:
-        ops.set_mfma_rows("q4", 2)
+    for path, rows in (("valu", 0), ("mfma", 1)):
+        raw = torch.empty((3, 2 * inter), dtype=torch.float32, device=dev)
+        h = ops.gate_up_swiglu(d(wg), d(wu), inter // 32, kt, bf16_dev(x, dev), raw_out=raw,
+                               policy=ops.Policy(mfma_rows_q4=rows))
+        outs[path] = (raw.cpu().numpy(), bits(h))
     ref = np.concatenate([qo.gemv(wg, "q4", x, inter // 32, kt, acc=np.float64),
                           qo.gemv(wu, "q4", x, inter // 32, kt, acc=np.float64)], axis=1)
     for path, (raw_np, hb) in outs.items():   # each path's epilogue on its own accumulators

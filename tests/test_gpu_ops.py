@@ -131,17 +131,17 @@ def test_swiglu(dev, in_f32):
 # ------------------------------------------------------------------ fused [q,k,v,RoPE]
 
 @pytest.fixture
-def ksplit(request):
-    """Force the GEMV K-split (0 = automatic) for one test, then restore automatic."""
-    ops.set_gemv_ksplit(request.param)
-    yield request.param
-    ops.set_gemv_ksplit(0)
+def ksplit(request, vpath):
+    """Force the general GEMV's K-split (0 = automatic) for one test on top of its VALU
+    kernel family."""
+    with ops.policy_scope(ops.current_policy().replace(gemv_ksplit=request.param)):
+        yield request.param
 
 
 @pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (1, True, 0), (3, True, 0),
                                                (3, True, 1), (2, True, 8)],
                          indirect=["ksplit"])
-def test_qkv_rope(dev, valu, batch, norm, ksplit):
+def test_qkv_rope(dev, vpath, batch, norm, ksplit):
     rng = np.random.default_rng(13)
     hq, hkv, hid, lmax = 40, 8, 2560, 512
     kt = hid // 256
@@ -194,8 +194,8 @@ def test_qkv_rope(dev, valu, batch, norm, ksplit):
 
 
 @pytest.mark.parametrize("batch,ksplit", [(1, 0), (3, 0), (2, 1)], indirect=["ksplit"])
-def test_qkv_rope_ssq_in(dev, valu, batch, ksplit):
-    """The norm fed the producer's per-32 sums of squares gives the same normalised input
+def test_qkv_rope_ssq_in(dev, vpath, batch, ksplit):
+    """The norm fed the producer's per-16 sums of squares gives the same normalised input
     (to bf16 rounding) and GEMV outputs as the oracle on that input."""
     rng = np.random.default_rng(23)
     hq, hkv, hid, lmax = 40, 8, 2560, 128
@@ -211,7 +211,7 @@ def test_qkv_rope_ssq_in(dev, valu, batch, ksplit):
     xn = torch.empty((batch, hid), dtype=torch.bfloat16, device=dev)
     nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(hid).astype(np.float32))
     h = (rng.standard_normal((batch, hid)) * 20).astype(np.float32)
-    ss = torch.from_numpy(ssq32(h).astype(np.float32)).to(dev)
+    ss = torch.from_numpy(ssq16(h).astype(np.float32)).to(dev)
     d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
     ops.qkv_rope(d(wq), d(wk), d(wv), hq, hkv, kt, torch.from_numpy(h).to(dev),
                  torch.from_numpy(pos).to(dev), tab, kc, vc, norm_w=bf16_dev(nw, dev),
@@ -227,7 +227,7 @@ def test_qkv_rope_ssq_in(dev, valu, batch, ksplit):
 
 @pytest.mark.parametrize("batch,norm,ksplit", [(1, False, 0), (2, True, 0), (1, True, 2),
                                                (3, True, 5)], indirect=["ksplit"])
-def test_gate_up_swiglu(dev, valu, batch, norm, ksplit):
+def test_gate_up_swiglu(dev, vpath, batch, norm, ksplit):
     rng = np.random.default_rng(14)
     hid, inter = 2560, 8192
     kt = hid // 256
@@ -381,22 +381,34 @@ def test_gqa_decode_garbage_past_length(dev, apath):
 
 # ------------------------------------------------------------------ helpers
 
-def ssq32(y):
-    """float64 sums of squares over consecutive 32 entries of each row."""
+def ssq16(y):
+    """float64 sums of squares over consecutive 16 entries of each row."""
     y = np.asarray(y, np.float64)
-    return (y.reshape(y.shape[0], -1, 32) ** 2).sum(-1)
+    return (y.reshape(y.shape[0], -1, 16) ** 2).sum(-1)
 
 
-def test_embed_and_argmax(dev):
+@pytest.mark.parametrize("kind", ["q8", "q4", "bf16"])
+def test_embed_and_argmax(dev, kind):
+    """Embedding rows from q8 / q4 tiles (a tied lm_head, dequantised exactly as the oracle
+    does) or a stored bf16 matrix, with their per-16 sums of squares; a token out of range
+    gives a NaN row; the device argmax takes the first maximum."""
     rng = np.random.default_rng(18)
     vocab, hid = 1024, 512
-    w = synth.q8_tiles(rng, vocab, hid).reshape(-1, 8704)
-    toks = np.array([0, 31, 32, 1023], np.int32)
-    ss = torch.empty((4, hid // 32), dtype=torch.float32, device=dev)
-    h = ops.embed_q8(torch.from_numpy(w.reshape(-1)).to(dev), torch.from_numpy(toks).to(dev),
-                     vocab, hid, ssq_out=ss).cpu().numpy()
-    assert np.array_equal(h, do.embed_rows(w, toks, vocab, hid))
-    assert_close(ss.cpu().numpy(), ssq32(h), rel=1e-6)
+    toks = np.array([0, 31, 32, 1023, 1024], np.int32)
+    if kind == "bf16":
+        table = synth.random_bf16(rng, (vocab, hid))
+        tdev = bf16_dev(table, dev)
+        want = qo.bf16_to_f32(table[toks[:4]])
+    else:
+        tiles = (synth.q8_tiles if kind == "q8" else synth.q4_tiles)(rng, vocab, hid)
+        tiles = tiles.reshape(-1, tiles.shape[-1])
+        tdev = torch.from_numpy(tiles.reshape(-1)).to(dev)
+        want = do.embed_rows(tiles, toks[:4], vocab, hid, kind)
+    ss = torch.empty((5, hid // 16), dtype=torch.float32, device=dev)
+    h = ops.embed(tdev, kind, torch.from_numpy(toks).to(dev), vocab, hid, ssq_out=ss).cpu().numpy()
+    assert np.array_equal(h[:4], want)
+    assert np.isnan(h[4]).all()
+    assert_close(ss.cpu().numpy()[:4], ssq16(h[:4]), rel=1e-6)
     logits = rng.standard_normal((3, 100352)).astype(np.float32)
     logits[1, 5000] = logits[1, 7000] = 99.0         # first maximum wins
     idx = ops.argmax(torch.from_numpy(logits).to(dev)).cpu().numpy()
@@ -415,7 +427,7 @@ def test_embed_and_argmax(dev):
 def test_attn_records_o_proj_equals_chain(dev, apath, hq, hkv, L, lmax, n_split, n_out):
     """Attention publishing split records, then the o-projection merging them in its prologue,
     gives bit for bit what attention with its own merge followed by the o-projection GEMV
-    gives (y and the per-tile-row sums of squares); the records merge to the oracle's
+    gives (y and the per-16-row sums of squares); the records merge to the oracle's
     attention output."""
     rng = np.random.default_rng(hq * 1000 + L + n_split)
     q = synth.random_bf16(rng, (1, hq, 64))
@@ -431,14 +443,14 @@ def test_attn_records_o_proj_equals_chain(dev, apath, hq, hkv, L, lmax, n_split,
 
     attn, af = ops.gqa_decode(qd, kd, vd, lens, 0.125, n_split=n_split, want_f32=True, ws=ws)
     h_c = d(h0)
-    ss_c = torch.zeros((1, nt), dtype=torch.float32, device=dev)
+    ss_c = torch.zeros((1, 2 * nt), dtype=torch.float32, device=dev)
     ops.gemv_ex(W, "q4", attn.view(1, hq * 64), nt, hq // 4, residual=h_c, out=h_c,
                 ssq_out=ss_c, ws=ws)
 
     rec = ops.gqa_decode_records(qd, kd, vd, lens, n_split, 0.125, ws=ws)
     assert rec.shape == (1, hkv, n_split, hq // hkv, 68)
     h_f = d(h0)
-    ss_f = torch.zeros((1, nt), dtype=torch.float32, device=dev)
+    ss_f = torch.zeros((1, 2 * nt), dtype=torch.float32, device=dev)
     ops.gemv_attn_q4(W, nt, rec, residual=h_f, out=h_f, ssq_out=ss_f)
     torch.cuda.synchronize()
     assert np.array_equal(h_f.cpu().numpy().view(np.uint32), h_c.cpu().numpy().view(np.uint32))
@@ -475,70 +487,6 @@ def test_attn_records_o_proj_rejects(dev):
     rec = torch.zeros((1, 8, 19, 5, 68), dtype=torch.float32, device=dev)
     with pytest.raises(Q4NXError, match="n_split"):
         ops.gemv_attn_q4(W, 8, rec)               # 19 splits: more than the merge holds
-
-
-# ------------------------------------------------------------------ fused layer tail
-
-@pytest.mark.parametrize("batch", [1, 3])
-def test_layer_tail_equals_chain(dev, valu, batch):
-    """o-proj -> RMSNorm/[gate,up,SwiGLU] -> down in one three-stage launch gives bit for bit
-    what the three separate launches give with the same K splits (1, 2 and 4 parts with
-    10-wave workgroups up to batch 2; 2, 3 and 4 with 8 waves above), and the chain
-    agrees with the float64 oracle run on the kernel's own intermediates."""
-    parts = (1, 2, 4) if batch <= 2 else (2, 3, 4)
-    rng = np.random.default_rng(31 + batch)
-    hid, qd, inter = 2560, 2560, 8192
-    wo = synth.q4_tiles(rng, hid, qd).reshape(-1)
-    wg = synth.q4_tiles(rng, inter, hid).reshape(-1)
-    wu = synth.q4_tiles(rng, inter, hid).reshape(-1)
-    wd = synth.q4_tiles(rng, hid, inter).reshape(-1)
-    attn = synth.random_bf16(rng, (batch, qd))
-    h0 = (rng.standard_normal((batch, hid)) * 3).astype(np.float32)
-    nw = synth.f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(hid).astype(np.float32))
-    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    W = [d(x) for x in (wo, wg, wu, wd)]
-    ad, nwd = bf16_dev(attn, dev), bf16_dev(nw, dev)
-    ws = ops.Workspace(16 << 20, device=dev)
-
-    h_f, ss_f = d(h0), torch.zeros((batch, hid // 32), dtype=torch.float32, device=dev)
-    mlp_f = torch.zeros((batch, inter), dtype=torch.bfloat16, device=dev)
-    ops.layer_tail(*W, hid, qd, inter, ad, h_f, ss_f, nwd, 1e-5, mlp_f, ws=ws)
-    ops.ws_check(ws)
-
-    h_c, ss_c = d(h0), torch.zeros((batch, hid // 32), dtype=torch.float32, device=dev)
-    try:
-        ops.set_gemv_ksplit(parts[0])
-        ops.gemv_ex(W[0], "q4", ad, hid // 32, qd // 256, residual=h_c, out=h_c, ssq_out=ss_c,
-                    ws=ws)
-        h1 = h_c.cpu().numpy().copy()
-        ops.set_gemv_ksplit(parts[1])
-        mlp_c = ops.gate_up_swiglu(W[1], W[2], inter // 32, hid // 256, h_c, norm_w=nwd,
-                                   eps=1e-5, ws=ws, ssq_in=ss_c)
-        ops.set_gemv_ksplit(parts[2])
-        ops.gemv_ex(W[3], "q4", mlp_c, hid // 32, inter // 256, residual=h_c, out=h_c,
-                    ssq_out=ss_c, ws=ws)
-    finally:
-        ops.set_gemv_ksplit(0)
-    assert np.array_equal(bits(mlp_f), bits(mlp_c))
-    assert np.array_equal(h_f.cpu().numpy().view(np.uint32), h_c.cpu().numpy().view(np.uint32))
-    assert np.array_equal(ss_f.cpu().numpy().view(np.uint32), ss_c.cpu().numpy().view(np.uint32))
-    # the chain itself, stage by stage, against the oracle on its own inputs
-    ref1 = h0 + qo.gemv(wo.reshape(-1, 5120), "q4", attn, hid // 32, qd // 256,
-                        acc=np.float64).reshape(batch, hid)
-    assert_close(h1, ref1)
-    mlp_bits = bits(mlp_f)
-    ref2 = qo.gemv(wd.reshape(-1, 5120), "q4", mlp_bits, hid // 32, inter // 256,
-                   acc=np.float64).reshape(batch, hid)
-    # the down GEMV's own output (the residual add is one more fp32 rounding of h)
-    assert_close(h_f.cpu().numpy().astype(np.float64) - h1, ref2)
-    xn = do.rmsnorm(h1, nw, 1e-5)
-    g = qo.gemv(wg.reshape(-1, 5120), "q4", qo.bf16_round(xn.astype(np.float32)), inter // 32,
-                hid // 256, acc=np.float64).reshape(batch, inter)
-    u = qo.gemv(wu.reshape(-1, 5120), "q4", qo.bf16_round(xn.astype(np.float32)), inter // 32,
-                hid // 256, acc=np.float64).reshape(batch, inter)
-    r = qo.bf16_to_f32(mlp_bits).astype(np.float64)
-    ref_m = do.swiglu_from_raw(g, u)
-    assert qo.metrics(r, ref_m)[1] > 0.9999      # xn may differ from the kernel's by 1 ulp
 
 
 @pytest.mark.parametrize("case", range(8))
