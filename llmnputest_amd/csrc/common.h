@@ -197,16 +197,23 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // RMSNorm from the producer's sums of squares: a row of x has n = K/16 partial sums (one per
-// 16 entries); lane l holds entries l, l + 64, l + 128, ... (loaded clamped into sq) and adds
-// them in that order, and wave_sum of the lane sums is the row's total. Every consumer of the
-// sums uses this order, so all kernel families normalise with the same bits.
+// 16 entries; n is a multiple of 16 and the row 16-byte aligned). Lane l loads the float4s
+// at entries 4(l + 64j), j < NQ (one load instruction each, so the 64 lanes of a wave touch
+// each line of the row once), and adds them as (s.x + s.y) + (s.z + s.w) in j order;
+// wave_sum of the lane sums is the row's total. Every consumer of the sums uses this order,
+// so all kernel families normalise with the same bits.
 constexpr int kSsqRows = 16;   // entries per partial sum of squares
-template <int NSS>
-__device__ __forceinline__ float ssq_lane_sum(const float (&sq)[NSS], int lane, int n) {
+template <int NQ>
+__device__ __forceinline__ void ssq_load(const float* row, int lane, int n, float4 (&q)[NQ]) {
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) q[j] = *(const float4*)(row + min(4 * (lane + 64 * j), n - 4));
+}
+template <int NQ>
+__device__ __forceinline__ float ssq_lane_sum(const float4 (&q)[NQ], int lane, int n) {
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < NSS; ++j)
-    if (lane + 64 * j < n) s += sq[j];
+  for (int j = 0; j < NQ; ++j)
+    if (4 * (lane + 64 * j) < n) s += (q[j].x + q[j].y) + (q[j].z + q[j].w);
   return s;
 }
 

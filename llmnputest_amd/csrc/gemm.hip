@@ -423,10 +423,9 @@ __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h,
     }
   }
   const float* srow = ssq + (int64_t)m * n_ss;
-  float sq[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) sq[j] = srow[min(l + 64 * j, n_ss - 1)];
-  const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<8>(sq, l, n_ss)) / (float)K + eps);
+  float4 sq[2];   // n_ss <= 512
+  ssq_load<2>(srow, l, n_ss, sq);
+  const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<2>(sq, l, n_ss)) / (float)K + eps);
   uint16_t* xr = xn + (int64_t)m * xn_stride;
 #pragma unroll
   for (int i = 0; i < kMaxChunks; ++i) {

@@ -178,8 +178,8 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   uint4 nw[TPW];
   const bool pre_ssq = norm && a.ssq_in != nullptr;
   const int n_ss = K / kSsqRows;
-  constexpr int kSsqLoads = 8;   // K / 16 <= 512 partial sums per row
-  float sq[B][kSsqLoads];
+  constexpr int kSsqLoads = 2;   // float4s per lane: K / 16 <= 512 partial sums per row
+  float4 sq[B][kSsqLoads];
   constexpr int kSsqIt = 3;
   float4 hs[B][kSsqIt];
   const bool split_norm = norm && ks > 1 && !pre_ssq;
@@ -206,9 +206,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
     if (pre_ssq) {
 #pragma unroll
       for (int b = 0; b < B; ++b)
-#pragma unroll
-        for (int j = 0; j < kSsqLoads; ++j)
-          sq[b][j] = a.ssq_in[min(b, a.batch - 1) * n_ss + min(lane + 64 * j, n_ss - 1)];
+        ssq_load<kSsqLoads>(a.ssq_in + (size_t)min(b, a.batch - 1) * n_ss, lane, n_ss, sq[b]);
     }
     // with K split and no partials given, this workgroup's tiles see only part of the row:
     // the sum of squares reads the whole row (strided over all threads; three float4 per
@@ -282,11 +280,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 #pragma unroll
     for (int b = 0; b < B; ++b)
 #pragma unroll
-      for (int j = 0; j < kSsqLoads; j += 4) {
-        float4 v = make_float4(sq[b][j], sq[b][j + 1], sq[b][j + 2], sq[b][j + 3]);
-        pin(v);
-        sq[b][j] = v.x; sq[b][j + 1] = v.y; sq[b][j + 2] = v.z; sq[b][j + 3] = v.w;
-      }
+      for (int j = 0; j < kSsqLoads; ++j) pin(sq[b][j]);
   }
 
   uint4 xr[B][TPW];       // 8 bf16 per lane per tile
@@ -809,8 +803,8 @@ static int check_x(const void* x, int64_t x_stride, int k_tiles, const char* wha
 
 static int check_ssq_in(const float* ssq_in, const uint16_t* norm_w, int k_tiles,
                         const char* what) {
-  Q4NX_REQUIRE(ssq_in == nullptr || (norm_w != nullptr && Q4NX_ALIGNED(ssq_in, 4)),
-               Q4NX_ERR_ARG, "%s: ssq_in goes with norm_w (4-byte aligned)", what);
+  Q4NX_REQUIRE(ssq_in == nullptr || (norm_w != nullptr && Q4NX_ALIGNED(ssq_in, 16)),
+               Q4NX_ERR_ARG, "%s: ssq_in goes with norm_w (16-byte aligned)", what);
   Q4NX_REQUIRE(ssq_in == nullptr || k_tiles <= 32, Q4NX_ERR_SHAPE,
                "%s: ssq_in supports K <= 8192, K=%d", what, k_tiles * 256);
   return Q4NX_OK;

