@@ -447,8 +447,10 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     ap.add_argument("--only", default=None, metavar="GROUPS",
-                    help="profiling: only these comma-separated secondary groups (" +
-                         ",".join(SECONDARY_GROUPS) + "); prints their JSON and exits")
+                    help="profiling: only these comma-separated groups (" +
+                         ",".join(SECONDARY_GROUPS + ("decode",)) +
+                         "; decode: the batch-1 decode at --ctx / --new-tokens); prints their "
+                         "JSON and exits")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -466,11 +468,20 @@ def main() -> int:
         return copy_calibration(a.calibrate_copy, 10, dev)
     if a.only:
         groups = tuple(g for g in a.only.split(",") if g)
-        bad = [g for g in groups if g not in SECONDARY_GROUPS]
+        bad = [g for g in groups if g not in SECONDARY_GROUPS + ("decode",)]
         if bad:
-            print(f"unknown groups {bad}; choose from {SECONDARY_GROUPS}", file=sys.stderr)
+            print(f"unknown groups {bad}; choose from {SECONDARY_GROUPS + ('decode',)}",
+                  file=sys.stderr)
             return 2
-        print(json.dumps({"other_shapes": secondary_bench(dev, groups)}), flush=True)
+        out = {}
+        if "decode" in groups:
+            d = decode_bench(a.ctx, a.new_tokens, dev, 0)
+            d.pop("weights")
+            out["decode"] = d
+        sec = tuple(g for g in groups if g != "decode")
+        if sec:
+            out["other_shapes"] = secondary_bench(dev, sec)
+        print(json.dumps(out), flush=True)
         return 0
 
     r = gemv_bench(a.steps, a.warmup, a.rot, dev)
