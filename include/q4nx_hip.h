@@ -52,6 +52,9 @@ extern "C" {
 
 /* Size of the counter region at the start of every workspace (16384 counters). */
 #define Q4NX_WS_COUNTER_BYTES 65536
+/* q4nx_gqa_decode_static's library-owned scratch per GPU: the counter region and 8 MiB
+ * of split records. */
+#define Q4NX_STATIC_SCRATCH_BYTES (Q4NX_WS_COUNTER_BYTES + (8 << 20))
 
 int q4nx_abi_version(void);
 /* Message of the last error on this thread ("" if none). */
@@ -240,6 +243,23 @@ int q4nx_gqa_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *
  * shape or policy. */
 int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len,
                            const q4nx_policy *policy);
+/* q4nx_gqa_decode without a workspace argument: it allocates nothing. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The arrival counters and
+ * split records live in a library-owned device array of Q4NX_STATIC_SCRATCH_BYTES per GPU
+ * (the workspace layout: counters, then records), held until the process ends. The loader
+ * zero-fills it and every call leaves the counters at zero. The first call on a device
+ * (made with it current, outside graph capture) looks up that device's copy of the array.
+ * A call whose records would not fit (Q4NX_WS_COUNTER_BYTES + B*Hkv*n_split*(Hq/Hkv)*68*4
+ * bytes, with n_split as chosen for n_split = 0) is refused with Q4NX_ERR_WS before
+ * anything is launched. Every call on one GPU shares the array: calls ordered on one
+ * stream are safe, calls that overlap on one GPU race. Arguments, results and bits as in
+ * q4nx_gqa_decode at the same n_split and policy. */
+int q4nx_gqa_decode_static(const uint16_t *q, const uint16_t *k_cache,
+                           const uint16_t *v_cache, uint16_t *out, float *out_f32, int batch,
+                           int n_q_heads, int n_kv_heads, int head_dim, const int32_t *lens,
+                           int max_len, int64_t kv_b_stride, int64_t kv_h_stride, float scale,
+                           int n_split, const q4nx_policy *policy, void *stream);
 /* The split count to give q4nx_gqa_decode_records when q4nx_gemv_attn_q4 merges the
  * records: q4nx_gqa_decode_splits capped at 12 (every split is a record each o-projection
  * workgroup reads, so the pair runs fastest with fewer, longer splits). */

@@ -81,6 +81,8 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_gqa_decode_ws_bytes": (c_sz, [c_i, c_i, c_i, c_i, c_pol]),
     "q4nx_gqa_decode": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
                               c_i64, c_f, c_i, c_p, c_sz, c_pol, c_p]),
+    "q4nx_gqa_decode_static": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i,
+                                     c_i64, c_i64, c_f, c_i, c_pol, c_p]),
     "q4nx_gqa_decode_splits": (c_i, [c_i, c_i, c_i, c_i, c_pol]),
     "q4nx_gqa_decode_records_splits": (c_i, [c_i, c_i, c_i, c_i, c_pol]),
     "q4nx_gqa_decode_records": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,

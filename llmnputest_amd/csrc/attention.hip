@@ -22,6 +22,8 @@
 #include <atomic>
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "policy.h"
 
@@ -588,6 +590,40 @@ static size_t partial_bytes(int batch, int hkv, int n_split, int G) {
   return (size_t)batch * hkv * n_split * G * kPartStride * 4;
 }
 
+// The allocation-free attention entry point's workspace: one library-owned array per GPU,
+// laid out like a caller's workspace (arrival counters, then split records). The loader
+// zero-fills it, and every launch leaves its counters at zero again. Host code never uses
+// the array's name as an address: each device's copy is reached through the pointer that
+// hipGetSymbolAddress returned for that device.
+constexpr size_t kStaticScratchBytes = Q4NX_STATIC_SCRATCH_BYTES;
+static_assert(kStaticScratchBytes % 256 == 0, "the scratch keeps the workspace alignment");
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};   // set once per device, under g_scratch_mu
+
+// This device's copy of `scratch`, resolved on the first call made with the device current.
+static int static_scratch(void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  Q4NX_REQUIRE(e == hipSuccess, Q4NX_ERR_LAUNCH, "%s: hipGetDevice: %s", what,
+               hipGetErrorString(e));
+  Q4NX_REQUIRE(dev >= 0 && dev < kMaxDevices, Q4NX_ERR_ARG, "%s: device %d beyond %d", what, dev,
+               kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    Q4NX_REQUIRE(e == hipSuccess && p != nullptr, Q4NX_ERR_LAUNCH,
+                 "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                 hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return Q4NX_OK;
+}
+
 }  // namespace q4nx
 
 using namespace q4nx;
@@ -684,6 +720,35 @@ int q4nx_gqa_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   return attn_run(q, k_cache, v_cache, out, out_f32, batch, n_q_heads, n_kv_heads, head_dim,
                   lens, max_len, kv_b_stride, kv_h_stride, scale, n_split, ws, ws_bytes, policy,
                   stream, false, "q4nx_gqa_decode");
+}
+
+int q4nx_gqa_decode_static(const uint16_t* q, const uint16_t* k_cache,
+                           const uint16_t* v_cache, uint16_t* out, float* out_f32, int batch,
+                           int n_q_heads, int n_kv_heads, int head_dim, const int32_t* lens,
+                           int max_len, int64_t kv_b_stride, int64_t kv_h_stride, float scale,
+                           int n_split, const q4nx_policy* policy, void* stream) {
+  const char* what = "q4nx_gqa_decode_static";
+  Policy P;
+  if (int rc = resolve_policy(policy, &P, what)) return rc;
+  Q4NX_REQUIRE(batch >= 1 && n_kv_heads >= 1 && n_q_heads >= n_kv_heads &&
+                   n_q_heads % n_kv_heads == 0 && max_len >= 1 && n_split >= 0 &&
+                   n_split <= 4096,
+               Q4NX_ERR_SHAPE, "%s: batch=%d Hq=%d Hkv=%d max_len=%d n_split=%d", what, batch,
+               n_q_heads, n_kv_heads, max_len, n_split);
+  const int ns = n_split > 0 ? n_split : auto_split(batch, n_kv_heads, max_len, P.attn_mfma != 0);
+  const size_t need = ns > 1 ? (size_t)Q4NX_WS_COUNTER_BYTES +
+                                   partial_bytes(batch, n_kv_heads, ns, n_q_heads / n_kv_heads)
+                             : 0;
+  Q4NX_REQUIRE(need <= kStaticScratchBytes, Q4NX_ERR_WS,
+               "%s: %d splits of batch %d x %d kv heads need %zu bytes of split records, more "
+               "than the %zu of the static scratch (fewer splits or q4nx_gqa_decode with a "
+               "workspace)",
+               what, ns, batch, n_kv_heads, need, kStaticScratchBytes);
+  void* ws = nullptr;
+  if (int rc = static_scratch(&ws, what)) return rc;
+  return attn_run(q, k_cache, v_cache, out, out_f32, batch, n_q_heads, n_kv_heads, head_dim,
+                  lens, max_len, kv_b_stride, kv_h_stride, scale, ns, ws, kStaticScratchBytes,
+                  policy, stream, false, what);
 }
 
 int q4nx_gqa_decode_splits(int batch, int n_q_heads, int n_kv_heads, int max_len,
