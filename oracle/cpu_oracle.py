@@ -35,6 +35,8 @@ def lib():
         h.oracle_gemv.restype = C.c_int
         h.oracle_gemv.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int,
                                   C.c_void_p, C.c_int]
+        h.cpu_q8_gemv.restype = C.c_int
+        h.cpu_q8_gemv.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int]
         _lib = h
     return _lib
 
@@ -86,3 +88,21 @@ def ref_baseline_x(k: int) -> np.ndarray:
     """The reference baseline's activation, float32 (cpu_baseline.cpp:143)."""
     i = np.arange(k)
     return (((i * 37) % 101) - 50).astype(np.float32) / np.float32(50.0)
+
+
+def q8_baseline_gemv(raw: np.ndarray, x_bf16: np.ndarray, n_t: int, k_t: int,
+                     threads: int | None = None) -> np.ndarray:
+    """fp32 y = W x for one token from q8 tile bytes: the AVX2 CPU baseline
+    (cpu_q8_baseline.c, the method of designs/granite_gemv/cpu_baseline.cpp on the q8
+    tile)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    if raw.size != n_t * k_t * qo.Q8_TILE_BYTES:
+        raise ValueError("raw does not hold n_t x k_t q8 tiles")
+    x = np.ascontiguousarray(qo.bf16_to_f32(np.asarray(x_bf16)).reshape(k_t * 256),
+                             dtype=np.float32)
+    y = np.empty(n_t * 32, np.float32)
+    rc = lib().cpu_q8_gemv(raw.ctypes.data, n_t, k_t, x.ctypes.data, y.ctypes.data,
+                           threads or host_threads())
+    if rc != 0:
+        raise ValueError("cpu_q8_gemv: bad arguments")
+    return y

@@ -169,3 +169,26 @@ def test_reference_binary_live():
     w = qo.dequant_matrix(raw, "q4", n // 32, k // 256).astype(np.float64)
     y = w @ cpu_oracle.ref_baseline_x(k).astype(np.float64)
     assert np.allclose(y[:4], r["y0_3"], rtol=0, atol=1e-5)
+
+
+def test_q8_cpu_baseline_vs_oracle():
+    """The bench's AVX2 q8 CPU baseline (oracle/cpu_q8_baseline.c) against the float64 oracle
+    on the same tile bytes: signed codes (a uint8 reading flips them), scales per (row, 32-K
+    group) (a wrong group or row-block index moves rows), every thread count giving the same
+    bits (each tile-row is summed by one thread in a fixed order)."""
+    rng = np.random.default_rng(21)
+    n, k = 40 * 32, 1024
+    raw = synth.q8_tiles(rng, n, k).reshape(-1)
+    x = synth.random_bf16(rng, (k,))
+    ref = cpu_oracle.gemv(raw, "q8", x, n // 32, k // 256, threads=4)
+    y1 = cpu_oracle.q8_baseline_gemv(raw, x, n // 32, k // 256, threads=1)
+    y7 = cpu_oracle.q8_baseline_gemv(raw, x, n // 32, k // 256, threads=7)
+    assert np.array_equal(y1.view(np.uint32), y7.view(np.uint32))
+    rel, cos = qo.metrics(y1, ref)
+    assert rel < 1e-5 and cos > 0.9999999, (rel, cos)
+    # one-hot x: each output is exactly one dequantised column, summed in fp32 once per group
+    xo = np.zeros(k, np.uint16)
+    xo[300] = 0x3F80   # 1.0
+    col = qo.dequant_matrix(raw, "q8", n // 32, k // 256)[:, 300]
+    assert np.array_equal(cpu_oracle.q8_baseline_gemv(raw, xo, n // 32, k // 256, threads=3),
+                          col)
