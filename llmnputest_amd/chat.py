@@ -13,8 +13,9 @@ decoded on the device and the reference's report line is printed.
 `--hf-tiny` runs chat.py's flow itself (chat.py:36-42, 80-94): a transformers causal LM whose
 lm_head is swapped for the GPU one with `attach_lm_head` and a .q4nx file, greedy `generate`
 with the rest of the model in torch on the CPU, and the report line with the head's share
-of the wall time. Without model files the model is a small random Qwen3 and its lm_head is
-written as q8 tiles by `synth.quantize_q8`.
+of the wall time. Without model files the model is a random `Qwen3_5ForCausalLM` with
+the reference model's head (hidden 1024, vocab 248320, tied embeddings) and a few layers,
+and its lm_head is written as q8 tiles by `synth.quantize_q8`.
 """
 
 from __future__ import annotations
@@ -29,27 +30,42 @@ import torch
 MAX_NEW = 128   # chat.py:22
 
 
+def tiny_qwen35(seed: int, n_layers: int = 4):
+    """A random-weight `Qwen3_5ForCausalLM` with the reference model's head: hidden 1024,
+    vocab 248320, embeddings tied to the lm_head (reference/from_q4nx.py:140-171 builds the
+    same class from the q4nx file; no model files are available offline). Layers follow
+    Qwen3.5's pattern of three gated delta-net layers to one full-attention layer, ending on a
+    full-attention layer."""
+    import transformers
+
+    types = ["linear_attention"] * n_layers
+    for i in range(n_layers - 1, -1, -4):
+        types[i] = "full_attention"
+    cfg = transformers.Qwen3_5TextConfig(
+        vocab_size=248320, hidden_size=1024, intermediate_size=3584, num_hidden_layers=n_layers,
+        num_attention_heads=8, num_key_value_heads=2, head_dim=256, linear_num_key_heads=16,
+        linear_num_value_heads=16, linear_key_head_dim=128, linear_value_head_dim=128,
+        layer_types=types, tie_word_embeddings=True, max_position_embeddings=1024)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(seed)
+    return transformers.Qwen3_5ForCausalLM(cfg).eval()
+
+
 def hf_tiny(new_tokens: int, seed: int) -> int:
     import tempfile
-
-    import transformers
 
     from . import npu, q4nx, synth
 
     t0 = time.time()
-    cfg = transformers.Qwen3Config(vocab_size=32768, hidden_size=1024, intermediate_size=3072,
-                                   num_hidden_layers=4, num_attention_heads=16,
-                                   num_key_value_heads=8, head_dim=64, tie_word_embeddings=True,
-                                   max_position_embeddings=1024)
-    torch.manual_seed(seed)
-    model = transformers.Qwen3ForCausalLM(cfg).eval()
+    model = tiny_qwen35(seed)
+    cfg = model.config
     with tempfile.TemporaryDirectory() as d:
         path = f"{d}/model.q4nx"
         q4nx.write_q4nx(path, {"lm_head.weight": (
             "q8", synth.quantize_q8(model.lm_head.weight.detach().float().numpy()))})
         head = npu.attach_lm_head(model, q4nx.Q4NX(path))
     print(f"gpu      lm_head on the gpu, {head.n_rows} x {head.k}, q8 tiles "
-          f"(random Qwen3, {cfg.num_hidden_layers} layers, in torch on the cpu)")
+          f"(random Qwen3.5, {cfg.num_hidden_layers} layers, in torch on the cpu)")
     print(f"ready    {time.time() - t0:.1f}s\n")
     ids = torch.from_numpy(np.random.default_rng(seed).integers(0, cfg.vocab_size, (1, 16)))
     head.design.seconds = head.design.calls = head.npu_calls = 0

@@ -124,6 +124,24 @@ def dequant(tiles: torch.Tensor, kind: str, n_tile_rows: int, k_tiles: int,
 
 # ---------------------------------------------------------------- GEMV
 
+def gemv_trimmed(tiles: torch.Tensor, kind: str, x: torch.Tensor, n: int, k: int,
+                 ws: "Workspace | None" = None, policy: "Policy | None" = None) -> torch.Tensor:
+    """y = W @ x for a tensor stored padded to whole tiles (N or K not a tile multiple, as
+    tools/q4nx.py:180-184 describes): x bf16 [K] or [B, K] is zero-extended to the stored K
+    (the padding columns then add nothing) and the padding rows of y are dropped. Returns
+    fp32 [n] or [B, n]."""
+    n_t, k_t = -(-n // 32), -(-k // 256)
+    _dev(x, "x", torch.bfloat16)
+    if x.shape[-1] != k:
+        raise Q4NXFormatError(f"x has K={x.shape[-1]}, the tensor has K={k}")
+    if k != k_t * 256:
+        xp = torch.zeros((*x.shape[:-1], k_t * 256), dtype=torch.bfloat16, device=x.device)
+        xp[..., :k] = x
+        x = xp
+    y = gemv(tiles, kind, x.contiguous(), n_t, k_t, ws=ws, policy=policy)
+    return y[..., :n]
+
+
 def gemv(tiles: torch.Tensor, kind: str, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
          residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
          ws: Workspace | None = None, policy: Policy | None = None) -> torch.Tensor:

@@ -59,6 +59,15 @@ def tiled_shape(n: int, k: int) -> tuple[int, int]:
     return n // TILE_ROWS, k // TILE_K
 
 
+def padded_shape(n: int, k: int) -> tuple[int, int]:
+    """(tile_rows, k_tiles) that store an [N, K] tensor whose N or K need not be a tile
+    multiple: the file pads to whole tiles (N=16 is stored as 32 rows) and a reader trims
+    the padding back off (tools/q4nx.py:180-197)."""
+    if n <= 0 or k <= 0:
+        raise Q4NXFormatError(f"[{n}, {k}] is not a tensor shape")
+    return -(-n // TILE_ROWS), -(-k // TILE_K)
+
+
 def tensor_bytes(kind: str, n: int, k: int) -> int:
     tr, kt = tiled_shape(n, k)
     return tr * kt * TILE_BYTES[kind]
@@ -96,8 +105,9 @@ def projection_shape(name: str, cfg: dict) -> tuple[int, int]:
 
 def check_stored_shape(stored, n: int, k: int) -> None:
     """The config-derived factoring must reproduce the stored [tiles, tile_bytes] shape
-    (designs/granite_gemv/granite_gemv.py:282-288). A mismatch is an error here, not a skip."""
-    tr, kt = tiled_shape(n, k)
+    (designs/granite_gemv/granite_gemv.py:282-288), padding to whole tiles included. A
+    mismatch is an error here, not a skip."""
+    tr, kt = padded_shape(n, k)
     if len(stored) == 3:   # [n_t, k_t, bytes]
         ok = stored[0] == tr and stored[1] == kt and stored[2] in (Q4_TILE_BYTES, Q8_TILE_BYTES)
     elif len(stored) == 2:  # [n_t * k_t, bytes]
@@ -156,6 +166,38 @@ class Q4NX:
         kind = kind_of_tile_bytes(tile_bytes)
         b = np.frombuffer(self.raw(name), dtype=np.uint8)
         return kind, b.reshape(-1, tile_bytes)
+
+    def tensor(self, name: str, shape: tuple[int, int] | None = None, device="cuda",
+               dtype=None):
+        """The reference's `Q4NX.tensor` (tools/q4nx.py:176-197) on the GPU: a tiled tensor is
+        dequantised and un-tiled by the HIP kernels (bf16 by default, float32 if asked) and
+        `shape` = the logical (N, K) trims the tile padding; a plain tensor comes back as
+        stored (bf16 as torch.bfloat16). Returns a torch tensor on `device`."""
+        import torch
+        from . import ops
+        e = self.header[name]
+        if e["dtype"] != "I8":
+            v = self.plain(name)
+            t = torch.from_numpy(np.array(v, copy=True))
+            if e["dtype"] == "BF16":
+                t = t.view(torch.bfloat16)
+            return t.to(device)
+        kind, tiles = self.tiles(name)
+        st = e["shape"]
+        n_t, k_t = (st[0], st[1]) if len(st) == 3 else (None, None)
+        if shape is not None:
+            tr, kt = padded_shape(*shape)
+            if n_t is None:
+                n_t, k_t = tr, kt
+            if (n_t, k_t) != (tr, kt) or n_t * k_t != tiles.shape[0]:
+                raise Q4NXFormatError(f"{name}: shape {tuple(shape)} needs {tr}x{kt} tiles, "
+                                      f"the file stores {list(st)}")
+        elif n_t is None:
+            raise Q4NXFormatError(f"{name} is stored as {list(st)}: give its logical shape")
+        dev_tiles = torch.from_numpy(np.array(tiles, copy=True)).to(device)
+        w = ops.dequant(dev_tiles, kind, n_t, k_t, untile=True,
+                        out_dtype=torch.bfloat16 if dtype is None else dtype)
+        return w if shape is None else w[: shape[0], : shape[1]]
 
     def plain(self, name: str) -> np.ndarray:
         """A tensor stored as-is (embeddings, norms): bf16 comes back as raw uint16 bits."""

@@ -63,3 +63,50 @@ def test_generate_with_gpu_lm_head(dev, tmp_path):
         top = np.sort(last)[-2:]
         if top[1] - top[0] > REL * np.abs(last).max():
             assert int(seq[12 + i]) == int(np.argmax(last)), i
+
+
+def test_generate_qwen35_head_real_shape(dev, tmp_path):
+    """The reference's chat model class (Qwen3_5ForCausalLM, reference/from_q4nx.py:140-171)
+    at its real head shape, 248320 x 1024 q8 with tied embeddings (random weights, two
+    layers: a gated delta-net and a full-attention one), through `chat.tiny_qwen35`, the model
+    `chat --hf-tiny` drives. Each head call (the 8-row prompt block, then one row per step)
+    is checked against the float64 oracle on the hidden states it received, and generate
+    takes the head's argmax."""
+    pytest.importorskip("transformers")
+    from llmnputest_amd import chat
+    from oracle import cpu_oracle
+
+    n, k = 248320, 1024
+    model = chat.tiny_qwen35(seed=3, n_layers=2)
+    assert model.lm_head.weight.shape == (n, k)
+    assert model.lm_head.weight.data_ptr() == model.model.embed_tokens.weight.data_ptr()
+    tiles = synth.quantize_q8(model.lm_head.weight.detach().float().numpy())
+    path = tmp_path / "model.q4nx"
+    q4nx.write_q4nx(path, {"lm_head.weight": ("q8", tiles)})
+    head = npu.attach_lm_head(model, q4nx.Q4NX(path))
+    assert model.lm_head is head and head.n_rows == n and head.k == k
+
+    calls = []
+    head.register_forward_hook(lambda mod, args, out: calls.append((args[0].detach().clone(),
+                                                                    out.detach().clone())))
+    prompt = torch.from_numpy(np.random.default_rng(4).integers(0, n, (1, 8)))
+    new = 6
+    with torch.no_grad():
+        seq = model.generate(prompt, max_new_tokens=new, do_sample=False, pad_token_id=0)[0]
+    assert seq.shape[0] == 8 + new
+    assert len(calls) == new and head.npu_calls == new and head.cpu_calls == 0
+
+    raw = tiles.reshape(-1)
+    for i, (h, logits) in enumerate(calls):
+        hb = qo.bf16_round(h.reshape(-1, k).float().numpy())
+        ref = cpu_oracle.gemv(raw, "q8", hb, n // 32, k // 256)
+        got = logits.reshape(-1, n).float().numpy()
+        assert got.shape == ref.shape
+        for r in range(ref.shape[0]):
+            rel, cos = qo.metrics(got[r], ref[r])
+            assert rel < REL and cos > 0.9999999, (i, r, rel, cos)
+        last = ref[-1]
+        assert int(seq[8 + i]) == int(np.argmax(got[-1]))
+        top = np.sort(last)[-2:]
+        if top[1] - top[0] > REL * np.abs(last).max():
+            assert int(seq[8 + i]) == int(np.argmax(last)), i

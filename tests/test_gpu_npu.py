@@ -85,3 +85,33 @@ def test_attach_lm_head(dev, tmp_path):
     ref = qo.gemv(w8.reshape(-1, 8704), "q8", h.view(torch.int16).numpy().view(np.uint16),
                   N // 32, K // 256, acc=np.float64)
     _rows_close(y.numpy(), ref)
+
+
+@pytest.mark.parametrize("kind,n,k", [("q4", 16, 200), ("q8", 40, 300), ("q4", 100, 2560)])
+def test_padded_tensor_trim_and_gemv(dev, tmp_path, kind, n, k):
+    """A tensor whose N or K is not a tile multiple, stored padded to whole tiles: `tensor`
+    with the logical shape returns exactly the oracle's dequantised matrix with the padding
+    trimmed (tools/q4nx.py:176-197), and `gemv_trimmed` gives W @ x of the trimmed matrix."""
+    from llmnputest_amd import ops
+    rng = np.random.default_rng(n + k)
+    n_t, k_t = q4nx.padded_shape(n, k)
+    t = synth.q4_tiles(rng, n_t * 32, k_t * 256) if kind == "q4" else synth.q8_tiles(rng, n_t * 32, k_t * 256)
+    path = tmp_path / "pad.q4nx"
+    q4nx.write_q4nx(path, {"w.weight": (kind, t)})
+    f = q4nx.Q4NX(path)
+    full = qo.dequant_matrix(t.reshape(-1), kind, n_t, k_t)
+    got32 = f.tensor("w.weight", (n, k), device=dev, dtype=torch.float32)
+    assert got32.shape == (n, k)
+    assert np.array_equal(got32.cpu().numpy(), full[:n, :k])
+    got16 = f.tensor("w.weight", (n, k), device=dev)
+    want16 = qo.bf16_round(full[:n, :k])
+    assert np.array_equal(got16.contiguous().view(torch.int16).cpu().numpy().view(np.uint16), want16)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        f.tensor("w.weight", (n + 32, k), device=dev)
+    x = synth.random_bf16(rng, (3, k))
+    y = ops.gemv_trimmed(torch.from_numpy(t.reshape(-1)).to(dev), kind,
+                         torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16), n, k)
+    assert y.shape == (3, n)
+    ref = full[:n, :k].astype(np.float64) @ qo.bf16_to_f32(x).astype(np.float64).T
+    rel, cos = qo.metrics(y.cpu().numpy(), ref.T)
+    assert rel < 1e-5 and cos > 0.9999999, (rel, cos)

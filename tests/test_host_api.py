@@ -48,6 +48,15 @@ def test_projection_shapes_and_factoring():
         q4nx.tiled_shape(2560, 1000)
     with pytest.raises(q4nx.Q4NXFormatError):
         q4nx.kind_of_tile_bytes(5121)
+    # a tensor whose N or K is not a tile multiple is stored padded to whole tiles
+    # (tools/q4nx.py:180-184): N=16 as 32 rows, K=200 as 256
+    assert q4nx.padded_shape(16, 200) == (1, 1)
+    assert q4nx.padded_shape(40, 300) == (2, 2)
+    assert q4nx.padded_shape(8192, 2560) == q4nx.tiled_shape(8192, 2560)
+    q4nx.check_stored_shape([1, 1, 5120], 16, 200)
+    q4nx.check_stored_shape([4, 8704], 40, 300)
+    with pytest.raises(q4nx.Q4NXFormatError):
+        q4nx.check_stored_shape([2, 1, 5120], 16, 200)
     q4nx.check_tile_bytes(256 * 10 * 5120, "q4", 8192, 2560)
     with pytest.raises(q4nx.Q4NXFormatError):
         q4nx.check_tile_bytes(256 * 10 * 5120 - 1, "q4", 8192, 2560)
