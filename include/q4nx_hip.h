@@ -116,7 +116,7 @@ int q4nx_gemv_q8(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
  * block an order-preserving key of (max y over its rows, first such row);
  * q4nx_decode_advance reduces them. y may be NULL when only the keys are wanted.
  * ssq_out (optional, fp32 [batch][N/16]): sum of y^2 over each 16-row block.
- * ssq_in (optional, with norm_w; fp32 [batch][K/16], K <= 8192): the same partial sums
+ * ssq_in (optional, with norm_w; fp32 [batch][K/16], K <= 8192, 16-byte aligned): the same partial sums
  * for x, as the producer of x wrote them; the prologue then adds these (in a fixed order)
  * instead of reducing x across the workgroup (the one-row kernels need them with norm_w).
  * ws as for the GEMVs above (K split when the launch has few tile-rows). No reference

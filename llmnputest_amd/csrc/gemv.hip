@@ -682,13 +682,33 @@ static int round_batch(int batch) { return batch <= 1 ? 1 : batch <= 2 ? 2 : bat
 
 // K-tiles per wave: the fewest that fit the group's K into the workgroup's wave budget
 // (16 waves for batch <= 2, 8 above); 1, 2 or 4.
-static int plan_tpw(int G, int k_t, int batch, const Policy& P) {
+// The most K-tiles per wave the automatic plan gives a wave at this batch, raising the K split
+// instead. More K-tiles per wave spill registers to scratch in the gfx950 build (four K-tiles
+// at any batch; two at 2 and 8 rows, up to 1.2 KB per lane), and the spill traffic costs more
+// than a K split's merge: gate/up 2560->8192 at 8 rows 202 us with four K-tiles per wave,
+// 113 with two, 47 with one; at 2 rows one K-tile 17.2 us against 19.9. At 4 rows two K-tiles
+// spill 12 B (q4) and measured faster than one (26.8 against 28.5 us).
+static int spill_free_tpw(int batch) {
+  const int b = round_batch(batch);
+  return b == 1 || b == 4 ? 2 : 1;
+}
+
+// K-tiles per wave for a group of G tile-rows over k_t K-tiles, at most `cap` unless the
+// policy forces a count; 0 when that does not fit one workgroup.
+static int plan_tpw(int G, int k_t, int batch, const Policy& P, int cap = 4) {
   const int max_waves = round_batch(batch) <= 2 ? kMaxWaves : kMaxWaves / 2;
   const int forced = P.gemv_tpw;
   int tpw = forced > 0 ? forced : (G * k_t + max_waves - 1) / max_waves;
   tpw = tpw <= 1 ? 1 : tpw <= 2 ? 2 : tpw <= 4 ? 4 : 0;
+  if (forced <= 0 && tpw > cap) tpw = 0;
   if (tpw && G * ((k_t + tpw - 1) / tpw) > max_waves) tpw = 0;
   return tpw;  // 0: K too long for one workgroup
+}
+
+// plan_tpw with the spill-free cap, else (K too long for it) any count that fits
+static int plan_tpw_any(int G, int k_t, int batch, const Policy& P) {
+  const int t = plan_tpw(G, k_t, batch, P, spill_free_tpw(batch));
+  return t > 0 ? t : plan_tpw(G, k_t, batch, P);
 }
 
 template <int KIND, int B, int TPW>
@@ -732,8 +752,13 @@ static size_t split_bytes(int n_groups, int G, int ks, int batch) {
 // K parts per group: plan_ksplit's choice, raised (up to 8) until one part fits in a
 // workgroup at this batch's wave budget (long K with more than two rows).
 static int plan_ksplit_fit(int n_groups, int G, int k_t, int batch, const Policy& P) {
-  int ks = plan_ksplit(n_groups, G, k_t, P);
-  while (ks < 8 && ks < k_t && plan_tpw(G, (k_t + ks - 1) / ks, batch, P) == 0) ++ks;
+  const int ks0 = plan_ksplit(n_groups, G, k_t, P);
+  int ks = ks0;
+  for (int cap : {spill_free_tpw(batch), 4}) {   // spill-free K-tiles per wave first
+    ks = ks0;
+    while (ks < 8 && ks < k_t && plan_tpw(G, (k_t + ks - 1) / ks, batch, P, cap) == 0) ++ks;
+    if (plan_tpw(G, (k_t + ks - 1) / ks, batch, P, cap) > 0) break;
+  }
   return ks;
 }
 
@@ -755,7 +780,7 @@ static int launch(int kind, GemvArgs& a, int n_groups, const Policy& P, hipStrea
     a.part_bytes = (uint32_t)(need - Q4NX_WS_COUNTER_BYTES);
   }
   const int kpp = (a.k_t + ks - 1) / ks;   // largest part
-  const int tpw = plan_tpw(a.G, kpp, a.batch, P);
+  const int tpw = plan_tpw_any(a.G, kpp, a.batch, P);
   Q4NX_REQUIRE(tpw > 0, Q4NX_ERR_SHAPE, "%s: K=%d is longer than one workgroup covers", what,
                a.k_t * 256);
   const int wm = (kpp + tpw - 1) / tpw;
