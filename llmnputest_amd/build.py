@@ -26,10 +26,13 @@ HIPCC_FLAGS = [
     "-fPIC",
     # packed fp32 VALU forms are kept out of generated code on this target
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA results in VGPRs: the epilogue reads them without v_accvgpr_read copies
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
+# MFMA results in VGPRs: the epilogues read them without v_accvgpr_read copies. The prefill
+# contraction keeps its MFMA accumulators in AGPRs instead, which leaves the VGPRs to its
+# staged operands and the separately accumulated Q4_1 minimum.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+AGPR_ACCUMULATORS: set[str] = set()
 
 
 def hipcc() -> str:
@@ -41,7 +44,8 @@ def hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     out = OBJ / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(out)]
+    extra = [] if src.name in AGPR_ACCUMULATORS else VGPR_FORM
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                      if "packed-fp32-ops" not in l and l.strip())

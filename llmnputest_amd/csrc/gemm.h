@@ -55,6 +55,12 @@ bool mfma_use(int kind, int rows, const Policy& P);
 size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows, const Policy& P);
 // whether ws_bytes holds the normalised rows an RMSNorm prologue needs on this path
 bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes);
+// The prefill kernel (gemm_pf.hip) takes plain contractions from this many rows.
+constexpr int kPrefillRows = 128;
+// whether a launch of op `op` described by `a` goes to the prefill kernel
+bool pf_use(int op, const GemmArgs& a);
+// launches `a` on the prefill kernel (whole K per workgroup, no split)
+void pf_launch(int kind, const GemmArgs& a, hipStream_t st);
 // launches `a` (all but the split-K fields filled in); returns Q4NX_OK or an error code
 int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
                 const Policy& P, hipStream_t st, const char* what);

@@ -1,0 +1,63 @@
+// q4nx tile formats as the matrix-core kernels stage and read them: per-kind tile sizes and
+// the code -> bf16 operand conversions shared by the batched (gemm.hip) and prefill
+// (gemm_pf.hip) contractions.
+#pragma once
+
+#include "common.h"
+
+namespace q4nx {
+
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
+
+template <int KIND>
+struct GemmFmt;
+template <>
+struct GemmFmt<4> {
+  static constexpr int kTile = kQ4TileBytes;
+  static constexpr int kCodes = 2 * kMetaBytes;   // codes start after d and m
+  static constexpr int kLoads = 5;                // 16-byte loads per lane per tile
+  static constexpr int kSlot = kQ4TileBytes;      // LDS bytes per staged tile
+};
+template <>
+struct GemmFmt<8> {
+  static constexpr int kTile = kQ8TileBytes;
+  static constexpr int kCodes = kMetaBytes;
+  static constexpr int kLoads = 9;                // 8704 B: the 9th load of lanes 32..63 is padding
+  static constexpr int kSlot = 9216;
+};
+
+// 8 transposed code bytes (k-slots 0..7 of one row pair) -> bf16 16 + c for the even row (low
+// nibbles) and the odd row (high nibbles).
+__device__ __forceinline__ void q4_operands(i32x2_t r, u32x4_t& ev, u32x4_t& od) {
+  const uint32_t w[2] = {(uint32_t)r.x, (uint32_t)r.y};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      // [b(2q), 0, b(2q+1), 0]
+      const uint32_t t = perm(0u, w[h], q ? 0x0C030C02u : 0x0C010C00u);
+      ev[2 * h + q] = ((t & 0x000F000Fu) << 3) | 0x41804180u;
+      od[2 * h + q] = ((t >> 1) & 0x00780078u) | 0x41804180u;
+    }
+  }
+}
+
+// 8 transposed int8 codes -> bf16 of q + 128 (exact: at most 8 significant bits); the byte
+// conversions compile to v_cvt_f32_ubyte0..3.
+__device__ __forceinline__ u32x4_t q8_operand(i32x2_t r) {
+  const uint32_t w[2] = {(uint32_t)r.x ^ 0x80808080u, (uint32_t)r.y ^ 0x80808080u};
+  u32x4_t o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t f0 = __float_as_uint((float)(w[h] & 0xFFu));
+    const uint32_t f1 = __float_as_uint((float)((w[h] >> 8) & 0xFFu));
+    const uint32_t f2 = __float_as_uint((float)((w[h] >> 16) & 0xFFu));
+    const uint32_t f3 = __float_as_uint((float)((w[h] >> 24) & 0xFFu));
+    o[2 * h] = perm(f1, f0, 0x07060302u);
+    o[2 * h + 1] = perm(f3, f2, 0x07060302u);
+  }
+  return o;
+}
+
+}  // namespace q4nx

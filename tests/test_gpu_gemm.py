@@ -159,3 +159,70 @@ def test_gemm_q8_lm_head_prefill(dev):
     ref = qo.gemv(raw[lo // 32 * k_t: hi // 32 * k_t], "q8", x, (hi - lo) // 32, k_t,
                   acc=np.float64)
     _check_rows(y[:, lo:hi], ref)
+
+
+# ------------------------------------------------------------------ prompt blocks (prefill kernel)
+# Launches of at least 512 workgroups of four tile-rows x 128 rows go to the prefill kernel
+# (scale and minimum folded into exact bf16 MFMA operands); smaller ones stay on the batched
+# kernel above.
+
+def _pf_workgroups(m, n):
+    return -(-(n // 32) // 4) * -(-m // 128)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("m,n,k", [
+    (4100, 2016, 512),   # 63 tile-rows: the last workgroup's fourth wave has none; ragged rows
+    (2048, 4096, 1024),
+])
+def test_gemm_prefill_parity(dev, kind, m, n, k):
+    """Every row against the float64 oracle at the GEMV bar."""
+    assert _pf_workgroups(m, n) >= 512
+    raw, rng = _tiles(kind, n, k, 21 + m)
+    x = synth.random_bf16(rng, (m, k))
+    y = ops.gemm(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y, ref)
+
+
+def test_gemm_prefill_long_k(dev):
+    """K = 8192 (32 tiles per wave, 256 pipelined steps): every row at the GEMV bar."""
+    m, n, k = 2048, 4096, 8192
+    raw, rng = _tiles("q4", n, k, 23)
+    x = synth.random_bf16(rng, (m, k))
+    y = ops.gemm(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y, ref)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+def test_gemm_prefill_onehot_exact(dev, kind):
+    """One-hot rows reproduce the float32 dequantised column bit for bit: hi + lo carries c d
+    (q4) or q s (q8) exactly and the minimum joins in one rounding."""
+    n, k, m = 2048, 1024, 4096
+    assert _pf_workgroups(m, n) >= 512
+    raw, _ = _tiles(kind, n, k, 3)
+    cols = np.arange(m) * 5 % k
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), cols] = 1.0
+    y = ops.gemm(_dev_u8(raw, dev), kind, _dev_bf16(qo.bf16_round(x), dev), n // 32,
+                 k // 256).cpu().numpy()
+    wm = qo.dequant_matrix(raw, kind, n // 32, k // 256)
+    assert np.array_equal(y.view(np.uint32), wm[:, cols].T.copy().view(np.uint32))
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e30])
+def test_gemm_prefill_activation_range_residual_stride(dev, scale):
+    """Extreme activation ranges, rows with a stride longer than K and a residual."""
+    m, n, k = 4096, 2048, 512
+    assert _pf_workgroups(m, n) >= 512
+    raw, rng = _tiles("q4", n, k, 14)
+    xf = rng.standard_normal((m, k + 64)).astype(np.float32) * np.float32(scale)
+    xfull = qo.bf16_round(xf)
+    xd = _dev_bf16(xfull, dev)[:, :k]
+    res = rng.standard_normal((m, n)).astype(np.float32) * np.float32(scale)
+    y = ops.gemm(_dev_u8(raw, dev), "q4", xd, n // 32, k // 256,
+                 residual=torch.from_numpy(res).to(dev)).cpu().numpy()
+    ref = qo.gemv(raw, "q4", np.ascontiguousarray(xfull[:, :k]), n // 32, k // 256,
+                  acc=np.float64) + res
+    _check_rows(y, ref)
