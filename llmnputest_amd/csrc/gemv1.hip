@@ -14,7 +14,12 @@
 //   and nothing is merged across workgroups. The two row blocks of a group go to
 //   workgroups 8 apart, which the dispatcher places on the same XCD, so the tile metadata
 //   both read is fetched into one L2. Each wave owns TPW consecutive K-tiles of one member
-//   tile-row; the waves combine once through LDS, in wave order.
+//   tile-row; the waves combine once through LDS, in wave order. [q,k,v,RoPE] has only 56
+//   groups at the 3B shape, so its workgroups own half a row block (8 rows of each member,
+//   224 workgroups): each lane still reads its 32 bytes (the sibling workgroup on the same
+//   XCD reads the same lines, from L2) and uses the half it needs — 6.2 -> 5.5 us per launch,
+//   bit-identical. The plain and gate/up launches measured slower that way (5.4 -> 6.3,
+//   9.3 -> 11.4 us: their L1 traffic doubles for CUs they already fill).
 //
 // Data path
 //   Lane l of a wave reads the 32 contiguous code bytes at rb * 2048 + 32 l of each of its
@@ -51,10 +56,11 @@ __device__ __forceinline__ unsigned long long key_max16(unsigned long long k) {
   return k;
 }
 
-template <int OP, int G, int TPW, int NSS, int XNS>
+template <int OP, int G, int TPW, int NSS, int XNS, int HB>
 __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   constexpr bool NORM = NSS > 0;
   constexpr bool XREC = XNS > 0;
+  static_assert(HB == 16 || (HB == 8 && OP == G1_QKV), "half row blocks: q/k/v only");
   __shared__ float sred[16][16];
 
   // every argument read before the weight stream, in one round of scalar loads (the empty
@@ -79,14 +85,30 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   const int WM = (k_t + TPW - 1) / TPW;   // waves per member (the launch gives G * WM)
   const int member = (G == 2 && wave >= WM) ? 1 : 0, chunk = wave - member * WM;
   const int bi = blockIdx.x;
-  int group, rb;
-  if ((n_groups & 7) == 0) {
-    group = (bi >> 4) * 8 + (bi & 7);
-    rb = (bi >> 3) & 1;
+  // HB = 16: two workgroups per group (its row blocks); HB = 8: four (the halves of each
+  // row block). A group's workgroups are 8 apart, so the dispatcher puts them on one XCD.
+  int group, rb, half = 0;
+  if constexpr (HB == 16) {
+    if ((n_groups & 7) == 0) {
+      group = (bi >> 4) * 8 + (bi & 7);
+      rb = (bi >> 3) & 1;
+    } else {
+      group = bi >> 1;
+      rb = bi & 1;
+    }
   } else {
-    group = bi >> 1;
-    rb = bi & 1;
+    int sub;
+    if ((n_groups & 7) == 0) {
+      group = (bi >> 5) * 8 + (bi & 7);
+      sub = (bi >> 3) & 3;
+    } else {
+      group = bi >> 2;
+      sub = bi & 3;
+    }
+    rb = sub >> 1;
+    half = sub & 1;
   }
+  const int r0 = rb * 16 + half * 8;   // first output row of this workgroup in the tile-row
   // member tile-row and its tensor
   int tr, seg = 0, hg = group;
   const uint8_t* wseg;
@@ -105,7 +127,8 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   const int K = k_t * kTileK;
   const int qq = lane & 7, gk = lane >> 3;
   const int k0 = gk * 32 + qq * 4;                 // this lane's first K inside a tile
-  const int mi = gk * 32 + rb * 16 + 2 * qq;       // meta index of the lane's two rows
+  // meta index of the lane's rows (two of the block for HB = 16, one of the half for HB = 8)
+  const int mi = HB == 16 ? gk * 32 + rb * 16 + 2 * qq : gk * 32 + r0 + qq;
   const int kt0 = chunk * TPW;
 
   // ---- 1. every load of the wave
@@ -164,8 +187,13 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
       const uint4* src = (const uint4*)(tile + 1024 + rb * 2048 + lane * 32);
       wq[t][0] = src[0];
       wq[t][1] = src[1];
-      md[t] = *(const uint32_t*)(tile + 2 * mi);
-      mm[t] = *(const uint32_t*)(tile + kMetaBytes + 2 * mi);
+      if constexpr (HB == 16) {
+        md[t] = *(const uint32_t*)(tile + 2 * mi);
+        mm[t] = *(const uint32_t*)(tile + kMetaBytes + 2 * mi);
+      } else {
+        md[t] = *(const uint16_t*)(tile + 2 * mi);
+        mm[t] = *(const uint16_t*)(tile + kMetaBytes + 2 * mi);
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -212,7 +240,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   float ep_c = 0.f, ep_s = 0.f;
   if constexpr (OP == G1_QKV) {
     const bool ok = ep_pos >= 0 && ep_pos < a.max_pos;
-    const float* tb = ok ? a.rope_tab + (int64_t)ep_pos * 64 + rb * 16 + er : a.rope_tab;
+    const float* tb = ok ? a.rope_tab + (int64_t)ep_pos * 64 + r0 + (er & (HB - 1)) : a.rope_tab;
     ep_c = tb[0];
     ep_s = tb[32];
   }
@@ -250,56 +278,100 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     const bool live = kt0 + t < a.k_t;
-    float pv[16], X = 0.f;
+    float X = 0.f;
+    constexpr float kC = 1048576.0f;   // undo the 2^-20 of the codes
+    if constexpr (HB == 16) {
+      float pv[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) pv[i] = 0.f;
+      for (int i = 0; i < 16; ++i) pv[i] = 0.f;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      // dwords: rows 0-7 at k, rows 8-15 at k, rows 0-7 at k+1, rows 8-15 at k+1; the low
-      // nibble of byte i is row 2i, the high nibble row 2i + 1. Both go to bits 4-7.
-      const uint4 w = wq[t][c];
-      const uint32_t Lx = (w.x << 4) & 0xF0F0F0F0u, Ly = (w.y << 4) & 0xF0F0F0F0u;
-      const uint32_t Lz = (w.z << 4) & 0xF0F0F0F0u, Lw = (w.w << 4) & 0xF0F0F0F0u;
-      const uint32_t Hx = w.x & 0xF0F0F0F0u, Hy = w.y & 0xF0F0F0F0u;
-      const uint32_t Hz = w.z & 0xF0F0F0F0u, Hw = w.w & 0xF0F0F0F0u;
-      const uint32_t xc = xp[t][c];
+      for (int c = 0; c < 2; ++c) {
+        // dwords: rows 0-7 at k, rows 8-15 at k, rows 0-7 at k+1, rows 8-15 at k+1; the low
+        // nibble of byte i is row 2i, the high nibble row 2i + 1. Both go to bits 4-7.
+        const uint4 w = wq[t][c];
+        const uint32_t Lx = (w.x << 4) & 0xF0F0F0F0u, Ly = (w.y << 4) & 0xF0F0F0F0u;
+        const uint32_t Lz = (w.z << 4) & 0xF0F0F0F0u, Lw = (w.w << 4) & 0xF0F0F0F0u;
+        const uint32_t Hx = w.x & 0xF0F0F0F0u, Hy = w.y & 0xF0F0F0F0u;
+        const uint32_t Hz = w.z & 0xF0F0F0F0u, Hw = w.w & 0xF0F0F0F0u;
+        const uint32_t xc = xp[t][c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[2 * i] = dot2(perm(Lz, Lx, sel_pair(i)), xc, pv[2 * i]);
+          pv[2 * i + 1] = dot2(perm(Hz, Hx, sel_pair(i)), xc, pv[2 * i + 1]);
+          pv[8 + 2 * i] = dot2(perm(Lw, Ly, sel_pair(i)), xc, pv[8 + 2 * i]);
+          pv[8 + 2 * i + 1] = dot2(perm(Hw, Hy, sel_pair(i)), xc, pv[8 + 2 * i + 1]);
+        }
+        X = dot2(xc, 0x3C003C00u, X);
+      }
+      // 16 rows over the 8 lanes of the K-group: lane bit 2 (half mirror), bit 1, bit 0
+      float t8[8], t4[4], r2[2];
+      const bool u2 = (lane & 4) != 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float keep = u2 ? pv[i + 8] : pv[i], send = u2 ? pv[i] : pv[i + 8];
+        t8[i] = keep + dpp<kDppHalfMirror>(send);
+      }
+      const bool u1 = (lane & 2) != 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        pv[2 * i] = dot2(perm(Lz, Lx, sel_pair(i)), xc, pv[2 * i]);
-        pv[2 * i + 1] = dot2(perm(Hz, Hx, sel_pair(i)), xc, pv[2 * i + 1]);
-        pv[8 + 2 * i] = dot2(perm(Lw, Ly, sel_pair(i)), xc, pv[8 + 2 * i]);
-        pv[8 + 2 * i + 1] = dot2(perm(Hw, Hy, sel_pair(i)), xc, pv[8 + 2 * i + 1]);
+        const float keep = u1 ? t8[i + 4] : t8[i], send = u1 ? t8[i] : t8[i + 4];
+        t4[i] = keep + dpp<kDppXor2>(send);
       }
-      X = dot2(xc, 0x3C003C00u, X);
-    }
-    // 16 rows over the 8 lanes of the K-group: lane bit 2 (half mirror), bit 1, bit 0
-    float t8[8], t4[4], r2[2];
-    const bool u2 = (lane & 4) != 0;
+      const bool u0 = (lane & 1) != 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float keep = u2 ? pv[i + 8] : pv[i], send = u2 ? pv[i] : pv[i + 8];
-      t8[i] = keep + dpp<kDppHalfMirror>(send);
-    }
-    const bool u1 = (lane & 2) != 0;
+      for (int i = 0; i < 2; ++i) {
+        const float keep = u0 ? t4[i + 2] : t4[i], send = u0 ? t4[i] : t4[i + 2];
+        r2[i] = keep + dpp<kDppXor1>(send);
+      }
+      X += dpp<kDppHalfMirror>(X);
+      X += dpp<kDppXor2>(X);
+      X += dpp<kDppXor1>(X);
+      const float c0 = fmaf(bf16lo(md[t]), r2[0] * kC, bf16lo(mm[t]) * X);
+      const float c1 = fmaf(bf16hi(md[t]), r2[1] * kC, bf16hi(mm[t]) * X);
+      acc0 += live ? c0 : 0.f;
+      acc1 += live ? c1 : 0.f;
+    } else {
+      // the 8 rows of this half: one dword at k and one at k + 1 of each 16-byte load
+      float pv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float keep = u1 ? t8[i + 4] : t8[i], send = u1 ? t8[i] : t8[i + 4];
-      t4[i] = keep + dpp<kDppXor2>(send);
-    }
-    const bool u0 = (lane & 1) != 0;
+      for (int i = 0; i < 8; ++i) pv[i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float keep = u0 ? t4[i + 2] : t4[i], send = u0 ? t4[i] : t4[i + 2];
-      r2[i] = keep + dpp<kDppXor1>(send);
+      for (int c = 0; c < 2; ++c) {
+        const uint4 w = wq[t][c];
+        const uint32_t a0 = half ? w.y : w.x, a1 = half ? w.w : w.z;
+        const uint32_t L0 = (a0 << 4) & 0xF0F0F0F0u, L1 = (a1 << 4) & 0xF0F0F0F0u;
+        const uint32_t H0 = a0 & 0xF0F0F0F0u, H1 = a1 & 0xF0F0F0F0u;
+        const uint32_t xc = xp[t][c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[2 * i] = dot2(perm(L1, L0, sel_pair(i)), xc, pv[2 * i]);
+          pv[2 * i + 1] = dot2(perm(H1, H0, sel_pair(i)), xc, pv[2 * i + 1]);
+        }
+        X = dot2(xc, 0x3C003C00u, X);
+      }
+      // 8 rows over the 8 lanes of the K-group: lane l keeps row l % 8
+      float t4[4], t2[2];
+      const bool u2 = (lane & 4) != 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float keep = u2 ? pv[i + 4] : pv[i], send = u2 ? pv[i] : pv[i + 4];
+        t4[i] = keep + dpp<kDppHalfMirror>(send);
+      }
+      const bool u1 = (lane & 2) != 0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float keep = u1 ? t4[i + 2] : t4[i], send = u1 ? t4[i] : t4[i + 2];
+        t2[i] = keep + dpp<kDppXor2>(send);
+      }
+      const bool u0 = (lane & 1) != 0;
+      const float keep = u0 ? t2[1] : t2[0], send = u0 ? t2[0] : t2[1];
+      const float r1 = keep + dpp<kDppXor1>(send);
+      X += dpp<kDppHalfMirror>(X);
+      X += dpp<kDppXor2>(X);
+      X += dpp<kDppXor1>(X);
+      const float c0 = fmaf(bf16lo(md[t]), r1 * kC, bf16lo(mm[t]) * X);
+      acc0 += live ? c0 : 0.f;
     }
-    X += dpp<kDppHalfMirror>(X);
-    X += dpp<kDppXor2>(X);
-    X += dpp<kDppXor1>(X);
-    constexpr float kC = 1048576.0f;   // undo the 2^-20 of the codes
-    const float c0 = fmaf(bf16lo(md[t]), r2[0] * kC, bf16lo(mm[t]) * X);
-    const float c1 = fmaf(bf16hi(md[t]), r2[1] * kC, bf16hi(mm[t]) * X);
-    acc0 += live ? c0 : 0.f;
-    acc1 += live ? c1 : 0.f;
   }
 
   // ---- 5. sum over the 8 K-groups (lane bits 3..5), undo the activation scale
@@ -311,20 +383,24 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
     v0 = xor32_sum(xor16_sum(v0));
     v1 = xor32_sum(xor16_sum(v1));
     if (lane < 8) {
-      sred[wave][2 * lane] = v0 * sc;
-      sred[wave][2 * lane + 1] = v1 * sc;
+      if constexpr (HB == 16) {
+        sred[wave][2 * lane] = v0 * sc;
+        sred[wave][2 * lane + 1] = v1 * sc;
+      } else {
+        sred[wave][lane] = v0 * sc;
+      }
     }
   }
   __syncthreads();
   if (tid >= 64) return;
 
-  // ---- 6. waves of each member in order; thread r < 16 holds row r of each member
+  // ---- 6. waves of each member in order; thread r < HB holds row r of each member
   float s[G];
 #pragma unroll
   for (int m = 0; m < G; ++m) {
     float v[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) v[c] = sred[min(m * WM + c, 15)][er];
+    for (int c = 0; c < 16; ++c) v[c] = sred[min(m * WM + c, 15)][er & (HB - 1)];
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 16; ++c)
@@ -358,9 +434,9 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
         a.raw_out[N + n] = s[1];
       }
     }
-  } else {   // QKV: dims d and d + 32 of one head, d = rb * 16 + r
-    if (tid < 16) {
-      const int d = rb * 16 + er;
+  } else {   // QKV: dims d and d + 32 of one head, d = r0 + r
+    if (tid < HB) {
+      const int d = r0 + er;
       const int seg_off = seg == 0 ? 0 : seg == 1 ? a.n_q_heads * 64 : (a.n_q_heads + a.n_kv_heads) * 64;
       if (a.raw_out != nullptr) {
         a.raw_out[seg_off + hg * 64 + d] = s[0];
@@ -401,9 +477,12 @@ bool gemv1_fits(int G, int k_t, bool norm) {
   return !norm || k_t * kTileK / kSsqRows <= 512;
 }
 
+// blocks: workgroups of 16-row blocks (two per group); HB = 8 launches twice as many
 template <int OP, int G, int TPW, int NSS, int XNS>
 static void go(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
-  hipLaunchKernelGGL((gemv1_kernel<OP, G, TPW, NSS, XNS>), dim3(blocks), dim3(threads), 0, s, a);
+  constexpr int HB = OP == G1_QKV ? 8 : 16;
+  hipLaunchKernelGGL((gemv1_kernel<OP, G, TPW, NSS, XNS, HB>), dim3(HB == 8 ? 2 * blocks : blocks),
+                     dim3(threads), 0, s, a);
 }
 
 template <int OP, int G, int TPW>
