@@ -29,13 +29,18 @@
 //   branch, so the weight stream starts at once.
 //
 // Arithmetic (exact products, fp32 sums)
-//   x is converted to fp16 with one power-of-two scale per wave (bf16 values are exact in
-//   fp16's range after scaling). A 4-bit code placed in bits 4-7 of an fp16 is the
+//   x is converted to fp16 with one power-of-two scale per 32-K group (bf16 values are exact
+//   in fp16's range after scaling). A 4-bit code placed in bits 4-7 of an fp16 is the
 //   subnormal c * 2^-20, and v_dot2_f32_f16 multiplies two of them by two x values exactly;
 //   one v_perm_b32 builds [c(k), c(k+1)] for a row. The 16 row sums of a lane are reduced
-//   over the 8 lanes of its K-group (bits 2, 1, 0 of the lane: 14 adds), leaving each lane
-//   two rows of one group, to which that group's scale and minimum are applied:
+//   over the 8 lanes of its K-group in three DPP steps (14 adds); each lane reads its bytes
+//   into lane-dependent register slots so that two of the steps need no selects. Each lane
+//   is left with two rows of one group, to which that group's scale and minimum are applied:
 //   y_r += d_r * sum(c x) + m_r * sum(x) (the Q4_1 factoring, granite_gemv.h:19-29).
+//
+// The kernel's time is its launch, the weight stream and the VALU work of the waves that
+// receive the last bytes, so the VALU count per K-tile is kept low: no register clears
+// before the first dot products, no per-wave cross-row max, a fixed-order wave sum.
 
 #include "common.h"
 #include "gemv1.h"
@@ -44,6 +49,22 @@ namespace q4nx {
 
 __device__ __forceinline__ constexpr uint32_t sel_pair(int i) {
   return 0x0c040c00u + (uint32_t)i * 0x00010001u;   // [s1.b_i, 0, s0.b_i, 0]
+}
+
+// a.x*b.x + a.y*b.y with no accumulator operand: the VOP3P form takes the constant 0, where
+// the accumulating VOP2 form would first need a register cleared to zero
+__device__ __forceinline__ float dot2_0(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float acc, bool first) {
+  return first ? dot2_0(a, b) : dot2(a, b, acc);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 
 // 64-bit max over aligned groups of 16 lanes (every lane of the group gets it).
@@ -61,7 +82,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   constexpr bool NORM = NSS > 0;
   constexpr bool XREC = XNS > 0;
   static_assert(HB == 16 || (HB == 8 && OP == G1_QKV), "half row blocks: q/k/v only");
-  __shared__ float sred[16][16];
+  __shared__ float sred[G][16][16];   // [member][wave of the member][row]
 
   // every argument read before the weight stream, in one round of scalar loads (the empty
   // asm consumes them all at once, so the compiler cannot spread them over dependent rounds)
@@ -127,8 +148,15 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   const int K = k_t * kTileK;
   const int qq = lane & 7, gk = lane >> 3;
   const int k0 = gk * 32 + qq * 4;                 // this lane's first K inside a tile
-  // meta index of the lane's rows (two of the block for HB = 16, one of the half for HB = 8)
-  const int mi = HB == 16 ? gk * 32 + rb * 16 + 2 * qq : gk * 32 + r0 + qq;
+  // The 8 lanes of a K-group reduce their row sums in three DPP steps (partners lane ^ 7,
+  // lane ^ 2, lane ^ 1). Byte slot j of a lane's code dwords is read from byte j ^ gsw, so
+  // the rows a lane keeps at the first two steps sit in the same registers in every lane and
+  // those steps are single DPP adds; only the last step selects. The lane finishes row R
+  // (and R + 1 for a 16-row block) of its workgroup.
+  const int b0 = lane & 1, b1 = (lane >> 1) & 1, b2 = (lane >> 2) & 1;
+  const int gsw = 2 * b2 + (b1 ^ b2);
+  const int R = HB == 16 ? 2 * gsw + 8 * b0 : 2 * gsw + b0;
+  const int mi = gk * 32 + (HB == 16 ? rb * 16 : r0) + R;   // meta index of row R
   const int kt0 = chunk * TPW;
 
   // ---- 1. every load of the wave
@@ -198,6 +226,10 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
+  // wave slots this workgroup has no wave for add zero in the fixed 16-term sum of step 6
+  for (int i = tid; i < G * 256; i += G * WM * 64)
+    if (((i >> 4) & 15) >= WM) sred[i >> 8][(i >> 4) & 15][i & 15] = 0.f;
+
   // ---- 2. activations: as given, RMSNorm of h, or merged attention records; bf16 bits
   uint2 xr[TPW];
   if constexpr (XREC) {
@@ -245,22 +277,23 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
     ep_s = tb[32];
   }
 
-  // ---- 3. fp16 conversion with one power-of-two scale per wave (its live tiles)
-  float xm = 0.f;
+  // ---- 3. fp16 conversion with one power-of-two scale 2^se per K-group of 8 lanes (the
+  // lanes whose products are summed before the group's scale and minimum apply). The largest
+  // |x| is taken on the bf16 bits: its exponent field E bounds it by 2^(E - 126), and
+  // se = 141 - E brings it under 2^15, inside fp16's range. (A wave's clamped duplicate of
+  // the last K-tile repeats values the wave already holds, so it never changes the max.)
+  uint32_t am = 0;
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
-    if (kt0 + t < a.k_t) {
-      xm = fmaxf(xm, fmaxf(fabsf(bf16lo(xr[t].x)), fabsf(bf16hi(xr[t].x))));
-      xm = fmaxf(xm, fmaxf(fabsf(bf16lo(xr[t].y)), fabsf(bf16hi(xr[t].y))));
-    }
-  xm = wave_max(xm);
-  int e = 0;
-  if (xm > 0.f && xm <= 3.0e38f) {
-    (void)frexpf(xm, &e);   // xm < 2^e
-    e -= 15;                // scaled max < 2^15 < fp16 max
-    e = e < -120 ? -120 : e;
+  for (int t = 0; t < TPW; ++t) {
+    const uint32_t u = xr[t].x, v = xr[t].y;
+    am = max(am, max(max(__builtin_amdgcn_ubfe(u, 0, 15), __builtin_amdgcn_ubfe(u, 16, 15)),
+                     max(__builtin_amdgcn_ubfe(v, 0, 15), __builtin_amdgcn_ubfe(v, 16, 15))));
   }
-  const float xs = ldexpf(1.0f, -e);
+  am = max(am, dpp_u<kDppXor1>(am));
+  am = max(am, dpp_u<kDppXor2>(am));
+  am = max(am, dpp_u<kDppHalfMirror>(am));
+  const int se = min(141 - (int)(am >> 7), 120);   // zero / subnormal groups: 2^120
+  const float xs = __uint_as_float((uint32_t)(se + 127) << 23);
   uint32_t xp[TPW][2];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
@@ -274,16 +307,20 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   }
 
   // ---- 4. tiles
+  uint32_t sl[4];   // v_perm selectors of the lane's byte slots
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sl[j] = sel_pair(j ^ gsw);
+  // r * 2^20 undoes the codes' 2^-20, and both sums carry the activation scale 2^se
+  const int ur = 20 - se, ux = -se;
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    const bool live = kt0 + t < a.k_t;
+    const bool live = kt0 + t < a.k_t;   // always true for t = 0
     float X = 0.f;
-    constexpr float kC = 1048576.0f;   // undo the 2^-20 of the codes
     if constexpr (HB == 16) {
-      float pv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) pv[i] = 0.f;
+      // pv[8 dw + 2 j + nib]: dword dw (rows 0-7 / 8-15), byte j ^ gsw, low / high nibble,
+      // i.e. row 8 dw + 2 (j ^ gsw) + nib, summed over the lane's 4 K
+      float pv[16] = {};
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         // dwords: rows 0-7 at k, rows 8-15 at k, rows 0-7 at k+1, rows 8-15 at k+1; the low
@@ -295,46 +332,46 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
         const uint32_t Hz = w.z & 0xF0F0F0F0u, Hw = w.w & 0xF0F0F0F0u;
         const uint32_t xc = xp[t][c];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pv[2 * i] = dot2(perm(Lz, Lx, sel_pair(i)), xc, pv[2 * i]);
-          pv[2 * i + 1] = dot2(perm(Hz, Hx, sel_pair(i)), xc, pv[2 * i + 1]);
-          pv[8 + 2 * i] = dot2(perm(Lw, Ly, sel_pair(i)), xc, pv[8 + 2 * i]);
-          pv[8 + 2 * i + 1] = dot2(perm(Hw, Hy, sel_pair(i)), xc, pv[8 + 2 * i + 1]);
+        for (int j = 0; j < 4; ++j) {
+          pv[2 * j] = dot2_acc(perm(Lz, Lx, sl[j]), xc, pv[2 * j], c == 0);
+          pv[2 * j + 1] = dot2_acc(perm(Hz, Hx, sl[j]), xc, pv[2 * j + 1], c == 0);
+          pv[8 + 2 * j] = dot2_acc(perm(Lw, Ly, sl[j]), xc, pv[8 + 2 * j], c == 0);
+          pv[8 + 2 * j + 1] = dot2_acc(perm(Hw, Hy, sl[j]), xc, pv[8 + 2 * j + 1], c == 0);
         }
-        X = dot2(xc, 0x3C003C00u, X);
+        X = dot2_acc(xc, 0x3C003C00u, X, c == 0);
       }
-      // 16 rows over the 8 lanes of the K-group: lane bit 2 (half mirror), bit 1, bit 0
+      // 16 rows over the 8 lanes of the K-group. Slot s holds row s ^ (2 gsw), and gsw
+      // differs by 2 between lane and lane ^ 7 and by 1 between lane and lane ^ 2: the
+      // partner's slot s + 4 (s + 2) holds the row of this lane's slot s.
       float t8[8], t4[4], r2[2];
-      const bool u2 = (lane & 4) != 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float keep = u2 ? pv[i + 8] : pv[i], send = u2 ? pv[i] : pv[i + 8];
-        t8[i] = keep + dpp<kDppHalfMirror>(send);
+      for (int u = 0; u < 8; ++u) {
+        const int s = (u & 3) + 8 * (u >> 2);
+        t8[u] = pv[s] + dpp<kDppHalfMirror>(pv[s + 4]);
       }
-      const bool u1 = (lane & 2) != 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float keep = u1 ? t8[i + 4] : t8[i], send = u1 ? t8[i] : t8[i + 4];
-        t4[i] = keep + dpp<kDppXor2>(send);
+      for (int v = 0; v < 4; ++v) {
+        const int u = (v & 1) + 4 * (v >> 1);
+        t4[v] = t8[u] + dpp<kDppXor2>(t8[u + 2]);
       }
-      const bool u0 = (lane & 1) != 0;
+      // t4: rows 2 gsw, +1, +8, +9, the same in lane ^ 1, which keeps the other pair
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const float keep = u0 ? t4[i + 2] : t4[i], send = u0 ? t4[i] : t4[i + 2];
+        const float keep = b0 ? t4[i + 2] : t4[i], send = b0 ? t4[i] : t4[i + 2];
         r2[i] = keep + dpp<kDppXor1>(send);
       }
       X += dpp<kDppHalfMirror>(X);
       X += dpp<kDppXor2>(X);
       X += dpp<kDppXor1>(X);
-      const float c0 = fmaf(bf16lo(md[t]), r2[0] * kC, bf16lo(mm[t]) * X);
-      const float c1 = fmaf(bf16hi(md[t]), r2[1] * kC, bf16hi(mm[t]) * X);
-      acc0 += live ? c0 : 0.f;
-      acc1 += live ? c1 : 0.f;
+      const float Xs = __builtin_amdgcn_ldexpf(X, ux);
+      const float c0 = fmaf(bf16lo(md[t]), __builtin_amdgcn_ldexpf(r2[0], ur), bf16lo(mm[t]) * Xs);
+      const float c1 = fmaf(bf16hi(md[t]), __builtin_amdgcn_ldexpf(r2[1], ur), bf16hi(mm[t]) * Xs);
+      acc0 = t == 0 ? c0 : acc0 + (live ? c0 : 0.f);
+      acc1 = t == 0 ? c1 : acc1 + (live ? c1 : 0.f);
     } else {
-      // the 8 rows of this half: one dword at k and one at k + 1 of each 16-byte load
-      float pv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) pv[i] = 0.f;
+      // the 8 rows of this half: one dword at k and one at k + 1 of each 16-byte load;
+      // pv[2 j + nib] is row 2 (j ^ gsw) + nib of the half
+      float pv[8] = {};
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const uint4 w = wq[t][c];
@@ -343,69 +380,57 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
         const uint32_t H0 = a0 & 0xF0F0F0F0u, H1 = a1 & 0xF0F0F0F0u;
         const uint32_t xc = xp[t][c];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pv[2 * i] = dot2(perm(L1, L0, sel_pair(i)), xc, pv[2 * i]);
-          pv[2 * i + 1] = dot2(perm(H1, H0, sel_pair(i)), xc, pv[2 * i + 1]);
+        for (int j = 0; j < 4; ++j) {
+          pv[2 * j] = dot2_acc(perm(L1, L0, sl[j]), xc, pv[2 * j], c == 0);
+          pv[2 * j + 1] = dot2_acc(perm(H1, H0, sl[j]), xc, pv[2 * j + 1], c == 0);
         }
-        X = dot2(xc, 0x3C003C00u, X);
+        X = dot2_acc(xc, 0x3C003C00u, X, c == 0);
       }
-      // 8 rows over the 8 lanes of the K-group: lane l keeps row l % 8
+      // 8 rows over the 8 lanes of the K-group, as above; lane ^ 1 shares rows 2 gsw, +1
       float t4[4], t2[2];
-      const bool u2 = (lane & 4) != 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float keep = u2 ? pv[i + 4] : pv[i], send = u2 ? pv[i] : pv[i + 4];
-        t4[i] = keep + dpp<kDppHalfMirror>(send);
-      }
-      const bool u1 = (lane & 2) != 0;
+      for (int u = 0; u < 4; ++u) t4[u] = pv[u] + dpp<kDppHalfMirror>(pv[u + 4]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const float keep = u1 ? t4[i + 2] : t4[i], send = u1 ? t4[i] : t4[i + 2];
-        t2[i] = keep + dpp<kDppXor2>(send);
-      }
-      const bool u0 = (lane & 1) != 0;
-      const float keep = u0 ? t2[1] : t2[0], send = u0 ? t2[0] : t2[1];
+      for (int v = 0; v < 2; ++v) t2[v] = t4[v] + dpp<kDppXor2>(t4[v + 2]);
+      const float keep = b0 ? t2[1] : t2[0], send = b0 ? t2[0] : t2[1];
       const float r1 = keep + dpp<kDppXor1>(send);
       X += dpp<kDppHalfMirror>(X);
       X += dpp<kDppXor2>(X);
       X += dpp<kDppXor1>(X);
-      const float c0 = fmaf(bf16lo(md[t]), r1 * kC, bf16lo(mm[t]) * X);
-      acc0 += live ? c0 : 0.f;
+      const float Xs = __builtin_amdgcn_ldexpf(X, ux);
+      const float c0 = fmaf(bf16lo(md[t]), __builtin_amdgcn_ldexpf(r1, ur), bf16lo(mm[t]) * Xs);
+      acc0 = t == 0 ? c0 : acc0 + (live ? c0 : 0.f);
     }
   }
 
-  // ---- 5. sum over the 8 K-groups (lane bits 3..5), undo the activation scale
+  // ---- 5. sum over the 8 K-groups (lane bits 3..5)
   {
-    const float sc = ldexpf(1.0f, e);
     float v0 = acc0, v1 = acc1;
     v0 += dpp<kDppRor8>(v0);
     v1 += dpp<kDppRor8>(v1);
     v0 = xor32_sum(xor16_sum(v0));
     v1 = xor32_sum(xor16_sum(v1));
     if (lane < 8) {
-      if constexpr (HB == 16) {
-        sred[wave][2 * lane] = v0 * sc;
-        sred[wave][2 * lane + 1] = v1 * sc;
-      } else {
-        sred[wave][lane] = v0 * sc;
-      }
+      sred[member][chunk][R] = v0;
+      if constexpr (HB == 16) sred[member][chunk][R + 1] = v1;
     }
   }
   __syncthreads();
   if (tid >= 64) return;
 
-  // ---- 6. waves of each member in order; thread r < HB holds row r of each member
+  // ---- 6. the 16 wave slots of each member (zero past its waves) in a fixed pairwise
+  // order; thread r < HB holds row r of each member
   float s[G];
 #pragma unroll
   for (int m = 0; m < G; ++m) {
     float v[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) v[c] = sred[min(m * WM + c, 15)][er & (HB - 1)];
-    float acc = 0.f;
+    for (int c = 0; c < 16; ++c) v[c] = sred[m][c][er & (HB - 1)];
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c < WM) acc += v[c];
-    s[m] = acc;
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int c = 0; c < w; ++c) v[c] = v[2 * c] + v[2 * c + 1];
+    s[m] = v[0];
   }
 
   // ---- 7. epilogue
