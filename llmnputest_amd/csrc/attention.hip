@@ -240,7 +240,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
   for (int e = tid; e < G * 64; e += 256) {
     const int h = e >> 6, d = e & 63;
     const float Ls = s_fin[h][65];
-    const float o = Ls > 0.f ? s_fin[h][d] / Ls : 0.f;   // an empty sequence gives zeros
+    const float o = Ls > 0.f ? attn_div(s_fin[h][d], Ls) : 0.f;   // an empty sequence: 0
     const size_t oi = ((size_t)b * a.hq + kvh * G + h) * 64 + d;
     if (a.out) a.out[oi] = f32_to_bf16(o);
     if (a.out_f32) a.out_f32[oi] = o;

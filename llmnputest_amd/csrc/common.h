@@ -39,6 +39,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return r;
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return (uint16_t)pack_bf16x2(f, 0.f); }
+// The same rounding for operands that are consumed in place (a NaN stays a NaN, its payload
+// is not kept): one instruction.
+__device__ __forceinline__ uint32_t pack_bf16x2_op(float lo, float hi) {
+  const f32x2_v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
+}
+
+// RMSNorm scale 1 / sqrt(ss / K + eps) from a row's sum of squares ss. Every kernel family
+// computes it with this one sequence (v_rcp_f32, v_rsq_f32: 1 ulp each), so all of them
+// normalise a row to the same bits.
+__device__ __forceinline__ float rms_inv(float ss, int K, float eps) {
+  return __builtin_amdgcn_rsqf(fmaf(ss, __builtin_amdgcn_rcpf((float)K), eps));
+}
+// a / l for the attention split merge (both the attention kernel's own merge and the
+// o-projection's prologue use it, so the two paths agree bit for bit)
+__device__ __forceinline__ float attn_div(float a, float l) {
+  return a * __builtin_amdgcn_rcpf(l);
+}
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* __restrict__ x
   if ((tid & 63) == 0) part[tid >> 6] = ss;
   __syncthreads();
   const float tot = part[0] + part[1] + part[2] + part[3];
-  const float inv = 1.0f / sqrtf(tot / (float)cols + eps);
+  const float inv = rms_inv(tot, cols, eps);
   for (int c = tid; c < cols; c += 256) {
     const float v = XF32 ? xf[c] : bf16_to_f32(xb[c]);
     const float o = (v * inv) * bf16_to_f32(w[c]);

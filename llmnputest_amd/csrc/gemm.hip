@@ -373,7 +373,7 @@ __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h,
   const float* srow = ssq + (int64_t)m * n_ss;
   float4 sq[2];   // n_ss <= 512
   ssq_load<2>(srow, l, n_ss, sq);
-  const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<2>(sq, l, n_ss)) / (float)K + eps);
+  const float inv = rms_inv(wave_sum(ssq_lane_sum<2>(sq, l, n_ss)), K, eps);
   uint16_t* xr = xn + (int64_t)m * xn_stride;
 #pragma unroll
   for (int i = 0; i < kMaxChunks; ++i) {

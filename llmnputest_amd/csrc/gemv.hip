@@ -323,7 +323,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
   if (pre_ssq) {
 #pragma unroll
     for (int b = 0; b < B; ++b)
-      inv_rms[b] = 1.0f / sqrtf(wave_sum(ssq_lane_sum<kSsqLoads>(sq[b], lane, n_ss)) / (float)K + a.eps);
+      inv_rms[b] = rms_inv(wave_sum(ssq_lane_sum<kSsqLoads>(sq[b], lane, n_ss)), K, a.eps);
   } else if (norm) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
@@ -350,7 +350,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
 #pragma unroll
       for (int w = 0; w < kMaxWaves; ++w)
         if (w < n_sum_waves) s += v[w];
-      inv_rms[b] = 1.0f / sqrtf(s / (float)K + a.eps);
+      inv_rms[b] = rms_inv(s, K, a.eps);
     }
   }
   if (norm) {

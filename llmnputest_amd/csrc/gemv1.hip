@@ -251,18 +251,20 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
           A3 = fmaf(racc[i].w, f, A3);
         }
     }
-    const float o0 = L > 0.f ? A0 / L : 0.f, o1 = L > 0.f ? A1 / L : 0.f;
-    const float o2 = L > 0.f ? A2 / L : 0.f, o3 = L > 0.f ? A3 / L : 0.f;
-    xr[0] = make_uint2((uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16),
-                       (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16));
+    const float o0 = L > 0.f ? attn_div(A0, L) : 0.f, o1 = L > 0.f ? attn_div(A1, L) : 0.f;
+    const float o2 = L > 0.f ? attn_div(A2, L) : 0.f, o3 = L > 0.f ? attn_div(A3, L) : 0.f;
+    xr[0] = make_uint2(pack_bf16x2_op(o0, o1), pack_bf16x2_op(o2, o3));
   } else if constexpr (NORM) {
-    const float inv = 1.0f / sqrtf(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / kSsqRows)) / (float)K + a.eps);
+    const float inv = rms_inv(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / kSsqRows)), K, a.eps);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      xr[t].x = pack_bf16x2((hv[t].x * inv) * bf16lo(nv[t].x), (hv[t].y * inv) * bf16hi(nv[t].x));
-      xr[t].y = pack_bf16x2((hv[t].z * inv) * bf16lo(nv[t].y), (hv[t].w * inv) * bf16hi(nv[t].y));
+      const float n0 = (hv[t].x * inv) * bf16lo(nv[t].x), n1 = (hv[t].y * inv) * bf16hi(nv[t].x);
+      const float n2 = (hv[t].z * inv) * bf16lo(nv[t].y), n3 = (hv[t].w * inv) * bf16hi(nv[t].y);
+      xr[t] = make_uint2(pack_bf16x2_op(n0, n1), pack_bf16x2_op(n2, n3));
+      // the stored row keeps NaN payloads as every bf16 output does
       if (a.xn_out != nullptr && group == 0 && rb == 0 && member == 0 && kt0 + t < a.k_t)
-        *(uint2*)(a.xn_out + (kt0 + t) * kTileK + k0) = xr[t];
+        *(uint2*)(a.xn_out + (kt0 + t) * kTileK + k0) =
+            make_uint2(pack_bf16x2(n0, n1), pack_bf16x2(n2, n3));
     }
   } else {
 #pragma unroll
@@ -404,16 +406,19 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   }
 
   // ---- 5. sum over the 8 K-groups (lane bits 3..5)
-  {
-    float v0 = acc0, v1 = acc1;
-    v0 += dpp<kDppRor8>(v0);
-    v1 += dpp<kDppRor8>(v1);
+  if constexpr (HB == 16) {
+    // v_permlane16_swap(a, b) leaves rows (a0, b0, a2, b2) and (a1, b1, a3, b3): their sum
+    // carries row R's partial sums in the even 16-lane rows and row R + 1's in the odd ones
+    const float v0 = acc0 + dpp<kDppRor8>(acc0), v1 = acc1 + dpp<kDppRor8>(acc1);
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v0), __float_as_uint(v1),
+                                                     false, false);
+    const float p = xor32_sum(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+    if (lane < 8) sred[member][chunk][R] = p;
+    else if (lane >= 16 && lane < 24) sred[member][chunk][R + 1] = p;
+  } else {
+    float v0 = acc0 + dpp<kDppRor8>(acc0);
     v0 = xor32_sum(xor16_sum(v0));
-    v1 = xor32_sum(xor16_sum(v1));
-    if (lane < 8) {
-      sred[member][chunk][R] = v0;
-      if constexpr (HB == 16) sred[member][chunk][R + 1] = v1;
-    }
+    if (lane < 8) sred[member][chunk][R] = v0;
   }
   __syncthreads();
   if (tid >= 64) return;
