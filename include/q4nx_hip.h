@@ -66,9 +66,10 @@ const char *q4nx_last_error(void);
 typedef struct q4nx_policy {
   int mfma_rows_q4;   /* q4 GEMV / fused groups: rows from which they run on the matrix
                          cores (the q4nx_gemm kernels); 0 = never. Default 2. */
-  int mfma_rows_q8;   /* the same for q8. Default 1. */
-  int rowblock;       /* 1 (default): one-row q4 calls on the row-block kernels (one
-                         workgroup per 16 output rows); 0: on the general VALU GEMV */
+  int mfma_rows_q8;   /* the same for q8. Default 2. */
+  int rowblock;       /* 1 (default): one-row calls on the row-block kernels (one
+                         workgroup per 16 output rows; q4, and q8 for a plain GEMV);
+                         0: on the general VALU GEMV */
   int gemv_ksplit;    /* general VALU GEMV: workgroups per output group along K, 1..8;
                          0 = automatic (default) */
   int gemv_tiles_per_wave; /* general VALU GEMV: K-tiles per wave, 1, 2 or 4; 0 = automatic */

@@ -26,7 +26,7 @@ class Policy(C.Structure):
     _fields_ = [
         ("mfma_rows_q4", c_i),          # q4 rows from which the matrix cores take a call; 0 never
         ("mfma_rows_q8", c_i),          # the same for q8
-        ("rowblock", c_i),              # one-row q4 calls on the row-block kernels
+        ("rowblock", c_i),              # one-row calls on the row-block kernels
         ("gemv_ksplit", c_i),           # general VALU GEMV: K parts per group, 0 automatic
         ("gemv_tiles_per_wave", c_i),   # general VALU GEMV: K-tiles per wave, 0 automatic
         ("gemm_ksplit", c_i),           # matrix-core contraction: K parts, 0 automatic

@@ -835,11 +835,12 @@ static int check_ssq_in(const float* ssq_in, const uint16_t* norm_w, int k_tiles
   return Q4NX_OK;
 }
 
-// Whether a one-row q4 call of G member tile-rows runs on the row-block kernels (gemv1.hip):
-// the policy's choice, for the K they cover, with the producer's sums of squares for a norm.
+// Whether a one-row call of G member tile-rows runs on the row-block kernels (gemv1.hip; q4,
+// and q8 for a plain GEMV): the policy's choice, for the K they cover, with the producer's
+// sums of squares for a norm.
 static bool take_rowblock(int kind, int batch, int G, int k_tiles, const uint16_t* norm_w,
                           const float* ssq_in, const Policy& P) {
-  return P.rowblock && kind == Q4NX_KIND_Q4 && batch == 1 &&
+  return P.rowblock && (kind == Q4NX_KIND_Q4 || G == 1) && batch == 1 &&
          gemv1_fits(G, k_tiles, norm_w != nullptr) && (norm_w == nullptr || ssq_in != nullptr);
 }
 
@@ -920,7 +921,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
     g.residual = residual;
     g.ssq_out = ssq_out;
     g.keys = argmax_keys;
-    return gemv1_launch(G1_PLAIN, g, (hipStream_t)stream, what);
+    return gemv1_launch(G1_PLAIN, g, (hipStream_t)stream, what, kind);
   }
   GemvArgs a{};
   a.w[0] = w;

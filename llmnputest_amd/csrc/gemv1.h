@@ -1,4 +1,5 @@
-// Batch-1 q4 GEMV family (gemv1.hip): one workgroup per (output group, 16-row block).
+// Batch-1 GEMV family (gemv1.hip): one workgroup per (output group, 16-row block); q4
+// tiles, and q8 tiles for a plain GEMV.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -45,7 +46,8 @@ struct Gemv1Args {
 
 int gemv1_tpw(int G, int k_t);
 bool gemv1_fits(int G, int k_t, bool norm);
-int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what);
+int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what,
+                 int kind = 4);   // kind 8 (q8 tiles): plain GEMV only
 int gemv1_attn_launch(const Gemv1Args& a, hipStream_t s, const char* what);
 
 }  // namespace q4nx

@@ -77,11 +77,15 @@ __device__ __forceinline__ unsigned long long key_max16(unsigned long long k) {
   return k;
 }
 
-template <int OP, int G, int TPW, int NSS, int XNS, int HB>
+template <int OP, int G, int TPW, int NSS, int XNS, int HB, int KIND>
 __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   constexpr bool NORM = NSS > 0;
   constexpr bool XREC = XNS > 0;
   static_assert(HB == 16 || (HB == 8 && OP == G1_QKV), "half row blocks: q/k/v only");
+  static_assert(KIND == 4 || (KIND == 8 && OP == G1_PLAIN && !XREC && HB == 16),
+                "q8 tiles: plain GEMV only");
+  constexpr int TB = KIND == 8 ? kQ8TileBytes : kQ4TileBytes;
+  constexpr int NW = KIND == 8 ? 4 : 2;   // 16-byte code loads per lane and K-tile
   __shared__ float sred[G][16][16];   // [member][wave of the member][row]
 
   // every argument read before the weight stream, in one round of scalar loads (the empty
@@ -152,10 +156,12 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   // lane ^ 2, lane ^ 1). Byte slot j of a lane's code dwords is read from byte j ^ gsw, so
   // the rows a lane keeps at the first two steps sit in the same registers in every lane and
   // those steps are single DPP adds; only the last step selects. The lane finishes row R
-  // (and R + 1 for a 16-row block) of its workgroup.
+  // (and R + RS for a 16-row block) of its workgroup. A q4 byte holds two rows (its byte
+  // index is row bits 1-2), a q8 byte one (row bits 0-1).
   const int b0 = lane & 1, b1 = (lane >> 1) & 1, b2 = (lane >> 2) & 1;
   const int gsw = 2 * b2 + (b1 ^ b2);
-  const int R = HB == 16 ? 2 * gsw + 8 * b0 : 2 * gsw + b0;
+  constexpr int RS = KIND == 8 ? 4 : 1;
+  const int R = KIND == 8 ? gsw + 8 * b0 : HB == 16 ? 2 * gsw + 8 * b0 : 2 * gsw + b0;
   const int mi = gk * 32 + (HB == 16 ? rb * 16 : r0) + R;   // meta index of row R
   const int kt0 = chunk * TPW;
 
@@ -205,17 +211,22 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  uint4 wq[TPW][2];
+  uint4 wq[TPW][NW];
   uint32_t md[TPW], mm[TPW];
   {
-    const uint8_t* rowp = wseg + (size_t)tr * k_t * kQ4TileBytes;
+    const uint8_t* rowp = wseg + (size_t)tr * k_t * TB;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const uint8_t* tile = rowp + (size_t)min(kt0 + t, k_t - 1) * kQ4TileBytes;
-      const uint4* src = (const uint4*)(tile + 1024 + rb * 2048 + lane * 32);
-      wq[t][0] = src[0];
-      wq[t][1] = src[1];
-      if constexpr (HB == 16) {
+      const uint8_t* tile = rowp + (size_t)min(kt0 + t, k_t - 1) * TB;
+      const uint4* src = KIND == 8 ? (const uint4*)(tile + kMetaBytes + rb * 4096 + lane * 64)
+                                   : (const uint4*)(tile + 2 * kMetaBytes + rb * 2048 + lane * 32);
+#pragma unroll
+      for (int c = 0; c < NW; ++c) wq[t][c] = src[c];
+      if constexpr (KIND == 8) {   // the scales of rows R and R + 4
+        md[t] = (uint32_t)*(const uint16_t*)(tile + 2 * mi) |
+                ((uint32_t)*(const uint16_t*)(tile + 2 * (mi + RS)) << 16);
+        mm[t] = 0;
+      } else if constexpr (HB == 16) {
         md[t] = *(const uint32_t*)(tile + 2 * mi);
         mm[t] = *(const uint32_t*)(tile + kMetaBytes + 2 * mi);
       } else {
@@ -319,7 +330,50 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   for (int t = 0; t < TPW; ++t) {
     const bool live = kt0 + t < a.k_t;   // always true for t = 0
     float X = 0.f;
-    if constexpr (HB == 16) {
+    if constexpr (KIND == 8) {
+      // q8: the 16 bytes of load c are rows 0-15 at k = k0 + c; biased by 128 (xor 0x80) a
+      // code is the fp16 subnormal (c + 128) * 2^-24. pv[4 dw + j] is row 4 dw + (j ^ gsw).
+      float pv[16] = {};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint4 A = wq[t][2 * c], B = wq[t][2 * c + 1];
+        const uint32_t av[4] = {A.x ^ 0x80808080u, A.y ^ 0x80808080u, A.z ^ 0x80808080u,
+                                A.w ^ 0x80808080u};
+        const uint32_t bv[4] = {B.x ^ 0x80808080u, B.y ^ 0x80808080u, B.z ^ 0x80808080u,
+                                B.w ^ 0x80808080u};
+        const uint32_t xc = xp[t][c];
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            pv[4 * dw + j] = dot2_acc(perm(bv[dw], av[dw], sl[j]), xc, pv[4 * dw + j], c == 0);
+        X = dot2_acc(xc, 0x3C003C00u, X, c == 0);
+      }
+      // partners: lane ^ 7 holds row s ^ 2 of this lane's slot s in slot s + 2 (s bit 1 clear),
+      // lane ^ 2 holds it in slot s + 1 (s bit 0 clear); then rows gsw + 4v in t4[v]
+      float t8[8], t4[4], r2[2];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int sl8 = (u & 1) + 4 * (u >> 1);
+        t8[u] = pv[sl8] + dpp<kDppHalfMirror>(pv[sl8 + 2]);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) t4[v] = t8[2 * v] + dpp<kDppXor2>(t8[2 * v + 1]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {   // lane ^ 1 keeps the other two of the four rows
+        const float keep = b0 ? t4[i + 2] : t4[i], send = b0 ? t4[i] : t4[i + 2];
+        r2[i] = keep + dpp<kDppXor1>(send);
+      }
+      X += dpp<kDppHalfMirror>(X);
+      X += dpp<kDppXor2>(X);
+      X += dpp<kDppXor1>(X);
+      // s * sum(c x) = s * (sum((c + 128) x) - 128 sum(x))
+      const float Xb = 128.0f * __builtin_amdgcn_ldexpf(X, ux);
+      const float c0 = bf16lo(md[t]) * (__builtin_amdgcn_ldexpf(r2[0], ur + 4) - Xb);
+      const float c1 = bf16hi(md[t]) * (__builtin_amdgcn_ldexpf(r2[1], ur + 4) - Xb);
+      acc0 = t == 0 ? c0 : acc0 + (live ? c0 : 0.f);
+      acc1 = t == 0 ? c1 : acc1 + (live ? c1 : 0.f);
+    } else if constexpr (HB == 16) {
       // pv[8 dw + 2 j + nib]: dword dw (rows 0-7 / 8-15), byte j ^ gsw, low / high nibble,
       // i.e. row 8 dw + 2 (j ^ gsw) + nib, summed over the lane's 4 K
       float pv[16] = {};
@@ -414,7 +468,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
                                                      false, false);
     const float p = xor32_sum(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
     if (lane < 8) sred[member][chunk][R] = p;
-    else if (lane >= 16 && lane < 24) sred[member][chunk][R + 1] = p;
+    else if (lane >= 16 && lane < 24) sred[member][chunk][R + RS] = p;
   } else {
     float v0 = acc0 + dpp<kDppRor8>(acc0);
     v0 = xor32_sum(xor16_sum(v0));
@@ -508,37 +562,40 @@ bool gemv1_fits(int G, int k_t, bool norm) {
 }
 
 // blocks: workgroups of 16-row blocks (two per group); HB = 8 launches twice as many
-template <int OP, int G, int TPW, int NSS, int XNS>
+template <int OP, int G, int TPW, int NSS, int XNS, int KIND = 4>
 static void go(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
   constexpr int HB = OP == G1_QKV ? 8 : 16;
-  hipLaunchKernelGGL((gemv1_kernel<OP, G, TPW, NSS, XNS, HB>), dim3(HB == 8 ? 2 * blocks : blocks),
-                     dim3(threads), 0, s, a);
+  hipLaunchKernelGGL((gemv1_kernel<OP, G, TPW, NSS, XNS, HB, KIND>),
+                     dim3(HB == 8 ? 2 * blocks : blocks), dim3(threads), 0, s, a);
 }
 
-template <int OP, int G, int TPW>
+template <int OP, int G, int TPW, int KIND>
 static void go_norm(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
-  if (a.norm_w == nullptr) go<OP, G, TPW, 0, 0>(a, blocks, threads, s);
-  else if (a.k_t * kTileK / kSsqRows <= 256) go<OP, G, TPW, 1, 0>(a, blocks, threads, s);
-  else go<OP, G, TPW, 2, 0>(a, blocks, threads, s);
+  if (a.norm_w == nullptr) go<OP, G, TPW, 0, 0, KIND>(a, blocks, threads, s);
+  else if (a.k_t * kTileK / kSsqRows <= 256) go<OP, G, TPW, 1, 0, KIND>(a, blocks, threads, s);
+  else go<OP, G, TPW, 2, 0, KIND>(a, blocks, threads, s);
 }
 
-template <int OP, int G>
+template <int OP, int G, int KIND = 4>
 static void go_tpw(const Gemv1Args& a, int tpw, int blocks, int threads, hipStream_t s) {
   switch (tpw) {
-    case 1: go_norm<OP, G, 1>(a, blocks, threads, s); break;
-    case 2: go_norm<OP, G, 2>(a, blocks, threads, s); break;
-    default: go_norm<OP, G, 4>(a, blocks, threads, s); break;
+    case 1: go_norm<OP, G, 1, KIND>(a, blocks, threads, s); break;
+    case 2: go_norm<OP, G, 2, KIND>(a, blocks, threads, s); break;
+    default: go_norm<OP, G, 4, KIND>(a, blocks, threads, s); break;
   }
 }
 
-int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what) {
+int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what, int kind) {
   const int G = op == G1_PLAIN ? 1 : 2;
   const int tpw = gemv1_tpw(G, a.k_t);
   Q4NX_REQUIRE(tpw > 0, Q4NX_ERR_SHAPE, "%s: K=%d is longer than one workgroup covers", what,
                a.k_t * kTileK);
+  Q4NX_REQUIRE(kind == 4 || (kind == 8 && op == G1_PLAIN), Q4NX_ERR_ARG,
+               "%s: the row-block kernels take q8 tiles for a plain GEMV only", what);
   const int threads = G * ((a.k_t + tpw - 1) / tpw) * 64;
   const int blocks = 2 * a.n_groups;
-  if (op == G1_PLAIN) go_tpw<G1_PLAIN, 1>(a, tpw, blocks, threads, s);
+  if (op == G1_PLAIN && kind == 8) go_tpw<G1_PLAIN, 1, 8>(a, tpw, blocks, threads, s);
+  else if (op == G1_PLAIN) go_tpw<G1_PLAIN, 1>(a, tpw, blocks, threads, s);
   else if (op == G1_GATEUP) go_tpw<G1_GATEUP, 2>(a, tpw, blocks, threads, s);
   else go_tpw<G1_QKV, 2>(a, tpw, blocks, threads, s);
   return check_launch(what);

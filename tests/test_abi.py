@@ -44,7 +44,7 @@ def pol(**kw):
 def test_policy_defaults_and_validation():
     p = _lib.Policy()
     assert (p.mfma_rows_q4, p.mfma_rows_q8, p.rowblock, p.gemv_ksplit, p.gemv_tiles_per_wave,
-            p.gemm_ksplit, p.attn_mfma) == (2, 1, 1, 0, 0, 0, 1)
+            p.gemm_ksplit, p.attn_mfma) == (2, 2, 1, 0, 0, 0, 1)
     fake = C.c_void_p(0x10000)
     for bad in ({"gemv_ksplit": 9}, {"gemv_tiles_per_wave": 3}, {"gemm_ksplit": -1},
                 {"attn_mfma": 2}, {"rowblock": 5}, {"mfma_rows_q4": -1}):
@@ -200,8 +200,10 @@ def test_ws_queries():
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, pol(mfma_rows_q4=0)) == 65536 + 56 * 5 * 2 * 64 * 4
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, None) == 65536 + 56 * 5 * 16 * 64 * 4 + 2 * 2560 * 2
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 1, None) == 0     # one row: row-block kernel
-    # q8 lm_head at one row (matrix cores): 3136 workgroups, no split, one normalised row
-    assert lib.q4nx_gemv_ws_bytes(8, 3136, 10, 1, None) == 65536 + 2560 * 2
+    # q8 lm_head at one row: the row-block kernel (the default) needs nothing; on the matrix
+    # cores 3136 workgroups, no split, one normalised row
+    assert lib.q4nx_gemv_ws_bytes(8, 3136, 10, 1, None) == 0
+    assert lib.q4nx_gemv_ws_bytes(8, 3136, 10, 1, pol(mfma_rows_q8=1)) == 65536 + 2560 * 2
     assert lib.q4nx_gate_up_ws_bytes(256, 10, 1, None) == 0
     assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64, None) == 0  # one split: no workspace
     big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768, pol(attn_mfma=0))   # 64 splits
