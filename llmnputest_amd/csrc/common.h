@@ -52,6 +52,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2_op(float lo, float hi) {
 __device__ __forceinline__ float rms_inv(float ss, int K, float eps) {
   return __builtin_amdgcn_rsqf(fmaf(ss, __builtin_amdgcn_rcpf((float)K), eps));
 }
+// x narrowed to bf16 and widened back, for values used in place (a NaN stays a NaN)
+__device__ __forceinline__ float round_bf16_op(float x) { return bf16lo(pack_bf16x2_op(x, 0.f)); }
+
+// silu(g) * u = g / (1 + e^-g) * u (granite_elementwise.h:80-108), with e^-g as 2^(-g log2 e)
+// and a hardware reciprocal: every kernel family computes SwiGLU with this one sequence.
+__device__ __forceinline__ float swiglu(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f)) * u;
+}
+
 // a / l for the attention split merge (both the attention kernel's own merge and the
 // o-projection's prologue use it, so the two paths agree bit for bit)
 __device__ __forceinline__ float attn_div(float a, float l) {

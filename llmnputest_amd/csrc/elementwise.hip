@@ -86,13 +86,13 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ g,
   if (i >= total) return;
   float gv, uv;
   if (INF32) {  // fp32 accumulators are narrowed to bf16 first (granite_swiglu_f32.h:38-41)
-    gv = bf16_to_f32(f32_to_bf16(((const float*)g)[i]));
-    uv = bf16_to_f32(f32_to_bf16(((const float*)u)[i]));
+    gv = round_bf16_op(((const float*)g)[i]);
+    uv = round_bf16_op(((const float*)u)[i]);
   } else {
     gv = bf16_to_f32(((const uint16_t*)g)[i]);
     uv = bf16_to_f32(((const uint16_t*)u)[i]);
   }
-  const float h = (gv / (1.0f + expf(-gv))) * uv;
+  const float h = swiglu(gv, uv);
   y[i] = f32_to_bf16(h);
   if (y_f32) y_f32[i] = h;
 }

@@ -297,9 +297,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
       if (gm >= a.m_rows) continue;
       const int64_t n = (int64_t)group * 32 + j;
       const float gr = *outp(m, j), ur = *outp(m, 32 + j);
-      const float g = bf16_to_f32(f32_to_bf16(gr));
-      const float uu = bf16_to_f32(f32_to_bf16(ur));
-      const float h = (g / (1.0f + expf(-g))) * uu;
+      const float h = swiglu(round_bf16_op(gr), round_bf16_op(ur));
       a.h_out[gm * a.h_stride + n] = f32_to_bf16(h);
       if (a.raw_out != nullptr) {
         a.raw_out[gm * 2 * N + n] = gr;

@@ -614,9 +614,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       if (b < a.batch) {
         const int64_t n = (int64_t)group * 32 + r;
         const float gr = sgrp[b][r], ur = sgrp[b][32 + r];
-        const float g = bf16_to_f32(f32_to_bf16(gr));
-        const float uu = bf16_to_f32(f32_to_bf16(ur));
-        const float h = (g / (1.0f + expf(-g))) * uu;
+        const float h = swiglu(round_bf16_op(gr), round_bf16_op(ur));
         a.h_out[b * a.h_stride + n] = f32_to_bf16(h);
         if (a.raw_out != nullptr) {
           const int64_t N = (int64_t)a.n_tr[0] * 32;

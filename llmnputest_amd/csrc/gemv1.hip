@@ -77,6 +77,57 @@ __device__ __forceinline__ unsigned long long key_max16(unsigned long long k) {
   return k;
 }
 
+// The 16 wave slots of each member (zero past its waves) in a fixed pairwise order: row r
+// of each member, for thread r.
+template <int G>
+__device__ __forceinline__ void slot_sums(const float (*sred)[16][16], int r, float (&s)[G]) {
+#pragma unroll
+  for (int m = 0; m < G; ++m) {
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) v[c] = sred[m][c][r];
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int c = 0; c < w; ++c) v[c] = v[2 * c] + v[2 * c + 1];
+    s[m] = v[0];
+  }
+}
+
+// Epilogue of a plain or gate/up launch, run by the first wave: thread r < 16 finishes row r
+// of the workgroup's 16-row block (tile-row tr, block rb).
+template <int OP, int G>
+__device__ __forceinline__ void finish_block(const Gemv1Args& a, const float (*sred)[16][16],
+                                             int tid, int tr, int rb, float ep_res) {
+  const int er = tid & 15;
+  float s[G];
+  slot_sums<G>(sred, er, s);
+  const int64_t n = (int64_t)tr * 32 + rb * 16 + er;
+  if constexpr (OP == G1_PLAIN) {
+    float v = s[0];
+    if (a.residual != nullptr) v += ep_res;
+    if (tid < 16 && a.y != nullptr) a.y[n] = v;
+    if (a.ssq_out != nullptr) {   // sum of squares of the block's 16 outputs
+      const float q = group16_sum(tid < 16 ? v * v : 0.f);
+      if (tid == 0) a.ssq_out[(int64_t)tr * 2 + rb] = q;
+    }
+    if (a.keys != nullptr) {      // (max, first row) of the block, order-preserving
+      const unsigned long long kk = key_max16(tid < 16 ? argmax_key(v, (uint32_t)n) : 0ull);
+      if (tid == 0) a.keys[(int64_t)tr * 2 + rb] = kk;
+    }
+  } else {
+    static_assert(OP == G1_GATEUP, "plain or gate/up");
+    if (tid < 16) {
+      a.h_out[n] = f32_to_bf16(swiglu(round_bf16_op(s[0]), round_bf16_op(s[1])));
+      if (a.raw_out != nullptr) {
+        const int64_t N = (int64_t)a.n_groups * 32;
+        a.raw_out[n] = s[0];
+        a.raw_out[N + n] = s[1];
+      }
+    }
+  }
+}
+
 template <int OP, int G, int TPW, int NSS, int XNS, int HB, int KIND>
 __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   constexpr bool NORM = NSS > 0;
@@ -176,14 +227,15 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   for (int t = 0; t < TPW; ++t) {
     const int k = min(kt0 + t, k_t - 1) * kTileK + k0;
     if constexpr (XREC) {
-      // attention records of this lane's head (k / 64) and its four dims (k % 64 ..)
+      // attention records of this lane's head (k / 64) and its four dims (k % 64 ..): split
+      // i's record is i * att_g records past split 0's (the launch has XNS == att_split)
       const int h = k >> 6, kvh = h / att_g, hh = h - kvh * att_g;
+      const float* r0p = (const float*)xin + ((size_t)kvh * XNS * att_g + hh) * kAttnRecFloats;
+      const size_t rs = (size_t)att_g * kAttnRecFloats;
 #pragma unroll
       for (int i = 0; i < XNS; ++i) {
-        const int s = min(i, att_split - 1);
-        const float* r = (const float*)xin + ((size_t)(kvh * att_split + s) * att_g + hh) * kAttnRecFloats;
-        racc[i] = *(const float4*)(r + (k & 63));
-        rml[i] = *(const float2*)(r + 64);
+        racc[i] = *(const float4*)(r0p + i * rs + (k & 63));
+        rml[i] = *(const float2*)(r0p + i * rs + 64);
       }
     } else if constexpr (NORM) {
       hv[t] = *(const float4*)((const float*)xin + k);
@@ -243,24 +295,21 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
 
   // ---- 2. activations: as given, RMSNorm of h, or merged attention records; bf16 bits
   uint2 xr[TPW];
-  if constexpr (XREC) {
-    const int ns = a.att_split;
+  if constexpr (XREC) {   // the split merge of attention's own finish, in split order
     float M = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < XNS; ++i)
-      if (i < ns) M = fmaxf(M, rml[i].x);
+    for (int i = 0; i < XNS; ++i) M = fmaxf(M, rml[i].x);
     float L = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int i = 0; i < XNS; ++i)
-        if (i < ns) {
-          const float f = __builtin_amdgcn_exp2f(rml[i].x - M);
-          L = fmaf(rml[i].y, f, L);
-          A0 = fmaf(racc[i].x, f, A0);
-          A1 = fmaf(racc[i].y, f, A1);
-          A2 = fmaf(racc[i].z, f, A2);
-          A3 = fmaf(racc[i].w, f, A3);
-        }
+      for (int i = 0; i < XNS; ++i) {
+        const float f = __builtin_amdgcn_exp2f(rml[i].x - M);
+        L = fmaf(rml[i].y, f, L);
+        A0 = fmaf(racc[i].x, f, A0);
+        A1 = fmaf(racc[i].y, f, A1);
+        A2 = fmaf(racc[i].z, f, A2);
+        A3 = fmaf(racc[i].w, f, A3);
+      }
     }
     const float o0 = L > 0.f ? attn_div(A0, L) : 0.f, o1 = L > 0.f ? attn_div(A1, L) : 0.f;
     const float o2 = L > 0.f ? attn_div(A2, L) : 0.f, o3 = L > 0.f ? attn_div(A3, L) : 0.f;
@@ -477,48 +526,12 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   __syncthreads();
   if (tid >= 64) return;
 
-  // ---- 6. the 16 wave slots of each member (zero past its waves) in a fixed pairwise
-  // order; thread r < HB holds row r of each member
-  float s[G];
-#pragma unroll
-  for (int m = 0; m < G; ++m) {
-    float v[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c) v[c] = sred[m][c][er & (HB - 1)];
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-      for (int c = 0; c < w; ++c) v[c] = v[2 * c] + v[2 * c + 1];
-    s[m] = v[0];
-  }
-
-  // ---- 7. epilogue
-  if constexpr (OP == G1_PLAIN) {
-    const int64_t n = (int64_t)tr * 32 + rb * 16 + er;
-    float v = s[0];
-    if (a.residual != nullptr) v += ep_res;
-    if (tid < 16 && a.y != nullptr) a.y[n] = v;
-    if (a.ssq_out != nullptr) {   // sum of squares of the block's 16 outputs
-      const float q = group16_sum(tid < 16 ? v * v : 0.f);
-      if (tid == 0) a.ssq_out[(int64_t)tr * 2 + rb] = q;
-    }
-    if (a.keys != nullptr) {      // (max, first row) of the block, order-preserving
-      const unsigned long long kk = key_max16(tid < 16 ? argmax_key(v, (uint32_t)n) : 0ull);
-      if (tid == 0) a.keys[(int64_t)tr * 2 + rb] = kk;
-    }
-  } else if constexpr (OP == G1_GATEUP) {
-    if (tid < 16) {
-      const int64_t n = (int64_t)group * 32 + rb * 16 + er;
-      const float g = bf16_to_f32(f32_to_bf16(s[0]));
-      const float u = bf16_to_f32(f32_to_bf16(s[1]));
-      a.h_out[n] = f32_to_bf16((g / (1.0f + expf(-g))) * u);
-      if (a.raw_out != nullptr) {
-        const int64_t N = (int64_t)a.n_groups * 32;
-        a.raw_out[n] = s[0];
-        a.raw_out[N + n] = s[1];
-      }
-    }
-  } else {   // QKV: dims d and d + 32 of one head, d = r0 + r
+  // ---- 6, 7. the wave slots in a fixed order, then the epilogue
+  if constexpr (OP != G1_QKV) {
+    finish_block<OP, G>(a, sred, tid, tr, rb, ep_res);
+  } else {   // QKV: dims d and d + 32 of one head, d = r0 + r (thread r < HB)
+    float s[G];
+    slot_sums<G>(sred, er & (HB - 1), s);
     if (tid < HB) {
       const int d = r0 + er;
       const int seg_off = seg == 0 ? 0 : seg == 1 ? a.n_q_heads * 64 : (a.n_q_heads + a.n_kv_heads) * 64;
@@ -601,6 +614,16 @@ int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what, in
   return check_launch(what);
 }
 
+// The records prologue is compiled for each split count (its loads and merge unrolled
+// exactly, with no masks).
+template <int NS>
+static void go_splits(const Gemv1Args& a, int blocks, int threads, hipStream_t s) {
+  if constexpr (NS < kAttnRecMaxSplits) {
+    if (a.att_split != NS) return go_splits<NS + 1>(a, blocks, threads, s);
+  }
+  go<G1_PLAIN, 1, 1, 0, NS>(a, blocks, threads, s);
+}
+
 // The o-projection from attention records: one K-tile (four heads) per wave.
 int gemv1_attn_launch(const Gemv1Args& a, hipStream_t s, const char* what) {
   Q4NX_REQUIRE(a.k_t >= 1 && a.k_t <= kAttnRecMaxKTiles, Q4NX_ERR_SHAPE,
@@ -608,17 +631,7 @@ int gemv1_attn_launch(const Gemv1Args& a, hipStream_t s, const char* what) {
   Q4NX_REQUIRE(a.att_split >= 1 && a.att_split <= kAttnRecMaxSplits, Q4NX_ERR_SHAPE,
                "%s: %d splits (1..%d)", what, a.att_split, kAttnRecMaxSplits);
   const int blocks = 2 * a.n_groups, threads = a.k_t * 64;
-  switch ((a.att_split + 1) / 2) {
-    case 1: go<G1_PLAIN, 1, 1, 0, 2>(a, blocks, threads, s); break;
-    case 2: go<G1_PLAIN, 1, 1, 0, 4>(a, blocks, threads, s); break;
-    case 3: go<G1_PLAIN, 1, 1, 0, 6>(a, blocks, threads, s); break;
-    case 4: go<G1_PLAIN, 1, 1, 0, 8>(a, blocks, threads, s); break;
-    case 5: go<G1_PLAIN, 1, 1, 0, 10>(a, blocks, threads, s); break;
-    case 6: go<G1_PLAIN, 1, 1, 0, 12>(a, blocks, threads, s); break;
-    case 7: go<G1_PLAIN, 1, 1, 0, 14>(a, blocks, threads, s); break;
-    case 8: go<G1_PLAIN, 1, 1, 0, 16>(a, blocks, threads, s); break;
-    default: go<G1_PLAIN, 1, 1, 0, 18>(a, blocks, threads, s); break;
-  }
+  go_splits<1>(a, blocks, threads, s);
   return check_launch(what);
 }
 
