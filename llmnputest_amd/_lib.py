@@ -92,6 +92,8 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_embed": (c_i, [c_i, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
     "q4nx_argmax": (c_i, [c_p, c_i, c_i, c_i64, c_p, c_p, c_p]),
     "q4nx_decode_advance": (c_i, [c_p, c_i, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p]),
+    "q4nx_decode_advance_embed": (c_i, [c_p, c_i, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p,
+                                        c_i, c_i, c_p, c_p, c_p]),
 }
 
 _lib = None

@@ -108,14 +108,8 @@ __global__ __launch_bounds__(256) void round_bf16_kernel(const float* __restrict
 // h[b][c] = row tokens[b] of a [vocab][hidden] table: bf16 (KIND 16), or q4 / q8 tiles
 // dequantised as tools/q4nx.py:127-143 does (q4: code * d + m with one rounding, q8: code * s).
 template <int KIND>
-__global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ w,
-                                                    const int32_t* __restrict__ tokens,
-                                                    float* __restrict__ h,
-                                                    float* __restrict__ ssq_out, int vocab,
-                                                    int hidden) {
-  const int b = blockIdx.y;
-  const int c = blockIdx.x * 256 + threadIdx.x;   // hidden % 256 == 0: every lane is live
-  const int t = tokens[b];
+__device__ __forceinline__ float embed_value(const uint8_t* __restrict__ w, int t, int c,
+                                             int vocab, int hidden) {
   float v = __builtin_nanf("");                   // a token out of range gives a NaN row
   if (t >= 0 && t < vocab) {
     if constexpr (KIND == Q4NX_KIND_BF16) {
@@ -141,6 +135,18 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
       }
     }
   }
+  return v;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ w,
+                                                    const int32_t* __restrict__ tokens,
+                                                    float* __restrict__ h,
+                                                    float* __restrict__ ssq_out, int vocab,
+                                                    int hidden) {
+  const int b = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;   // hidden % 256 == 0: every lane is live
+  const float v = embed_value<KIND>(w, tokens[b], c, vocab, hidden);
   h[(size_t)b * hidden + c] = v;
   if (ssq_out != nullptr) {   // sum of squares per 16 entries, for a following RMSNorm
     const float s16 = group16_sum(v * v);
@@ -198,11 +204,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 }
 
 // ------------------------------------------------------------------ decode bookkeeping
-// keys: [batch][n_slots] order-preserving argmax keys (one per lm_head tile-row).
-__global__ __launch_bounds__(1024) void decode_advance_kernel(
+// keys: [batch][n_slots] order-preserving argmax keys (one per lm_head tile-row). With s_tok,
+// token b is also left in s_tok[b] (batch <= kAdvanceEmbedMaxBatch) for the whole workgroup.
+constexpr int kAdvanceEmbedMaxBatch = 64;
+__device__ __forceinline__ void decode_advance_body(
     const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
     int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
-    int32_t* __restrict__ step, int history_len, int batch) {
+    int32_t* __restrict__ step, int history_len, int batch, int* s_tok) {
   // Rows are taken `groups` at a time, `wpr` waves per row; each lane keeps eight key loads
   // in flight, then the lanes and the row's waves combine (max is order-independent).
   __shared__ unsigned long long sk[16];
@@ -236,6 +244,7 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
       for (int w = 1; w < wpr; ++w) k = sk[wave + w] > k ? sk[wave + w] : k;
       const int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
       tokens[b] = tok;
+      if (s_tok != nullptr) s_tok[b] = tok;
       const int32_t p = pos[b] + 1;
       pos[b] = p;
       lens[b] = p + 1;
@@ -244,6 +253,42 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
     __syncthreads();
   }
   if (tid == 0) step[0] = s + 1;
+}
+
+__global__ __launch_bounds__(1024) void decode_advance_kernel(
+    const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
+    int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
+    int32_t* __restrict__ step, int history_len, int batch) {
+  decode_advance_body(keys, n_slots, tokens, pos, lens, history, step, history_len, batch,
+                      nullptr);
+}
+
+// The same, then the embedding rows of the new tokens (as embed_kernel): the next step's
+// input is ready when the launch ends, with no launch of its own.
+template <int KIND>
+__global__ __launch_bounds__(1024) void decode_advance_embed_kernel(
+    const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
+    int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
+    int32_t* __restrict__ step, int history_len, int batch, const uint8_t* __restrict__ table,
+    int vocab, int hidden, float* __restrict__ h, float* __restrict__ ssq_out) {
+  __shared__ int s_tok[kAdvanceEmbedMaxBatch];
+  decode_advance_body(keys, n_slots, tokens, pos, lens, history, step, history_len, batch,
+                      s_tok);
+  __syncthreads();
+  for (int b = 0; b < batch; ++b) {
+    const int t = s_tok[b];
+    // hidden % 256 == 0: a 16-lane group is either all inside the row or all past it
+    for (int c0 = 0; c0 < hidden; c0 += 1024) {
+      const int c = c0 + (int)threadIdx.x;
+      const bool in = c < hidden;
+      const float v = embed_value<KIND>(table, t, in ? c : 0, vocab, hidden);
+      if (in) h[(size_t)b * hidden + c] = v;
+      if (ssq_out != nullptr) {
+        const float s16 = group16_sum(v * v);
+        if (in && (c & 15) == 0) ssq_out[(size_t)b * (hidden / 16) + (c >> 4)] = s16;
+      }
+    }
+  }
 }
 
 }  // namespace q4nx
@@ -346,6 +391,38 @@ int q4nx_decode_advance(const uint64_t* keys, int n_slots, int32_t* tokens, int3
                      (const unsigned long long*)keys, n_slots, tokens, pos, lens, history, step,
                      history_len, batch);
   return check_launch("q4nx_decode_advance");
+}
+
+int q4nx_decode_advance_embed(const uint64_t* keys, int n_slots, int32_t* tokens, int32_t* pos,
+                              int32_t* lens, int32_t* history, int32_t* step, int history_len,
+                              int batch, int kind, const void* table, int vocab, int hidden,
+                              float* h, float* ssq_out, void* stream) {
+  const char* what = "q4nx_decode_advance_embed";
+  Q4NX_REQUIRE(keys && tokens && pos && lens && step && table && h, Q4NX_ERR_ARG,
+               "%s: keys, tokens, pos, lens, step, table and h are required", what);
+  Q4NX_REQUIRE(kind == Q4NX_KIND_Q4 || kind == Q4NX_KIND_Q8 || kind == Q4NX_KIND_BF16,
+               Q4NX_ERR_ARG, "%s: kind must be Q4NX_KIND_Q4, _Q8 or _BF16, got %d", what, kind);
+  Q4NX_REQUIRE(batch >= 1 && batch <= kAdvanceEmbedMaxBatch && n_slots >= 1, Q4NX_ERR_SHAPE,
+               "%s: batch=%d (1..%d) n_slots=%d", what, batch, kAdvanceEmbedMaxBatch, n_slots);
+  Q4NX_REQUIRE(vocab > 0 && (kind == Q4NX_KIND_BF16 || vocab % 32 == 0) && hidden > 0 &&
+                   hidden % 256 == 0,
+               Q4NX_ERR_SHAPE, "%s: vocab=%d hidden=%d", what, vocab, hidden);
+  const auto* k = (const unsigned long long*)keys;
+  const uint8_t* w = (const uint8_t*)table;
+  hipStream_t s = (hipStream_t)stream;
+  if (kind == Q4NX_KIND_BF16)
+    hipLaunchKernelGGL(decode_advance_embed_kernel<Q4NX_KIND_BF16>, dim3(1), dim3(1024), 0, s, k,
+                       n_slots, tokens, pos, lens, history, step, history_len, batch, w, vocab,
+                       hidden, h, ssq_out);
+  else if (kind == Q4NX_KIND_Q8)
+    hipLaunchKernelGGL(decode_advance_embed_kernel<Q4NX_KIND_Q8>, dim3(1), dim3(1024), 0, s, k,
+                       n_slots, tokens, pos, lens, history, step, history_len, batch, w, vocab,
+                       hidden, h, ssq_out);
+  else
+    hipLaunchKernelGGL(decode_advance_embed_kernel<Q4NX_KIND_Q4>, dim3(1), dim3(1024), 0, s, k,
+                       n_slots, tokens, pos, lens, history, step, history_len, batch, w, vocab,
+                       hidden, h, ssq_out);
+  return check_launch(what);
 }
 
 }  // extern "C"

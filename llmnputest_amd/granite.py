@@ -247,8 +247,19 @@ class GraniteDecoder:
                 and c.n_q % 4 == 0 and c.n_q <= 40)
 
     # ------------------------------------------------------------ one step, eager
-    def _launch_step(self, b: int) -> None:
-        """Every kernel of one decode step for the first b sequences (no allocation)."""
+    def _embed_table(self):
+        """The embedding rows: a stored bf16 matrix, or the tied lm_head's tiles."""
+        w = self.w
+        return (w.embed, "bf16") if w.embed is not None else (w.lm_head, w.lm_head_kind)
+
+    def _embed(self, b: int) -> None:
+        table, kind = self._embed_table()
+        ops.embed(table, kind, self.tokens[:b], self.cfg.vocab, self.cfg.hidden, out=self.h[:b],
+                  ssq_out=self.ssq[:b])
+
+    def _launch_step(self, b: int, embed: bool = True) -> None:
+        """Every kernel of one decode step for the first b sequences (no allocation); without
+        `embed` the step starts from h as the previous step's advance left it."""
         c, w = self.cfg, self.w
         kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
         h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
@@ -257,11 +268,8 @@ class GraniteDecoder:
         n_split = self.attn_splits or ops.gqa_decode_records_splits(b, c.n_q, c.n_kv,
                                                                     self.max_len, policy=pol)
         fuse_o = self.fuses_attn_o(b, n_split)
-        if w.embed is not None:
-            ops.embed(w.embed, "bf16", self.tokens[:b], c.vocab, c.hidden, out=h, ssq_out=ssq)
-        else:
-            ops.embed(w.lm_head, w.lm_head_kind, self.tokens[:b], c.vocab, c.hidden, out=h,
-                      ssq_out=ssq)
+        if embed:
+            self._embed(b)
         for li, L in enumerate(w.layers):
             kc, vc = self.k_cache[li], self.v_cache[li]
             ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
@@ -305,20 +313,27 @@ class GraniteDecoder:
 
     # ------------------------------------------------------------ graph + greedy loop
     def _advance(self, b: int) -> None:
-        ops.decode_advance(self.keys[:b], self.cfg.vocab // 16, self.tokens[:b], self.pos[:b],
-                           self.lens[:b], self.step_ctr,
-                           self.history[:, :b] if b == self.max_batch else None)
+        """The next token from the argmax keys, positions and history advanced, and the
+        token's embedding row into h for the next step: one launch."""
+        table, kind = self._embed_table()
+        ops.decode_advance_embed(self.keys[:b], self.cfg.vocab // 16, self.tokens[:b],
+                                 self.pos[:b], self.lens[:b], self.step_ctr,
+                                 self.history[:, :b] if b == self.max_batch else None,
+                                 table, kind, self.cfg.vocab, self.cfg.hidden, self.h[:b],
+                                 self.ssq[:b])
 
     def capture(self, b: int) -> None:
-        """Capture one greedy step for b sequences: the step's kernels, then one launch that
-        turns the argmax key into the next token and advances positions and history."""
+        """Capture one greedy step for b sequences: the step's kernels from h, then one launch
+        that turns the argmax key into the next token, advances positions and history, and
+        embeds the token into h for the next replay (the first replay's h comes from
+        generate())."""
         snap = (self.tokens.clone(), self.pos.clone(), self.lens.clone())
         self._launch_step(b)                       # warm: sizes every workspace
         self._advance(b)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._launch_step(b)
+            self._launch_step(b, embed=False)
             self._advance(b)
         self.graph, self.graph_batch = g, b
         for t, s0 in zip((self.tokens, self.pos, self.lens), snap):
@@ -343,6 +358,7 @@ class GraniteDecoder:
         self.pos[:b].copy_(start)
         self.lens[:b].copy_(start + 1)
         self.step_ctr.zero_()
+        self._embed(b)                             # each replay embeds the token after it
         logs = [] if record_logits else None
         torch.cuda.synchronize()
         t0 = time.perf_counter()

@@ -255,6 +255,28 @@ def decode_advance(keys: torch.Tensor, n_slots: int, tokens: torch.Tensor, pos: 
               _ptr(lens), _ptr(history), _ptr(step), hl, b, _stream())
 
 
+def decode_advance_embed(keys: torch.Tensor, n_slots: int, tokens: torch.Tensor,
+                         pos: torch.Tensor, lens: torch.Tensor, step: torch.Tensor,
+                         history: torch.Tensor | None, table: torch.Tensor, kind: str, vocab: int,
+                         hidden: int, h: torch.Tensor, ssq_out: torch.Tensor | None = None) -> None:
+    """`decode_advance`, then `embed` of the new tokens into h (and ssq_out), in one launch."""
+    if kind == "bf16":
+        _dev(table, "table", torch.bfloat16)
+        if table.numel() != vocab * hidden:
+            raise ValueError(f"table has {table.numel()} values, expected {vocab}x{hidden}")
+    else:
+        _tiles(table, kind, vocab // 32, hidden // 256, "table")
+    b = tokens.numel()
+    _dev(h, "h", torch.float32)
+    if h.numel() < b * hidden:
+        raise ValueError(f"h holds {h.numel()} values, expected {b}x{hidden}")
+    _ssq(ssq_out, "ssq_out", b, hidden // 16)
+    hl = 0 if history is None else history.shape[0]
+    _lib.call("q4nx_decode_advance_embed", _ptr(keys), int(n_slots), _ptr(tokens), _ptr(pos),
+              _ptr(lens), _ptr(history), _ptr(step), hl, b, KIND[kind], _ptr(table), vocab,
+              hidden, _ptr(h), _ptr(ssq_out), _stream())
+
+
 def round_bf16(x: torch.Tensor) -> torch.Tensor:
     """bf16 rounding of an fp32 device tensor on the GPU (round to nearest even)."""
     _dev(x, "x", torch.float32)

@@ -100,6 +100,15 @@ def test_fused_and_attention_argument_errors():
     assert rc == ERR_ARG and "kind" in msg
     rc, msg = rc_msg("q4nx_dequant_q4", fake, None, 1, 1, 0, 0, None)
     assert rc == ERR_ARG
+    rc, msg = rc_msg("q4nx_decode_advance_embed", fake, 64, fake, fake, fake, None, fake, 0, 65,
+                     8, fake, 1024, 512, fake, None, None)
+    assert rc == ERR_SHAPE and "batch" in msg              # at most 64 sequences
+    rc, msg = rc_msg("q4nx_decode_advance_embed", fake, 64, fake, fake, fake, None, fake, 0, 1,
+                     8, fake, 1000, 512, fake, None, None)
+    assert rc == ERR_SHAPE                                 # q8 tiles: vocab not a multiple of 32
+    rc, msg = rc_msg("q4nx_decode_advance_embed", fake, 64, fake, fake, fake, None, fake, 0, 1,
+                     8, None, 1024, 512, fake, None, None)
+    assert rc == ERR_ARG and "table" in msg
 
 
 def test_attention_record_splits_and_errors():

@@ -415,6 +415,46 @@ def test_embed_and_argmax(dev, kind):
     assert idx.tolist() == np.argmax(logits, axis=1).tolist()
 
 
+@pytest.mark.parametrize("kind,batch", [("q8", 1), ("q4", 3), ("bf16", 2)])
+def test_decode_advance_embed_equals_advance_then_embed(dev, kind, batch):
+    """The fused greedy-loop launch (argmax keys -> token, positions, history, then the token's
+    embedding row and its sums of squares) writes exactly what decode_advance followed by
+    embed writes, including a NaN row for a token past the vocabulary."""
+    rng = np.random.default_rng(19 + batch)
+    vocab, hid = 1024, 512
+    if kind == "bf16":
+        table = synth.random_bf16(rng, (vocab, hid))
+        tdev = bf16_dev(table, dev)
+    else:
+        tiles = (synth.q8_tiles if kind == "q8" else synth.q4_tiles)(rng, vocab, hid)
+        tdev = torch.from_numpy(tiles.reshape(-1)).to(dev)
+    n_slots = vocab // 16 + (1 if batch == 3 else 0)   # batch 3: one extra slot, a token past V
+    keys = torch.from_numpy(rng.integers(0, 1 << 62, (batch, n_slots)).astype(np.int64)).to(dev)
+    if batch == 3:
+        keys[2, -1] = (1 << 63) - 1 - 2000   # the largest key of row 2: token 2000 >= vocab
+
+    def state():
+        i32 = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)
+        return dict(tokens=i32([0] * batch), pos=i32(list(range(5, 5 + batch))),
+                    lens=i32([0] * batch), step=i32([1]),
+                    history=torch.full((4, batch), -1, dtype=torch.int32, device=dev),
+                    h=torch.zeros((batch, hid), dtype=torch.float32, device=dev),
+                    ss=torch.zeros((batch, hid // 16), dtype=torch.float32, device=dev))
+
+    a, f = state(), state()
+    ops.decode_advance(keys, n_slots, a["tokens"], a["pos"], a["lens"], a["step"], a["history"])
+    ops.embed(tdev, kind, a["tokens"], vocab, hid, out=a["h"], ssq_out=a["ss"])
+    ops.decode_advance_embed(keys, n_slots, f["tokens"], f["pos"], f["lens"], f["step"],
+                             f["history"], tdev, kind, vocab, hid, f["h"], f["ss"])
+    torch.cuda.synchronize()
+    for name in a:
+        x, y = a[name].cpu().numpy(), f[name].cpu().numpy()
+        assert np.array_equal(x.view(np.uint32) if x.dtype == np.float32 else x,
+                              y.view(np.uint32) if y.dtype == np.float32 else y), name
+    if batch == 3:
+        assert int(f["tokens"][2]) == 2000 and np.isnan(f["h"][2].cpu().numpy()).all()
+
+
 @pytest.mark.parametrize("hq,hkv,L,lmax,n_split,n_out", [
     (40, 8, 2112, 2176, 17, 2560),   # the 3B decode shape at the automatic split count
     (40, 8, 2112, 2176, 18, 2560),   # the most splits the merge holds
