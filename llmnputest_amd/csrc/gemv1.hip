@@ -368,17 +368,31 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
     xp[t][1] = h2_bits(h);
   }
 
-  // ---- 4. tiles
+  // sum of the K-group's x (the minimum's factor) per tile, with the activation scale undone
+  const int ur = 20 - se, ux = -se;
+  float Xs[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    float X = dot2_0(xp[t][0], 0x3C003C00u);
+    X = dot2(xp[t][1], 0x3C003C00u, X);
+    X += dpp<kDppHalfMirror>(X);
+    X += dpp<kDppXor2>(X);
+    X += dpp<kDppXor1>(X);
+    Xs[t] = __builtin_amdgcn_ldexpf(X, ux);
+  }
   uint32_t sl[4];   // v_perm selectors of the lane's byte slots
 #pragma unroll
   for (int j = 0; j < 4; ++j) sl[j] = sel_pair(j ^ gsw);
-  // r * 2^20 undoes the codes' 2^-20, and both sums carry the activation scale 2^se
-  const int ur = 20 - se, ux = -se;
+  // Everything above needs only the activations, which land before the weights: it runs
+  // while the weight stream is still in flight, and the work after the last weight byte
+  // is only the tile arithmetic below.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 4. tiles (r * 2^20 undoes the codes' 2^-20; the sums carry the activation scale)
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     const bool live = kt0 + t < a.k_t;   // always true for t = 0
-    float X = 0.f;
     if constexpr (KIND == 8) {
       // q8: the 16 bytes of load c are rows 0-15 at k = k0 + c; biased by 128 (xor 0x80) a
       // code is the fp16 subnormal (c + 128) * 2^-24. pv[4 dw + j] is row 4 dw + (j ^ gsw).
@@ -396,7 +410,6 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             pv[4 * dw + j] = dot2_acc(perm(bv[dw], av[dw], sl[j]), xc, pv[4 * dw + j], c == 0);
-        X = dot2_acc(xc, 0x3C003C00u, X, c == 0);
       }
       // partners: lane ^ 7 holds row s ^ 2 of this lane's slot s in slot s + 2 (s bit 1 clear),
       // lane ^ 2 holds it in slot s + 1 (s bit 0 clear); then rows gsw + 4v in t4[v]
@@ -413,11 +426,8 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
         const float keep = b0 ? t4[i + 2] : t4[i], send = b0 ? t4[i] : t4[i + 2];
         r2[i] = keep + dpp<kDppXor1>(send);
       }
-      X += dpp<kDppHalfMirror>(X);
-      X += dpp<kDppXor2>(X);
-      X += dpp<kDppXor1>(X);
       // s * sum(c x) = s * (sum((c + 128) x) - 128 sum(x))
-      const float Xb = 128.0f * __builtin_amdgcn_ldexpf(X, ux);
+      const float Xb = 128.0f * Xs[t];
       const float c0 = bf16lo(md[t]) * (__builtin_amdgcn_ldexpf(r2[0], ur + 4) - Xb);
       const float c1 = bf16hi(md[t]) * (__builtin_amdgcn_ldexpf(r2[1], ur + 4) - Xb);
       acc0 = t == 0 ? c0 : acc0 + (live ? c0 : 0.f);
@@ -443,7 +453,6 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
           pv[8 + 2 * j] = dot2_acc(perm(Lw, Ly, sl[j]), xc, pv[8 + 2 * j], c == 0);
           pv[8 + 2 * j + 1] = dot2_acc(perm(Hw, Hy, sl[j]), xc, pv[8 + 2 * j + 1], c == 0);
         }
-        X = dot2_acc(xc, 0x3C003C00u, X, c == 0);
       }
       // 16 rows over the 8 lanes of the K-group. Slot s holds row s ^ (2 gsw), and gsw
       // differs by 2 between lane and lane ^ 7 and by 1 between lane and lane ^ 2: the
@@ -465,12 +474,8 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
         const float keep = b0 ? t4[i + 2] : t4[i], send = b0 ? t4[i] : t4[i + 2];
         r2[i] = keep + dpp<kDppXor1>(send);
       }
-      X += dpp<kDppHalfMirror>(X);
-      X += dpp<kDppXor2>(X);
-      X += dpp<kDppXor1>(X);
-      const float Xs = __builtin_amdgcn_ldexpf(X, ux);
-      const float c0 = fmaf(bf16lo(md[t]), __builtin_amdgcn_ldexpf(r2[0], ur), bf16lo(mm[t]) * Xs);
-      const float c1 = fmaf(bf16hi(md[t]), __builtin_amdgcn_ldexpf(r2[1], ur), bf16hi(mm[t]) * Xs);
+      const float c0 = fmaf(bf16lo(md[t]), __builtin_amdgcn_ldexpf(r2[0], ur), bf16lo(mm[t]) * Xs[t]);
+      const float c1 = fmaf(bf16hi(md[t]), __builtin_amdgcn_ldexpf(r2[1], ur), bf16hi(mm[t]) * Xs[t]);
       acc0 = t == 0 ? c0 : acc0 + (live ? c0 : 0.f);
       acc1 = t == 0 ? c1 : acc1 + (live ? c1 : 0.f);
     } else {
@@ -489,7 +494,6 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
           pv[2 * j] = dot2_acc(perm(L1, L0, sl[j]), xc, pv[2 * j], c == 0);
           pv[2 * j + 1] = dot2_acc(perm(H1, H0, sl[j]), xc, pv[2 * j + 1], c == 0);
         }
-        X = dot2_acc(xc, 0x3C003C00u, X, c == 0);
       }
       // 8 rows over the 8 lanes of the K-group, as above; lane ^ 1 shares rows 2 gsw, +1
       float t4[4], t2[2];
@@ -499,11 +503,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
       for (int v = 0; v < 2; ++v) t2[v] = t4[v] + dpp<kDppXor2>(t4[v + 2]);
       const float keep = b0 ? t2[1] : t2[0], send = b0 ? t2[0] : t2[1];
       const float r1 = keep + dpp<kDppXor1>(send);
-      X += dpp<kDppHalfMirror>(X);
-      X += dpp<kDppXor2>(X);
-      X += dpp<kDppXor1>(X);
-      const float Xs = __builtin_amdgcn_ldexpf(X, ux);
-      const float c0 = fmaf(bf16lo(md[t]), __builtin_amdgcn_ldexpf(r1, ur), bf16lo(mm[t]) * Xs);
+      const float c0 = fmaf(bf16lo(md[t]), __builtin_amdgcn_ldexpf(r1, ur), bf16lo(mm[t]) * Xs[t]);
       acc0 = t == 0 ? c0 : acc0 + (live ? c0 : 0.f);
     }
   }
