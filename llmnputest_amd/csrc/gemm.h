@@ -57,10 +57,14 @@ size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows, const P
 bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes);
 // The prefill kernel (gemm_pf.hip) takes plain contractions from this many rows.
 constexpr int kPrefillRows = 128;
-// whether a launch of op `op` described by `a` goes to the prefill kernel
+// workspace bytes the prefill kernel keeps its per-group sums of x in (past the counters,
+// the split records and the normalised rows), or 0 when the shape does not take that kernel
+size_t pf_ws_bytes(int n_tile_rows, int k_t, int m_rows);
+// whether a launch of op `op` described by `a` has the prefill kernel's shape
 bool pf_use(int op, const GemmArgs& a);
-// launches `a` on the prefill kernel (whole K per workgroup, no split)
-void pf_launch(int kind, const GemmArgs& a, hipStream_t st);
+// launches `a` on the prefill kernel (whole K per workgroup, no split): the per-group sums
+// of x into `sums` (pf_ws_bytes of them, 256-byte aligned), then the contraction
+void pf_launch(int kind, const GemmArgs& a, void* sums, hipStream_t st);
 // launches `a` (all but the split-K fields filled in); returns Q4NX_OK or an error code
 int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_bytes,
                 const Policy& P, hipStream_t st, const char* what);

@@ -475,9 +475,12 @@ bool mfma_use(int kind, int rows, const Policy& P) {
 }
 
 size_t mfma_ws_bytes(int kind, int op, int n_units, int k_t, int m_rows, const Policy& P) {
-  // room for the split-K records and for the normalised rows of an RMSNorm prologue
+  // room for the split-K records, for the normalised rows of an RMSNorm prologue and, for a
+  // plain prompt block, for the prefill kernel's per-group sums of x
   const size_t split = split_part_bytes(plan_gemm(kind, op, n_units, k_t, m_rows, P));
-  return Q4NX_WS_COUNTER_BYTES + align256(split) + align256((size_t)m_rows * k_t * kTileK * 2);
+  const size_t pf = op == GOP_PLAIN ? pf_ws_bytes(n_units, k_t, m_rows) : 0;
+  return Q4NX_WS_COUNTER_BYTES + align256(split) + align256((size_t)m_rows * k_t * kTileK * 2) +
+         pf;
 }
 
 bool mfma_norm_fits(int k_t, int m_rows, size_t ws_bytes) {
@@ -520,8 +523,11 @@ int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_
     a.x = xn;
     a.x_stride = xs;
   }
-  if (pf_use(op, a)) {   // a prompt block: the scale-in-operand prefill kernel
-    pf_launch(kind, a, st);
+  // a prompt block: the prefill kernel, when the workspace holds its per-group sums of x
+  // (past the counters, the split records and the normalised rows); else the batched kernel
+  const size_t pf_off = Q4NX_WS_COUNTER_BYTES + align256(split) + xn_b;
+  if (pf_use(op, a) && ws_ok && ws_bytes >= pf_off + pf_ws_bytes(a.n_tr[0], a.k_t, a.m_rows)) {
+    pf_launch(kind, a, (uint8_t*)ws + pf_off, st);
     return check_launch(what);
   }
   a.ksplit = p.ksplit;
@@ -554,7 +560,10 @@ size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows,
   if ((kind != Q4NX_KIND_Q4 && kind != Q4NX_KIND_Q8) || n_tile_rows < 1 || k_tiles < 1 ||
       m_rows < 1 || !resolve_policy_quiet(policy, &P))
     return 0;
-  return gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, n_tile_rows, k_tiles, m_rows, P));
+  const size_t split = gemm_split_bytes(plan_gemm(kind, GOP_PLAIN, n_tile_rows, k_tiles, m_rows, P));
+  const size_t pf = pf_ws_bytes(n_tile_rows, k_tiles, m_rows);
+  // the prefill kernel's sums sit past the counters and the split records
+  return pf ? (split ? split : Q4NX_WS_COUNTER_BYTES) + pf : split;
 }
 
 int q4nx_gemm(int kind, const uint8_t* w, int n_tile_rows, int k_tiles, const uint16_t* x,

@@ -162,22 +162,33 @@ def test_gemm_q8_lm_head_prefill(dev):
 
 
 # ------------------------------------------------------------------ prompt blocks (prefill kernel)
-# Launches of at least 512 workgroups of four tile-rows x 128 rows go to the prefill kernel
-# (scale and minimum folded into exact bf16 MFMA operands); smaller ones stay on the batched
-# kernel above.
+# Launches that fill the chip go to the prefill kernel (raw codes on the matrix cores, the
+# group scale on the VALU, the minimum as a contraction over per-group sums of x): blocks of
+# 128 rows from 768 workgroups of four tile-rows, else 64-row blocks from 512; smaller
+# launches stay on the batched kernel above.
 
-def _pf_workgroups(m, n):
-    return -(-(n // 32) // 4) * -(-m // 128)
+def _pf_workgroups(m, n, rows=128):
+    return -(-(n // 32) // 4) * -(-m // rows)
+
+
+def _pf_block_rows(m, n):
+    """Row-block size the library picks (0: not the prefill kernel)."""
+    if m >= 128 and _pf_workgroups(m, n, 128) >= 768:
+        return 128
+    if m >= 128 and _pf_workgroups(m, n, 64) >= 512:
+        return 64
+    return 0
 
 
 @pytest.mark.parametrize("kind", ["q4", "q8"])
 @pytest.mark.parametrize("m,n,k", [
     (4100, 2016, 512),   # 63 tile-rows: the last workgroup's fourth wave has none; ragged rows
     (2048, 4096, 1024),
+    (1544, 8192, 768),   # 128-row blocks; ragged rows, a partial chunk of groups (3 K-tiles)
 ])
 def test_gemm_prefill_parity(dev, kind, m, n, k):
     """Every row against the float64 oracle at the GEMV bar."""
-    assert _pf_workgroups(m, n) >= 512
+    assert _pf_block_rows(m, n) > 0
     raw, rng = _tiles(kind, n, k, 21 + m)
     x = synth.random_bf16(rng, (m, k))
     y = ops.gemm(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
@@ -196,11 +207,12 @@ def test_gemm_prefill_long_k(dev):
 
 
 @pytest.mark.parametrize("kind", ["q4", "q8"])
-def test_gemm_prefill_onehot_exact(dev, kind):
-    """One-hot rows reproduce the float32 dequantised column bit for bit: hi + lo carries c d
-    (q4) or q s (q8) exactly and the minimum joins in one rounding."""
-    n, k, m = 2048, 1024, 4096
-    assert _pf_workgroups(m, n) >= 512
+@pytest.mark.parametrize("n,m", [(2048, 4096), (8192, 1536)])   # 64- and 128-row blocks
+def test_gemm_prefill_onehot_exact(dev, kind, n, m):
+    """One-hot rows reproduce the float32 dequantised column bit for bit: d (16 + c) (q4) or
+    s (q + 128) (q8) is exact, and so is its sum with the minimum term."""
+    k = 1024
+    assert _pf_block_rows(m, n) == (64 if n == 2048 else 128)
     raw, _ = _tiles(kind, n, k, 3)
     cols = np.arange(m) * 5 % k
     x = np.zeros((m, k), np.float32)
@@ -211,11 +223,32 @@ def test_gemm_prefill_onehot_exact(dev, kind):
     assert np.array_equal(y.view(np.uint32), wm[:, cols].T.copy().view(np.uint32))
 
 
+@pytest.mark.parametrize("dist", ["student_t2", "outliers"])
+def test_gemm_prefill_heavy_tailed(dev, dist):
+    """Heavy-tailed activations on both row-block sizes: a few entries dwarf the rest of their
+    32-K group, so the group sums S carry most of the minimum term and the scaled code sums
+    cancel against it."""
+    k = 1024
+    for m, n in ((1536, 8192), (2048, 2048)):
+        assert _pf_block_rows(m, n) > 0
+        raw, rng = _tiles("q4", n, k, 31 + m)
+        if dist == "student_t2":
+            xf = rng.standard_t(2.0, (m, k)).astype(np.float32)
+        else:
+            xf = rng.standard_normal((m, k)).astype(np.float32)
+            hit = rng.random((m, k)) < 1e-3
+            xf[hit] *= np.float32(1e4)
+        x = qo.bf16_round(xf)
+        y = ops.gemm(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+        ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+        _check_rows(y, ref)
+
+
 @pytest.mark.parametrize("scale", [1e-30, 1e30])
 def test_gemm_prefill_activation_range_residual_stride(dev, scale):
     """Extreme activation ranges, rows with a stride longer than K and a residual."""
     m, n, k = 4096, 2048, 512
-    assert _pf_workgroups(m, n) >= 512
+    assert _pf_block_rows(m, n) > 0
     raw, rng = _tiles("q4", n, k, 14)
     xf = rng.standard_normal((m, k + 64)).astype(np.float32) * np.float32(scale)
     xfull = qo.bf16_round(xf)
