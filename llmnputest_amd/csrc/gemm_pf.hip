@@ -38,7 +38,6 @@ namespace q4nx {
 namespace {
 
 constexpr int kPfWaves = 4;
-constexpr int kPfRowPad = 32;      // floats per staged output row (the block of four waves fits 64 KB)
 constexpr int kPfChunkTiles = 4;   // K-tiles (32 groups) per minimum-term contraction
 constexpr int kPfMT = 8;           // m-tiles (16 rows) per workgroup
 
@@ -82,6 +81,10 @@ __device__ __forceinline__ void pf_build(const PfRaw& r, PfOps& o) {
   o.d[0] = bf16lo(r.sc);
   o.d[1] = bf16hi(r.sc);
 }
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
+// (vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, so they are not waited on)
+constexpr int vm_wait(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) & 3) << 14; }
 
 // (x0, x1) = t[0] + t[1] + t[2] exactly, as packed bf16 pairs (x0 in the low halves)
 __device__ __forceinline__ void split3(float x0, float x1, uint32_t (&t)[3]) {
@@ -147,9 +150,12 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
   constexpr int MB = 16 * MT;
   constexpr int UPT = MB * 4 / 256;        // 16-byte x units per thread and 32-K step
   constexpr int XB = MB * 4 * 16;          // bytes of one staged step of x
-  constexpr int XD = 2;                    // steps of x in flight in registers (divides the 8 steps of a tile)
+  constexpr int XD = 3;                    // steps of x in flight to LDS ahead of their step
   constexpr int NU = KIND == 4 ? 3 : 1;    // bf16 terms of u
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // The x ring: four step buffers, step t in buffer t % 4 (a position the unrolled steps of a
+  // K-tile know at compile time), and the four waves' tile slots.
+  __shared__ __attribute__((aligned(16))) uint8_t xr0[XB], xr1[XB], xr2[XB], xr3[XB];
+  __shared__ __attribute__((aligned(16))) uint8_t slots[kPfWaves * SLOT];
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -159,8 +165,7 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
   const int trc = live ? tr : n_tr - 1;
   const int m0 = blockIdx.y * MB;
   const uint8_t* wr = a.w[0] + (size_t)trc * a.k_t * TB;
-  uint8_t* xbuf = lds;                            // three staged steps of x
-  uint8_t* slot = lds + 3 * XB + wave * SLOT;     // this wave's weight tile
+  uint8_t* slot = slots + wave * SLOT;            // this wave's weight tile
   const int c = l & 15, s = l >> 4;
   const int n_steps = a.k_t * 8;
   const int n_ch = (a.k_t + kPfChunkTiles - 1) / kPfChunkTiles;
@@ -186,16 +191,33 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
     const int m = min(m0 + 16 * (u >> 6) + (u & 15), a.m_rows - 1);
     xsrc[j] = a.x + (int64_t)m * a.x_stride + 8 * ((u >> 4) & 3);
   }
-  auto x_load = [&](u32x4_t (&g)[UPT], int step) {
-    const int st = step < n_steps ? step : n_steps - 1;   // past the end: a re-read
+  auto xring = [&](int b) -> uint8_t* { return b == 0 ? xr0 : b == 1 ? xr1 : b == 2 ? xr2 : xr3; };
+  // x of a step straight from memory into its ring buffer (global_load_lds_dwordx4: lane l's
+  // 16 bytes land at the wave's base in M0 + 16 l, which is this layout). Issued as inline
+  // assembly: the compiler would otherwise wait for every direct load in flight before each
+  // read of the ring. The waits at the end of each step order the loads instead (vmcnt
+  // counts them, and loads complete in issue order, so a wait the compiler places for another
+  // load can only wait longer than it needs).
+  auto x_load = [&](int step, uint8_t* buf) {
+    const int st = step < n_steps ? step : n_steps - 1;   // past the end: a re-read, never used
     const int k = (st >> 3) * 256 + (st & 7) * 32;
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)buf +
+                          16 * 64 * wave;
 #pragma unroll
-    for (int j = 0; j < UPT; ++j) g[j] = *(const u32x4_t*)(xsrc[j] + k);
+    for (int j = 0; j < UPT; ++j)
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                   :: "v"(xsrc[j] + k), "s"(base + 16 * 256 * j) : "memory", "m0");
   };
-  auto x_store = [&](const u32x4_t (&g)[UPT], int buf) {
+
+  // Pipeline: during step s the MFMAs of s run while this wave builds the weight operands of
+  // s + 1 from its tile slot and loads x of s + XD into the ring; one barrier ends each step.
+  // The first steps' x and the first tile go out before the minimum term, whose own loads
+  // then wait alongside them.
+  u32x4_t pf[NLD];
 #pragma unroll
-    for (int j = 0; j < UPT; ++j) *(u32x4_t*)(xbuf + buf * XB + 16 * (tid + 256 * j)) = g[j];
-  };
+  for (int i = 0; i < NLD; ++i) pf[i] = *(const u32x4_t*)(wr + ld_off[i]);
+#pragma unroll
+  for (int t = 0; t < XD; ++t) x_load(t, xring(t));
 
   // ---- the minimum term first: acc = sum_g u S over every chunk of 32 groups. The lane's
   // B operand holds u of its two columns at groups 32 ch + 8 s + j, read from the
@@ -257,28 +279,14 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
     }
   }
 
-  // Pipeline: during step s the MFMAs of s run while this wave builds the weight operands of
-  // s + 1 from its tile slot, stages x of s + 2 into LDS and loads x of s + 2 + XD; one
-  // barrier ends each step.
-  u32x4_t pf[NLD];
-  u32x4_t gx[XD][UPT];   // x of steps s + 2 .. s + 1 + XD at step s, step t in gx[t % XD]
   {
-    u32x4_t g0[UPT], g1[UPT];
-    x_load(g0, 0);
-    x_load(g1, 1);
-#pragma unroll
-    for (int t = 2; t < 2 + XD; ++t) x_load(gx[t % XD], t);
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) pf[i] = *(const u32x4_t*)(wr + ld_off[i]);
+    // every load so far has landed (the minimum term waited for its own, issued after them)
+    __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
     for (int i = 0; i < NLD; ++i) *(u32x4_t*)(slot + 16 * (64 * i + l)) = pf[i];
-    {
-      const size_t off = (size_t)(a.k_t > 1 ? 1 : 0) * TB;
+    const size_t off = (size_t)(a.k_t > 1 ? 1 : 0) * TB;
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) pf[i] = *(const u32x4_t*)(wr + off + ld_off[i]);
-    }
-    x_store(g0, 0);
-    x_store(g1, 1);
+    for (int i = 0; i < NLD; ++i) pf[i] = *(const u32x4_t*)(wr + off + ld_off[i]);
   }
   __syncthreads();
   // the next step's operand data is read from LDS one step ahead (in the step before, ahead
@@ -287,7 +295,7 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
   PfRaw raw;
   pf_read<KIND>(slot, tr_off, meta_off, 0, raw);
   pf_build<KIND>(raw, ops[0]);
-  u32x4_t x0 = *(const u32x4_t*)(xbuf + 16 * l);
+  u32x4_t x0 = *(const u32x4_t*)(xr0 + 16 * l);
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
 
   for (int kt = 0; kt < a.k_t; ++kt) {
@@ -296,7 +304,8 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
       const int step = kt * 8 + kb;
       const int cur = kb & 1, nxt = cur ^ 1;
       // ---- this step's groups: P on the matrix cores, its scale on the VALU
-      const uint8_t* xb = xbuf + (step % 3) * XB;
+      x_load(step + XD, xring((kb + XD) & 3));
+      const uint8_t* xb = xring(kb & 3);
       if (kb < 7) pf_read<KIND>(slot, tr_off, meta_off, kb + 1, raw);
       // Pipelined by m-tile, fenced so that the schedule holds: x of m-tile mt + 1 is read
       // from LDS, the two MFMAs of mt issue, then m-tile mt - 1's P is scaled on the VALU
@@ -328,9 +337,6 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
           if (FENCE > 0 && mt % FENCE == FENCE - 1) __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // ---- x of step + 2 into LDS, x of step + 2 + XD into the freed registers
-      x_store(gx[(kb + 2) % XD], (step + 2) % 3);
-      x_load(gx[(kb + 2) % XD], step + 2 + XD);
       // ---- the next step's operands (the next tile into the slot first at a tile boundary;
       // past the last step they are built from re-read data and not used)
       if (kb == 7) {
@@ -342,53 +348,64 @@ __global__ __launch_bounds__(256) void gemm_pf_kernel(GemmArgs a, const u32x4_t*
         pf_read<KIND>(slot, tr_off, meta_off, 0, raw);
       }
       pf_build<KIND>(raw, ops[nxt]);
-      x0 = *(const u32x4_t*)(xbuf + ((step + 1) % 3) * XB + 16 * l);
-      // step + 2's x is in LDS for everyone once all have passed here; the buffer it took was
-      // last read during step - 1, before every thread passed the previous barrier
+      x0 = *(const u32x4_t*)(xring((kb + 1) & 3) + 16 * l);
+      // This thread's direct loads of step + 2's x must have landed before the barrier, after
+      // which everyone reads them. Loads complete in issue order, and issued after them are
+      // only step + 3's x (at the start of this step) and the next tile's prefetch when this
+      // step or the one before ended a K-tile (kb 7, after its x load): wait for all but those.
+      // (A read of the buffer would make the compiler wait for every direct load in flight.)
+      if (kb == 0 || kb == 7) __builtin_amdgcn_s_waitcnt(vm_wait(UPT + NLD));
+      else __builtin_amdgcn_s_waitcnt(vm_wait(UPT));
       __syncthreads();
     }
   }
 
-  // ---- outputs: every wave has finished with LDS (the last barrier), then each writes its
-  // [MB][32] block (row m = 16 mt + 4 s + e, column of operand h at lane c) and reads it
-  // back as 128-byte row segments
-  float* blk = (float*)lds + wave * MB * kPfRowPad;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int col = KIND == 4 ? (c >> 3) * 16 + 2 * (c & 7) + h : h * 16 + c;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) blk[(16 * mt + 4 * s + e) * kPfRowPad + col] = acc[mt][h][e];
-    }
-  if (!live) return;
+  // ---- outputs, through the x ring once every wave is done with it and the direct loads of
+  // the steps past the end have landed (each wave waits for its own, then the barrier): wave w
+  // stages half of its [MB][32] block at a time in buffer w (MB/2 rows of 128 bytes = XB;
+  // row m = 16 mt + 4 s + e, column of operand h at lane c) and reads it back as 128-byte
+  // row segments
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  __syncthreads();
+  float* blk = (float*)xring(wave);
   const int q = l & 7, r0 = l >> 3;   // 8 lanes per 32-float row, 8 rows per pass
 #pragma unroll
-  for (int p = 0; p < MB / 8; ++p) {
-    const int r = 8 * p + r0, m = m0 + r;
-    if (m < a.m_rows) {
-      float4 v = *(const float4*)(blk + r * kPfRowPad + 4 * q);
-      const int64_t o = (int64_t)m * a.y_stride + (int64_t)tr * 32 + 4 * q;
-      if (a.residual != nullptr) {
-        const float4 rr = *(const float4*)(a.residual + o);
-        v.x += rr.x;
-        v.y += rr.y;
-        v.z += rr.z;
-        v.w += rr.w;
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int mt = half * MT / 2; mt < (half + 1) * MT / 2; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int col = KIND == 4 ? (c >> 3) * 16 + 2 * (c & 7) + h : h * 16 + c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          blk[(16 * (mt - half * MT / 2) + 4 * s + e) * 32 + col] = acc[mt][h][e];
       }
-      *(float4*)(a.y + o) = v;
+    if (live) {
+#pragma unroll
+      for (int p = 0; p < MB / 16; ++p) {
+        const int r = 8 * p + r0, m = m0 + half * (MB / 2) + r;
+        if (m < a.m_rows) {
+          float4 v = *(const float4*)(blk + r * 32 + 4 * q);
+          const int64_t o = (int64_t)m * a.y_stride + (int64_t)tr * 32 + 4 * q;
+          if (a.residual != nullptr) {
+            const float4 rr = *(const float4*)(a.residual + o);
+            v.x += rr.x;
+            v.y += rr.y;
+            v.z += rr.z;
+            v.w += rr.w;
+          }
+          *(float4*)(a.y + o) = v;
+        }
+      }
     }
   }
 }
 
 template <int KIND, int MT>
 void pf_go(const GemmArgs& a, const u32x4_t* sums, hipStream_t st) {
-  constexpr int lds_slots = 3 * 16 * MT * 4 * 16 + kPfWaves * GemmFmt<KIND>::kSlot;
-  constexpr int lds_out = kPfWaves * 16 * MT * kPfRowPad * 4;
-  constexpr int lds = lds_slots > lds_out ? lds_slots : lds_out;
   const dim3 grid((unsigned)((a.n_tr[0] + kPfWaves - 1) / kPfWaves),
                   (unsigned)((a.m_rows + 16 * MT - 1) / (16 * MT)));
-  hipLaunchKernelGGL((gemm_pf_kernel<KIND, MT>), grid, dim3(256), lds, st, a, sums);
+  hipLaunchKernelGGL((gemm_pf_kernel<KIND, MT>), grid, dim3(256), 0, st, a, sums);
 }
 
 // m-tiles the sums cover (whole 128-row blocks, enough for either block size) and chunks of 32
