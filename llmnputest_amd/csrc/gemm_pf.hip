@@ -22,12 +22,12 @@
 // tile-rows; wave w owns tile-row 4*blockIdx.x + w for the whole K, so nothing is merged
 // across waves or workgroups. Each wave stages its tile in its own LDS slot (the transposing
 // LDS read needs it there) while the next tile is in flight to registers. The block's x is
-// loaded once for the four waves: every thread carries its share of the next steps in
-// registers and stores one step into a ring of three LDS buffers per step (one barrier per
-// step), laid out so that each m-tile's A operand is one conflict-free 16-byte LDS read per
-// lane. The minimum term runs first, from the tile-row's scales and minima (re-read: a
-// fifth of its bytes) and the pre-pass's sums, so the main loop carries no state for it. The
-// outputs leave through LDS as 128-byte row segments.
+// loaded once for the four waves, by direct global-to-LDS loads into a ring of four step
+// buffers, three steps ahead of their use (one barrier per step), laid out so that each
+// m-tile's A operand is one conflict-free 16-byte LDS read per lane. The minimum term runs
+// first, from the tile-row's scales and minima (re-read: a fifth of its bytes) and the
+// pre-pass's sums, so the main loop carries no state for it. The outputs leave through the
+// ring as 128-byte row segments.
 
 #include "common.h"
 #include "gemm.h"
