@@ -259,3 +259,35 @@ def test_gemm_prefill_activation_range_residual_stride(dev, scale):
     ref = qo.gemv(raw, "q4", np.ascontiguousarray(xfull[:, :k]), n // 32, k // 256,
                   acc=np.float64) + res
     _check_rows(y, ref)
+
+
+@pytest.mark.parametrize("kind", ["q4", "q8"])
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 256), (1536, 8192, 512), (2048, 4096, 768)])
+def test_gemm_prefill_short_k(dev, kind, m, n, k):
+    """One to three K-tiles per tile-row: the first tile's reload, the clamped prefetch of the
+    tile after the last and the steps of x past the end all stay unused."""
+    assert _pf_block_rows(m, n) > 0
+    raw, rng = _tiles(kind, n, k, 41 + k)
+    x = synth.random_bf16(rng, (m, k))
+    y = ops.gemm(_dev_u8(raw, dev), kind, _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    _check_rows(y, ref)
+
+
+def test_gemm_prefill_without_workspace(dev):
+    """A prompt block with no workspace (NULL, 0), or one too small for the per-group sums of
+    x, runs on the batched kernel instead: every row at the same bar."""
+    from llmnputest_amd import _lib
+    m, n, k = 2048, 4096, 512
+    assert _pf_block_rows(m, n) > 0
+    raw, rng = _tiles("q4", n, k, 43)
+    x = synth.random_bf16(rng, (m, k))
+    w, xd = _dev_u8(raw, dev), _dev_bf16(x, dev)
+    ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
+    need = _lib.lib().q4nx_gemm_ws_bytes(4, n // 32, k // 256, m, None)
+    small = torch.empty(need // 2, dtype=torch.uint8, device=dev)
+    for wp, wn in ((None, 0), (small.data_ptr(), small.numel())):
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        _lib.call("q4nx_gemm", 4, w.data_ptr(), n // 32, k // 256, xd.data_ptr(), k, m,
+                  y.data_ptr(), n, None, wp, wn, None, ops._stream())
+        _check_rows(y.cpu().numpy(), ref)
