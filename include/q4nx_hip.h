@@ -152,8 +152,9 @@ int q4nx_gemv_attn_q4(const uint8_t *w, int n_tile_rows, const float *att_rec, i
  *   y, residual: fp32 [m_rows][y_stride], y_stride % 4 == 0, 16-byte aligned.
  *   ws: workspace of q4nx_gemm_ws_bytes(...) bytes, zeroed once (K is split across
  *   workgroups when the launch has few of them; a prompt block that fills the chip keeps
- *   per-group sums of x there for the prefill kernel); NULL runs without either (a prompt
- *   block then takes the batched kernel). */
+ *   per-group sums of x there for the prefill kernel); NULL, or a workspace smaller than
+ *   q4nx_gemm_ws_bytes asks for, runs without either (a prompt block then takes the batched
+ *   kernel, whole K per workgroup). */
 size_t q4nx_gemm_ws_bytes(int kind, int n_tile_rows, int k_tiles, int m_rows,
                           const q4nx_policy *policy);
 int q4nx_gemm(int kind, const uint8_t *w, int n_tile_rows, int k_tiles, const uint16_t *x,
