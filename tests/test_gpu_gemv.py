@@ -263,3 +263,16 @@ def test_gemv_heavy_tailed_activations(dev, kpath, n, k, dist):
     for b in range(2):
         rel, cos = qo.metrics(y2[b], ref[b])
         assert rel < REL and cos > COS, (b, rel, cos)
+
+
+@pytest.mark.parametrize("k_t", [64, 65])
+def test_gemv_longest_k(dev, kpath, k_t):
+    """K = 16384 (64 K-tiles: sixteen waves of four K-tiles, the longest row a row-block
+    workgroup covers) and one K-tile more (the general kernel takes it at one row)."""
+    n = 256
+    raw, rng = _tiles("q4", n, 256 * k_t, 70 + k_t)
+    x = synth.random_bf16(rng, 256 * k_t)
+    y = ops.gemv(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k_t).cpu().numpy()
+    ref = qo.gemv(raw, "q4", x, n // 32, k_t, acc=np.float64)
+    rel, cos = qo.metrics(y, ref)
+    assert rel < REL and cos > COS, (rel, cos)
