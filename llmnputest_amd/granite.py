@@ -16,8 +16,11 @@ At one sequence the attention launch only publishes its split records
 (q4nx_gemv_attn_q4), which gives the same bits sooner. Then one lm_head launch (q8 or q4;
 final RMSNorm fused as its prologue, one order-preserving (max, row) key per 16-row block in
 its epilogue) and one bookkeeping launch that reduces the keys to the next token and
-advances positions. A whole step is captured once in a HIP graph and replayed; the greedy
-loop never leaves the device. Every launch carries the decoder's own launch policy.
+advances positions. A whole step is captured once in a HIP graph, and so are
+GRAPH_STEPS steps back to back in a second graph (each graph launch leaves the GPU idle for
+about 6-7 us, so generate() replays the longer graph and the one-step graph only for the
+remainder, or for every step when it records logits); the greedy loop never leaves the
+device. Every launch carries the decoder's own launch policy.
 
 Conventions (the reference fixes none of them): fp32 residual stream, pre-norm
 Llama/Granite order, final RMSNorm; the embedding of token t is row t of the stored
@@ -36,6 +39,9 @@ import torch
 from . import ops
 from .ops import Policy
 from .q4nx import Q4_TILE_BYTES, Q8_TILE_BYTES, Q4NX, TILE_BYTES, check_stored_shape, projection_shape
+
+# greedy steps per replay of the multi-step decode graph
+GRAPH_STEPS = 16
 
 
 @dataclass(frozen=True)
@@ -233,7 +239,8 @@ class GraniteDecoder:
         self.history = torch.zeros((self.max_len, b), dtype=torch.int32, device=dev)
         self.step_ctr = torch.zeros(1, dtype=torch.int32, device=dev)
         self.ws = ops.Workspace(ops.WS_COUNTER_BYTES + (64 << 20), device=dev)
-        self.graph: torch.cuda.CUDAGraph | None = None
+        self.graph: torch.cuda.CUDAGraph | None = None         # one greedy step
+        self.graph_steps: torch.cuda.CUDAGraph | None = None   # GRAPH_STEPS greedy steps
         self.graph_batch = 0
         self.calls = 0
         self.seconds = 0.0
@@ -326,17 +333,24 @@ class GraniteDecoder:
         """Capture one greedy step for b sequences: the step's kernels from h, then one launch
         that turns the argmax key into the next token, advances positions and history, and
         embeds the token into h for the next replay (the first replay's h comes from
-        generate())."""
-        snap = (self.tokens.clone(), self.pos.clone(), self.lens.clone())
+        generate()). A second graph holds GRAPH_STEPS such steps back to back: the same
+        launches in the same order, so replaying it once equals GRAPH_STEPS replays of the
+        first."""
+        snap = (self.tokens.clone(), self.pos.clone(), self.lens.clone(), self.step_ctr.clone())
         self._launch_step(b)                       # warm: sizes every workspace
         self._advance(b)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self._launch_step(b, embed=False)
-            self._advance(b)
-        self.graph, self.graph_batch = g, b
-        for t, s0 in zip((self.tokens, self.pos, self.lens), snap):
+        graphs = []
+        for steps in (1, GRAPH_STEPS):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(steps):
+                    self._launch_step(b, embed=False)
+                    self._advance(b)
+            graphs.append(g)
+        self.graph, self.graph_steps = graphs
+        self.graph_batch = b
+        for t, s0 in zip((self.tokens, self.pos, self.lens, self.step_ctr), snap):
             t.copy_(s0)
 
     def generate(self, first_tokens, start_pos, n_new: int, record_logits: bool = False):
@@ -362,10 +376,15 @@ class GraniteDecoder:
         logs = [] if record_logits else None
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(n_new):
-            self.graph.replay()
-            if record_logits:
+        if record_logits:
+            for _ in range(n_new):
+                self.graph.replay()
                 logs.append(self.logits[:b].clone())
+        else:
+            for _ in range(n_new // GRAPH_STEPS):
+                self.graph_steps.replay()
+            for _ in range(n_new % GRAPH_STEPS):
+                self.graph.replay()
         torch.cuda.synchronize()
         self.seconds += time.perf_counter() - t0
         self.calls += n_new

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from llmnputest_amd import ops, q4nx, synth
+from llmnputest_amd import granite, ops, q4nx, synth
 from llmnputest_amd.granite import GraniteConfig, GraniteDecoder, GraniteWeights
 from oracle import cpu_oracle
 from oracle import decode_oracle as do
@@ -103,6 +103,33 @@ def test_decode_steps_vs_oracle(dev, kpath, n_layers, batch, ctx, n_new):
     cfg = GraniteConfig(n_layers=n_layers)
     w = GraniteWeights.synthetic(cfg, seed=11, device=dev)
     run_and_check(w, batch, ctx, n_new, policy=ops.current_policy())
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_generate_multi_step_graph_matches_one_step(dev, batch):
+    """generate() without logits replays the GRAPH_STEPS-step graph, then the one-step graph
+    for the remainder; with logits it replays the one-step graph every step. Both issue the
+    same launches in the same order: tokens, final logits, residual stream, K/V caches and
+    positions agree bit for bit."""
+    cfg = GraniteConfig(n_layers=2, vocab=8192)
+    w = GraniteWeights.synthetic(cfg, seed=19, device=dev)
+    n_new = granite.GRAPH_STEPS + 3
+    first = np.arange(batch, dtype=np.int32) * 97 + 5
+    start = np.full(batch, 300, np.int32) - np.arange(batch, dtype=np.int32) * 7
+    runs = []
+    for record in (True, False):
+        dec = GraniteDecoder(w, max_batch=batch, max_len=512, device=dev)
+        dec.seed_cache(300, seed=3)
+        dec.generate(first, start, 2)                        # capture and warm both graphs
+        dec.seed_cache(300, seed=3)
+        toks, _ = dec.generate(first, start, n_new, record_logits=record)
+        torch.cuda.synchronize()
+        state = [dec.logits[:batch], dec.h[:batch], dec.pos[:batch], dec.lens[:batch],
+                 *dec.k_cache, *dec.v_cache]
+        runs.append((toks, [t.contiguous().view(torch.int8).cpu().numpy() for t in state]))
+    assert np.array_equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("lm_kind,stored_embed", [("q4", True), ("q4", False), ("q8", True)])
