@@ -203,7 +203,7 @@ class GraniteDecoder:
     """Decode state for up to `max_batch` sequences of up to `max_len` positions.
 
     `step()` runs one token for every sequence at its own position; `generate()` runs the
-    greedy loop on the device from a HIP graph of one step."""
+    greedy loop on the device from HIP graphs of GRAPH_STEPS steps and of one step."""
 
     def __init__(self, weights: GraniteWeights, max_batch: int = 1, max_len: int = 4096,
                  device="cuda", fused_attn_o: bool = True, attn_splits: int = 0,
