@@ -108,34 +108,36 @@ __global__ __launch_bounds__(256) void round_bf16_kernel(const float* __restrict
 // h[b][c] = row tokens[b] of a [vocab][hidden] table: bf16 (KIND 16), or q4 / q8 tiles
 // dequantised as tools/q4nx.py:127-143 does (q4: code * d + m with one rounding, q8: code * s).
 template <int KIND>
-__device__ __forceinline__ float embed_value(const uint8_t* __restrict__ w, int t, int c,
-                                             int vocab, int hidden) {
-  float v = __builtin_nanf("");                   // a token out of range gives a NaN row
-  if (t >= 0 && t < vocab) {
-    if constexpr (KIND == Q4NX_KIND_BF16) {
-      v = bf16_to_f32(((const uint16_t*)w)[(size_t)t * hidden + c]);
+__device__ __forceinline__ float embed_value_of(const uint8_t* __restrict__ w, int t, int c,
+                                                int hidden) {
+  if constexpr (KIND == Q4NX_KIND_BF16) {
+    return bf16_to_f32(((const uint16_t*)w)[(size_t)t * hidden + c]);
+  } else {
+    const int k_t = hidden / 256;
+    const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
+    const int kt = c >> 8, k = c & 255, kb = k >> 5;
+    const int g = kb * 32 + rb * 16 + r;
+    const int i = rb * 4096 + k * 16 + r;        // weight index inside the tile
+    if constexpr (KIND == Q4NX_KIND_Q8) {
+      const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
+      const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
+      return (float)(int)(int8_t)tile[kMetaBytes + i] * bf16_to_f32(s);
     } else {
-      const int k_t = hidden / 256;
-      const int tr = t >> 5, row = t & 31, rb = row >> 4, r = row & 15;
-      const int kt = c >> 8, k = c & 255, kb = k >> 5;
-      const int g = kb * 32 + rb * 16 + r;
-      const int i = rb * 4096 + k * 16 + r;        // weight index inside the tile
-      if constexpr (KIND == Q4NX_KIND_Q8) {
-        const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ8TileBytes;
-        const uint16_t s = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
-        v = (float)(int)(int8_t)tile[kMetaBytes + i] * bf16_to_f32(s);
-      } else {
-        const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ4TileBytes;
-        const uint16_t d = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
-        const uint16_t m = (uint16_t)tile[kMetaBytes + 2 * g] |
-                           ((uint16_t)tile[kMetaBytes + 2 * g + 1] << 8);
-        const uint8_t byte = tile[2 * kMetaBytes + (i >> 1)];
-        const int code = (i & 1) ? (byte >> 4) : (byte & 15);   // low nibble = even index
-        v = __fmul_rn((float)code, bf16_to_f32(d)) + bf16_to_f32(m);
-      }
+      const uint8_t* tile = w + ((size_t)tr * k_t + kt) * kQ4TileBytes;
+      const uint16_t d = (uint16_t)tile[2 * g] | ((uint16_t)tile[2 * g + 1] << 8);
+      const uint16_t m = (uint16_t)tile[kMetaBytes + 2 * g] |
+                         ((uint16_t)tile[kMetaBytes + 2 * g + 1] << 8);
+      const uint8_t byte = tile[2 * kMetaBytes + (i >> 1)];
+      const int code = (i & 1) ? (byte >> 4) : (byte & 15);   // low nibble = even index
+      return __fmul_rn((float)code, bf16_to_f32(d)) + bf16_to_f32(m);
     }
   }
-  return v;
+}
+template <int KIND>
+__device__ __forceinline__ float embed_value(const uint8_t* __restrict__ w, int t, int c,
+                                             int vocab, int hidden) {
+  // a token out of range gives a NaN row
+  return t >= 0 && t < vocab ? embed_value_of<KIND>(w, t, c, hidden) : __builtin_nanf("");
 }
 
 template <int KIND>
@@ -207,12 +209,47 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 // keys: [batch][n_slots] order-preserving argmax keys (one per lm_head tile-row). With s_tok,
 // token b is also left in s_tok[b] (batch <= kAdvanceEmbedMaxBatch) for the whole workgroup.
 constexpr int kAdvanceEmbedMaxBatch = 64;
+
+// max(k, k of the lane DPP control CTRL names), 64-bit (the two halves move together)
+template <int CTRL>
+__device__ __forceinline__ unsigned long long key_max_dpp(unsigned long long k) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xf,
+                                                            0xf, false);
+  const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+  return o > k ? o : k;
+}
+// max of a (lo, hi) pair the permlane swaps returned against the other
+__device__ __forceinline__ unsigned long long key_max_pair(uint32_t lo0, uint32_t hi0, uint32_t lo1,
+                                                          uint32_t hi1) {
+  const unsigned long long a = ((unsigned long long)hi0 << 32) | lo0;
+  const unsigned long long b = ((unsigned long long)hi1 << 32) | lo1;
+  return a > b ? a : b;
+}
+// The wave's largest key, in every lane, with no LDS round trip: DPP inside each row of 16
+// lanes, then the permlane swaps across rows and halves.
+__device__ __forceinline__ unsigned long long wave_key_max(unsigned long long k) {
+  k = key_max_dpp<kDppXor1>(k);
+  k = key_max_dpp<kDppXor2>(k);
+  k = key_max_dpp<kDppHalfMirror>(k);
+  k = key_max_dpp<kDppRor8>(k);
+  const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+  const auto l16 = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto h16 = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  k = key_max_pair(l16[0], h16[0], l16[1], h16[1]);
+  const uint32_t lo2 = (uint32_t)k, hi2 = (uint32_t)(k >> 32);
+  const auto l32 = __builtin_amdgcn_permlane32_swap(lo2, lo2, false, false);
+  const auto h32 = __builtin_amdgcn_permlane32_swap(hi2, hi2, false, false);
+  return key_max_pair(l32[0], h32[0], l32[1], h32[1]);
+}
+
 __device__ __forceinline__ void decode_advance_body(
     const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
     int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
     int32_t* __restrict__ step, int history_len, int batch, int* s_tok) {
   // Rows are taken `groups` at a time, `wpr` waves per row; each lane keeps eight key loads
-  // in flight, then the lanes and the row's waves combine (max is order-independent).
+  // in flight, then the lanes and the row's waves combine (max is order-independent). The
+  // row's position is loaded ahead of its keys, so no memory round trip follows the max.
   __shared__ unsigned long long sk[16];
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int n_waves = (int)(blockDim.x >> 6);
@@ -221,8 +258,11 @@ __device__ __forceinline__ void decode_advance_body(
   const int s = step[0];
   for (int b0 = 0; b0 < batch; b0 += groups) {
     const int b = b0 + wave / wpr, sub = wave % wpr;
+    const bool active = wave < groups * wpr && b < batch;
+    int32_t p_old = 0;
+    if (active && sub == 0 && l == 0) p_old = pos[b];
     unsigned long long k = 0ull;
-    if (wave < groups * wpr && b < batch) {
+    if (active) {
       const int T = wpr * 64;
       const unsigned long long* row = keys + (int64_t)b * n_slots;
       for (int i = sub * 64 + l; i < n_slots; i += 8 * T) {
@@ -232,23 +272,20 @@ __device__ __forceinline__ void decode_advance_body(
 #pragma unroll
         for (int j = 0; j < 8; ++j) k = v[j] > k ? v[j] : k;
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const unsigned long long v = __shfl_xor(k, o);
-        k = v > k ? v : k;
-      }
+      k = wave_key_max(k);
     }
     if (l == 0) sk[wave] = k;
     __syncthreads();
-    if (l == 0 && sub == 0 && wave < groups * wpr && b < batch) {
-      for (int w = 1; w < wpr; ++w) k = sk[wave + w] > k ? sk[wave + w] : k;
-      const int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
-      tokens[b] = tok;
-      if (s_tok != nullptr) s_tok[b] = tok;
-      const int32_t p = pos[b] + 1;
-      pos[b] = p;
-      lens[b] = p + 1;
-      if (history != nullptr && s < history_len) history[(int64_t)s * batch + b] = tok;
+    if (active && sub == 0) {   // the row's first wave combines its waves' maxima
+      k = wave_key_max(l < wpr ? sk[wave + l] : 0ull);
+      if (l == 0) {
+        const int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+        tokens[b] = tok;
+        if (s_tok != nullptr) s_tok[b] = tok;
+        pos[b] = p_old + 1;
+        lens[b] = p_old + 2;
+        if (history != nullptr && s < history_len) history[(int64_t)s * batch + b] = tok;
+      }
     }
     __syncthreads();
   }
@@ -275,17 +312,36 @@ __global__ __launch_bounds__(1024) void decode_advance_embed_kernel(
   decode_advance_body(keys, n_slots, tokens, pos, lens, history, step, history_len, batch,
                       s_tok);
   __syncthreads();
+  // Four 1024-column chunks of a row at a time: every load of the chunks is issued before
+  // the first value is stored, so the row costs one memory round trip, not one per chunk.
+  constexpr int kChunks = 4;
   for (int b = 0; b < batch; ++b) {
-    const int t = s_tok[b];
-    // hidden % 256 == 0: a 16-lane group is either all inside the row or all past it
-    for (int c0 = 0; c0 < hidden; c0 += 1024) {
-      const int c = c0 + (int)threadIdx.x;
-      const bool in = c < hidden;
-      const float v = embed_value<KIND>(table, t, in ? c : 0, vocab, hidden);
-      if (in) h[(size_t)b * hidden + c] = v;
-      if (ssq_out != nullptr) {
-        const float s16 = group16_sum(v * v);
-        if (in && (c & 15) == 0) ssq_out[(size_t)b * (hidden / 16) + (c >> 4)] = s16;
+    // the token is the same in every lane: one uniform branch on its range, then straight-line
+    // loads for all chunks
+    const int t = __builtin_amdgcn_readfirstlane(s_tok[b]);
+    const bool valid = t >= 0 && t < vocab;
+    for (int c0 = 0; c0 < hidden; c0 += 1024 * kChunks) {
+      float v[kChunks];
+      if (valid) {
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+          const int c = c0 + 1024 * j + (int)threadIdx.x;
+          v[j] = embed_value_of<KIND>(table, t, c < hidden ? c : 0, hidden);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) v[j] = __builtin_nanf("");
+      }
+      // hidden % 256 == 0: a 16-lane group is either all inside the row or all past it
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) {
+        const int c = c0 + 1024 * j + (int)threadIdx.x;
+        const bool in = c < hidden;
+        if (in) h[(size_t)b * hidden + c] = v[j];
+        if (ssq_out != nullptr) {
+          const float s16 = group16_sum(v[j] * v[j]);
+          if (in && (c & 15) == 0) ssq_out[(size_t)b * (hidden / 16) + (c >> 4)] = s16;
+        }
       }
     }
   }
