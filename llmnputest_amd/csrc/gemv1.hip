@@ -151,6 +151,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   const int32_t* const posp = a.pos;
   const int k_t = a.k_t, n_groups = a.n_groups, grp_q = a.grp_q, grp_k = a.grp_k;
   const int att_split = a.att_split, att_g = a.att_g;
+  const float rcp_g = XREC ? __builtin_amdgcn_rcpf((float)att_g) : 0.f;
   asm volatile("" ::"s"(w0), "s"(w1), "s"(w2), "s"(xin), "s"(norm_w), "s"(ssq_in), "s"(residual),
                "s"(posp), "s"(k_t), "s"(n_groups), "s"(grp_q), "s"(grp_k), "s"(att_split),
                "s"(att_g));
@@ -228,14 +229,21 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
     const int k = min(kt0 + t, k_t - 1) * kTileK + k0;
     if constexpr (XREC) {
       // attention records of this lane's head (k / 64) and its four dims (k % 64 ..): split
-      // i's record is i * att_g records past split 0's (the launch has XNS == att_split)
-      const int h = k >> 6, kvh = h / att_g, hh = h - kvh * att_g;
-      const float* r0p = (const float*)xin + ((size_t)kvh * XNS * att_g + hh) * kAttnRecFloats;
-      const size_t rs = (size_t)att_g * kAttnRecFloats;
+      // i's record is i * att_g records past split 0's (the launch has XNS == att_split).
+      // The kv head is an exact float quotient (h < 2^12 and att_g <= 64, so (h + 1/2) / att_g
+      // stays at least 1/128 from an integer), and the loads take 32-bit byte offsets from the
+      // uniform base (one launch's records are a few hundred KB).
+      const int h = k >> 6;
+      const int kvh = (int)(((float)h + 0.5f) * rcp_g);
+      const int hh = h - kvh * att_g;
+      const uint32_t o0 = (uint32_t)((kvh * XNS * att_g + hh) * kAttnRecFloats) * 4u;
+      const uint32_t oa = o0 + (uint32_t)(k & 63) * 4u, ob = o0 + 64u * 4u;
+      const uint32_t rs = (uint32_t)att_g * (kAttnRecFloats * 4u);   // uniform
 #pragma unroll
       for (int i = 0; i < XNS; ++i) {
-        racc[i] = *(const float4*)(r0p + i * rs + (k & 63));
-        rml[i] = *(const float2*)(r0p + i * rs + 64);
+        const char* ri = (const char*)xin + (size_t)((uint32_t)i * rs);   // uniform base
+        racc[i] = *(const float4*)(ri + oa);
+        rml[i] = *(const float2*)(ri + ob);
       }
     } else if constexpr (NORM) {
       hv[t] = *(const float4*)((const float*)xin + k);
