@@ -132,20 +132,20 @@ __device__ __forceinline__ void attn_round(AttnLane<G>& st, const uint4 (&kr)[kA
   }
 }
 
-// One pass of the split merge for this thread's outputs (thread t owns outputs t, t + 256, ..
-// = (head e / 64, dim e % 64)): the (m, l, acc[dim]) of splits cs .. cs + ns - 1 (ns <= P),
-// all loaded at once (past ns the last record again, masked), then folded into the running
-// (M, L, A) in split order.
-template <int G, int P>
+// One pass of the split merge for this thread's outputs (thread t of TH owns outputs t,
+// t + TH, .. = (head e / 64, dim e % 64)): the (m, l, acc[dim]) of splits cs .. cs + ns - 1
+// (ns <= P), all loaded at once (past ns the last record again, masked), then folded into the
+// running (M, L, A) in split order.
+template <int G, int P, int TH>
 __device__ __forceinline__ void attn_merge_pass(const float* recs, int cs, int ns,
-                                                float (&M)[(G * 64 + 255) / 256],
-                                                float (&L)[(G * 64 + 255) / 256],
-                                                float (&A)[(G * 64 + 255) / 256]) {
-  constexpr int kE = (G * 64 + 255) / 256;
+                                                float (&M)[(G * 64 + TH - 1) / TH],
+                                                float (&L)[(G * 64 + TH - 1) / TH],
+                                                float (&A)[(G * 64 + TH - 1) / TH]) {
+  constexpr int kE = (G * 64 + TH - 1) / TH;
   float mv[kE][P], lv[kE][P], av[kE][P];
 #pragma unroll
   for (int j = 0; j < kE; ++j) {
-    const int e = min((int)threadIdx.x + 256 * j, G * 64 - 1);
+    const int e = min((int)threadIdx.x + TH * j, G * 64 - 1);
     const int h = e >> 6, d = e & 63;
 #pragma unroll
     for (int i = 0; i < P; ++i) {
@@ -182,7 +182,8 @@ __device__ __forceinline__ void attn_merge_pass(const float* recs, int cs, int n
 // h of the group. With one split that is the answer; otherwise the record is published and
 // the last workgroup of the (sequence, kv head) to arrive merges every split's record
 // exactly, in split order (kMergeSplits records per pass).
-template <int G>
+// TH: threads of the workgroup (each thread merges outputs tid, tid + TH, ..).
+template <int G, int TH = 256>
 __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kPartStride],
                                             int* s_last, int bk, int split, int b, int kvh) {
   const int tid = threadIdx.x;
@@ -192,7 +193,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.partial, a.partial_bytes);
     const uint32_t rec_bytes = G * kPartStride * 4;
     const uint32_t rec = (uint32_t)((size_t)bk * a.n_split + split) * rec_bytes;
-    for (int e = tid; e < G * kPartStride / 4; e += 256)
+    for (int e = tid; e < G * kPartStride / 4; e += TH)
       st16_sys(pr, rec + e * 16, ((const uint4*)&s_fin[0][0])[e]);
     if (a.publish_only) return;
     wait_vm();
@@ -206,7 +207,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
 
     // every thread merges its own output columns over the split records, straight from
     // memory: one round of loads per pass, no staging through LDS, no barriers
-    constexpr int kE = (G * 64 + 255) / 256;   // outputs per thread
+    constexpr int kE = (G * 64 + TH - 1) / TH;   // outputs per thread
     const float* recs = a.partial + (size_t)bk * a.n_split * G * kPartStride;
     float M[kE], L[kE], A[kE];
 #pragma unroll
@@ -217,12 +218,12 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
     }
     for (int cs = 0; cs < a.n_split; cs += kMergeSplits) {
       const int ns = min(kMergeSplits, a.n_split - cs);
-      if (ns <= 8) attn_merge_pass<G, 8>(recs, cs, ns, M, L, A);
-      else attn_merge_pass<G, kMergeSplits>(recs, cs, ns, M, L, A);
+      if (ns <= 8) attn_merge_pass<G, 8, TH>(recs, cs, ns, M, L, A);
+      else attn_merge_pass<G, kMergeSplits, TH>(recs, cs, ns, M, L, A);
     }
 #pragma unroll
     for (int j = 0; j < kE; ++j) {
-      const int e = tid + 256 * j;
+      const int e = tid + TH * j;
       if (e < G * 64) {
         const int h = e >> 6, d = e & 63;
         s_fin[h][d] = A[j];
@@ -237,7 +238,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
     __syncthreads();
   }
 
-  for (int e = tid; e < G * 64; e += 256) {
+  for (int e = tid; e < G * 64; e += TH) {
     const int h = e >> 6, d = e & 63;
     const float Ls = s_fin[h][65];
     const float o = Ls > 0.f ? attn_div(s_fin[h][d], Ls) : 0.f;   // an empty sequence: 0
@@ -453,12 +454,16 @@ __device__ __forceinline__ void attn_mfma_round(MfmaLane& st, const u32x4_t (&kr
   }
 }
 
-template <int G, bool NT>
-__global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
+// NW waves of 32 positions per round (4, or 8 for launches whose splits are longer than a
+// 4-wave round: one round of 256 positions instead of two of 128).
+template <int G, bool NT, int NW = kAttnWaves>
+__global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
   static_assert(G * 32 <= 256 && G <= 16, "one thread per (head, split) in the merge");
-  __shared__ __attribute__((aligned(16))) float s_o[kAttnWaves * G * 64];   // wave states
+  constexpr int TH = NW * 64;
+  constexpr int R = NW * 32;   // positions per workgroup round
+  __shared__ __attribute__((aligned(16))) float s_o[NW * G * 64];   // wave states
   __shared__ __attribute__((aligned(16))) float s_fin[G][kPartStride];
-  __shared__ float s_wm[kAttnWaves][G], s_wl[kAttnWaves][G];
+  __shared__ float s_wm[NW][G], s_wl[NW][G];
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -482,8 +487,8 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
   u32x4_t kA[4], kB[4], kC[4];
   uint2 vA[8], vB[8], vC[8];
   attn_mfma_load<NT>(kbase, vbase, start + wo, stop, j, g, kA, vA);
-  if (stop - start > kAttnRound)   // a second round exists (known before the length is)
-    attn_mfma_load<NT>(kbase, vbase, start + kAttnRound + wo, stop, j, g, kB, vB);
+  if (stop - start > R)   // a second round exists (known before the length is)
+    attn_mfma_load<NT>(kbase, vbase, start + R + wo, stop, j, g, kB, vB);
   MfmaLane st;
   {
     const uint16_t* qrow = a.q + ((size_t)b * a.hq + kvh * G + (j < G ? j : 0)) * 64;
@@ -499,18 +504,18 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) st.o[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int end = min(stop, max(0, a.lens[b]));
-  const int nr = end > start ? (end - start + kAttnRound - 1) / kAttnRound : 0;
+  const int nr = end > start ? (end - start + R - 1) / R : 0;
   for (int r = 0; r < nr; r += 3) {
-    const int p0 = start + r * kAttnRound + wo;   // this wave's first position of round r
-    if (r + 2 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 2 * kAttnRound, stop, j, g, kC, vC);
+    const int p0 = start + r * R + wo;   // this wave's first position of round r
+    if (r + 2 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 2 * R, stop, j, g, kC, vC);
     attn_mfma_round(st, kA, vA, p0, end, g, a.scale_l2);
-    if (r + 3 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 3 * kAttnRound, stop, j, g, kA, vA);
-    if (r + 1 < nr) attn_mfma_round(st, kB, vB, p0 + kAttnRound, end, g, a.scale_l2);
-    if (r + 4 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 4 * kAttnRound, stop, j, g, kB, vB);
-    if (r + 2 < nr) attn_mfma_round(st, kC, vC, p0 + 2 * kAttnRound, end, g, a.scale_l2);
+    if (r + 3 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 3 * R, stop, j, g, kA, vA);
+    if (r + 1 < nr) attn_mfma_round(st, kB, vB, p0 + R, end, g, a.scale_l2);
+    if (r + 4 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 4 * R, stop, j, g, kB, vB);
+    if (r + 2 < nr) attn_mfma_round(st, kC, vC, p0 + 2 * R, end, g, a.scale_l2);
   }
 
-  // ---- merge the four waves: l over each head's lane groups, then (m, l, O) through LDS
+  // ---- merge the waves: l over each head's lane groups, then (m, l, O) through LDS
   st.l = xor32_sum(xor16_sum(st.l));
   if (j < G) {
     if (g == 0) {
@@ -523,15 +528,15 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
           make_float4(st.o[0][e], st.o[1][e], st.o[2][e], st.o[3][e]);
   }
   __syncthreads();
-  for (int e = tid; e < G * 64; e += 256) {
+  for (int e = tid; e < G * 64; e += TH) {
     const int h = e >> 6, d = e & 63;
     float M = s_wm[0][h];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, s_wm[w][h]);
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_wm[w][h]);
     const float Mb = M == -INFINITY ? 0.f : M;
     float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float f = ex2(s_wm[w][h] - Mb);
       L = fmaf(s_wl[w][h], f, L);
       A = fmaf(s_o[(w * G + h) * 64 + d], f, A);
@@ -545,7 +550,7 @@ __global__ __launch_bounds__(256) void gqa_mfma_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  attn_finish<G>(a, s_fin, &s_last, bk, split, b, kvh);
+  attn_finish<G, TH>(a, s_fin, &s_last, bk, split, b, kvh);
 }
 
 // Splits per (sequence, kv head), at least one round of positions each. VALU kernel: about
@@ -581,7 +586,12 @@ static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) 
   // K/V of 64 MB or more per launch streams past the caches (measured: batch 8 at 32768
   // positions 101 -> 93 us); smaller launches, decode's included, keep cached loads
   const bool nt = (size_t)a.batch * a.hkv * a.max_len * 256 >= ((size_t)64 << 20);
+  // splits longer than one 4-wave round take 8 waves (published records and the merged
+  // answer then come from the same kernel, bit for bit)
+  const bool wide = a.chunk > kAttnRound;
   if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
+  else if (mfma && wide)
+    hipLaunchKernelGGL((gqa_mfma_kernel<G, false, 8>), grid, dim3(512), 0, s, a);
   else if (mfma) hipLaunchKernelGGL((gqa_mfma_kernel<G, false>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(gqa_decode_kernel<G>, grid, dim3(256), 0, s, a);
 }
