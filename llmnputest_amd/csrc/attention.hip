@@ -586,9 +586,12 @@ static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) 
   // K/V of 64 MB or more per launch streams past the caches (measured: batch 8 at 32768
   // positions 101 -> 93 us); smaller launches, decode's included, keep cached loads
   const bool nt = (size_t)a.batch * a.hkv * a.max_len * 256 >= ((size_t)64 << 20);
-  // splits longer than one 4-wave round take 8 waves (published records and the merged
-  // answer then come from the same kernel, bit for bit)
-  const bool wide = a.chunk > kAttnRound;
+  // Splits longer than one 4-wave round take 8 waves (published records and the merged answer
+  // then come from the same kernel, bit for bit), when the launch fits the chip at one
+  // 8-wave workgroup per CU (170 VGPRs: two waves per SIMD); a larger grid keeps 4 waves and
+  // two workgroups per CU (batch 8 at context 2048: 3379 against 3169 tok/s).
+  constexpr unsigned kWideMaxWorkgroups = 256;   // compute units of an MI355X
+  const bool wide = a.chunk > kAttnRound && grid.x <= kWideMaxWorkgroups;
   if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
   else if (mfma && wide)
     hipLaunchKernelGGL((gqa_mfma_kernel<G, false, 8>), grid, dim3(512), 0, s, a);
