@@ -456,7 +456,8 @@ def test_decode_advance_embed_equals_advance_then_embed(dev, kind, batch):
 
 
 @pytest.mark.parametrize("hq,hkv,L,lmax,n_split,n_out", [
-    (40, 8, 2112, 2176, 17, 2560),   # the 3B decode shape at the automatic split count
+    (40, 8, 2112, 2176, 9, 2560),    # the 3B decode shape at the policy's split count (8 waves)
+    (40, 8, 2112, 2176, 17, 2560),   # the same with 17 splits (4 waves)
     (40, 8, 2112, 2176, 18, 2560),   # the most splits the merge holds
     (40, 8, 300, 320, 1, 512),       # one split still publishes a record
     (32, 8, 1000, 1024, 5, 512),
