@@ -415,6 +415,35 @@ def test_embed_and_argmax(dev, kind):
     assert idx.tolist() == np.argmax(logits, axis=1).tolist()
 
 
+@pytest.mark.parametrize("batch", [1, 3, 5, 8, 17, 40])
+def test_decode_advance_against_numpy(dev, batch):
+    """decode_advance over random keys at batch sizes that give every arrangement of its
+    reduction (16, 5, 3, 2 and 1 waves per row, and rows taken in several rounds): the token of
+    each row's largest key, positions and lengths advanced, history written at the step, the
+    step counter advanced; a row whose largest key appears twice yields that key's token."""
+    rng = np.random.default_rng(31 + batch)
+    n_slots = 6272
+    # keys as the lm_head epilogue writes them: an order-preserving value above, 2^32 - 1 minus
+    # the row below (slot i holds the best of rows 16 i .. 16 i + 15)
+    rows = np.arange(n_slots, dtype=np.int64) * 16 + rng.integers(0, 16, (batch, n_slots))
+    hi = rng.integers(0, 1 << 30, (batch, n_slots), dtype=np.int64)
+    hi[0, 100] = hi[0, 5000] = (1 << 30) + 7             # one value at two rows: the first wins
+    keys = (hi << 32) | (0xffffffff - rows)
+    pos0 = rng.integers(0, 4000, batch).astype(np.int32)
+    i32 = lambda a: torch.from_numpy(np.asarray(a, dtype=np.int32)).to(dev)
+    tok, pos, lens, step = i32(np.zeros(batch)), i32(pos0), i32(np.zeros(batch)), i32([2])
+    hist = torch.full((4, batch), -1, dtype=torch.int32, device=dev)
+    ops.decode_advance(torch.from_numpy(keys).to(dev), n_slots, tok, pos, lens, step, hist)
+    expect = rows[np.arange(batch), np.argmax(keys, axis=1)]
+    assert int(expect[0]) == int(rows[0, 100])
+    assert tok.cpu().numpy().tolist() == expect.tolist()
+    assert pos.cpu().numpy().tolist() == (pos0 + 1).tolist()
+    assert lens.cpu().numpy().tolist() == (pos0 + 2).tolist()
+    h = hist.cpu().numpy()
+    assert h[2].tolist() == expect.tolist() and (h[[0, 1, 3]] == -1).all()
+    assert int(step.cpu()) == 3
+
+
 @pytest.mark.parametrize("kind,batch", [("q8", 1), ("q4", 3), ("bf16", 2)])
 def test_decode_advance_embed_equals_advance_then_embed(dev, kind, batch):
     """The fused greedy-loop launch (argmax keys -> token, positions, history, then the token's
