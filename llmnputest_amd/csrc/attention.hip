@@ -592,7 +592,9 @@ static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) 
   // two workgroups per CU (batch 8 at context 2048: 3379 against 3169 tok/s).
   constexpr unsigned kWideMaxWorkgroups = 256;   // compute units of an MI355X
   const bool wide = a.chunk > kAttnRound && grid.x <= kWideMaxWorkgroups;
-  if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
+  if (mfma && nt && wide)
+    hipLaunchKernelGGL((gqa_mfma_kernel<G, true, 8>), grid, dim3(512), 0, s, a);
+  else if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
   else if (mfma && wide)
     hipLaunchKernelGGL((gqa_mfma_kernel<G, false, 8>), grid, dim3(512), 0, s, a);
   else if (mfma) hipLaunchKernelGGL((gqa_mfma_kernel<G, false>), grid, dim3(256), 0, s, a);
