@@ -553,6 +553,20 @@ __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
   attn_finish<G, TH>(a, s_fin, &s_last, bk, split, b, kvh);
 }
 
+// Positions per split as attn_run lays them out, and whether a matrix-core launch of `wgs`
+// workgroups with splits that long runs on 8 waves: a split longer than one 4-wave round,
+// when the launch fits one 8-wave workgroup per CU (170 VGPRs: two waves per SIMD; a larger
+// grid keeps 4 waves and two workgroups per CU). Its rounds of positions per split.
+constexpr long long kWideMaxWorkgroups = 256;   // compute units of an MI355X
+static int split_chunk(int max_len, int s) { return ((max_len + s - 1) / s + 7) & ~7; }
+static bool attn_wide(int chunk, long long wgs) {
+  return chunk > kAttnRound && wgs <= kWideMaxWorkgroups;
+}
+static int attn_rounds(int chunk, bool wide) {
+  const int r = wide ? 2 * kAttnRound : kAttnRound;
+  return (chunk + r - 1) / r;
+}
+
 // Splits per (sequence, kv head), at least one round of positions each. VALU kernel: about
 // 512 workgroups, at most 64 splits.
 static int auto_split(int batch, int hkv, int max_len, bool mfma) {
@@ -573,7 +587,20 @@ static int auto_split(int batch, int hkv, int max_len, bool mfma) {
     const int by_grid = 512 / bh;
     s = s > by_grid ? by_grid : s;
     s = s > 32 ? 32 : s;
-    return s < 1 ? 1 : s;
+    s = s < 1 ? 1 : s;
+    // then the fewest splits that take no more rounds (each in its own wave count) and still
+    // give 128 workgroups: the same time per workgroup with fewer records to merge (batch 8
+    // at context 2048: 3 splits on 8 waves, 3425 against 3367 tok/s with 8 on 4 waves; batch
+    // 8, L = 4096: 16.8 against 17.4 us). Below 128 workgroups fewer, longer ones finish
+    // later (batch 1, L = 512: 2 splits on 8 waves 6.8 us, 4 splits on 4 waves 6.4 us).
+    const int c0 = split_chunk(max_len, s);
+    const int r0 = attn_rounds(c0, attn_wide(c0, (long long)bh * s));
+    for (int t = 1; t < s; ++t) {
+      if ((long long)bh * t < 128) continue;
+      const int c = split_chunk(max_len, t);
+      if (attn_rounds(c, attn_wide(c, (long long)bh * t)) <= r0) return t;
+    }
+    return s;
   }
   const int by_grid = (512 + bh - 1) / bh;
   int s = by_len < by_grid ? by_len : by_grid;
@@ -586,12 +613,10 @@ static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) 
   // K/V of 64 MB or more per launch streams past the caches (measured: batch 8 at 32768
   // positions 101 -> 93 us); smaller launches, decode's included, keep cached loads
   const bool nt = (size_t)a.batch * a.hkv * a.max_len * 256 >= ((size_t)64 << 20);
-  // Splits longer than one 4-wave round take 8 waves (published records and the merged answer
-  // then come from the same kernel, bit for bit), when the launch fits the chip at one
-  // 8-wave workgroup per CU (170 VGPRs: two waves per SIMD); a larger grid keeps 4 waves and
-  // two workgroups per CU (batch 8 at context 2048: 3379 against 3169 tok/s).
-  constexpr unsigned kWideMaxWorkgroups = 256;   // compute units of an MI355X
-  const bool wide = a.chunk > kAttnRound && grid.x <= kWideMaxWorkgroups;
+  // 8 waves by attn_wide (published records and the merged answer then come from the same
+  // kernel, bit for bit; batch 8 at context 2048 with 8 splits, 512 workgroups: 3379 tok/s on
+  // 4 waves against 3169 on 8)
+  const bool wide = attn_wide(a.chunk, (long long)grid.x);
   if (mfma && nt && wide)
     hipLaunchKernelGGL((gqa_mfma_kernel<G, true, 8>), grid, dim3(512), 0, s, a);
   else if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
