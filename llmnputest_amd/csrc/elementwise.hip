@@ -247,9 +247,11 @@ __device__ __forceinline__ void decode_advance_body(
     const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
     int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
     int32_t* __restrict__ step, int history_len, int batch, int* s_tok) {
-  // Rows are taken `groups` at a time, `wpr` waves per row; each lane keeps eight key loads
-  // in flight, then the lanes and the row's waves combine (max is order-independent). The
-  // row's position is loaded ahead of its keys, so no memory round trip follows the max.
+  // Rows are taken `groups` at a time, `wpr` waves per row; each lane keeps up to kKeyLoads
+  // key loads in flight (a 100352-row head at batch 8: two round trips per lane, not seven),
+  // then the lanes and the row's waves combine (max is order-independent). The row's
+  // position is loaded ahead of its keys, so no memory round trip follows the max.
+  constexpr int kKeyLoads = 32;
   __shared__ unsigned long long sk[16];
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int n_waves = (int)(blockDim.x >> 6);
@@ -265,12 +267,12 @@ __device__ __forceinline__ void decode_advance_body(
     if (active) {
       const int T = wpr * 64;
       const unsigned long long* row = keys + (int64_t)b * n_slots;
-      for (int i = sub * 64 + l; i < n_slots; i += 8 * T) {
-        unsigned long long v[8];
+      for (int i = sub * 64 + l; i < n_slots; i += kKeyLoads * T) {
+        unsigned long long v[kKeyLoads];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = i + j * T < n_slots ? row[i + j * T] : 0ull;
+        for (int j = 0; j < kKeyLoads; ++j) v[j] = i + j * T < n_slots ? row[i + j * T] : 0ull;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) k = v[j] > k ? v[j] : k;
+        for (int j = 0; j < kKeyLoads; ++j) k = v[j] > k ? v[j] : k;
       }
       k = wave_key_max(k);
     }
@@ -312,36 +314,34 @@ __global__ __launch_bounds__(1024) void decode_advance_embed_kernel(
   decode_advance_body(keys, n_slots, tokens, pos, lens, history, step, history_len, batch,
                       s_tok);
   __syncthreads();
-  // Four 1024-column chunks of a row at a time: every load of the chunks is issued before
-  // the first value is stored, so the row costs one memory round trip, not one per chunk.
+  // Four 1024-entry chunks of the [batch][hidden] rows at a time, across row boundaries:
+  // every load of the chunks is issued before the first value is stored, so a group of
+  // chunks costs one memory round trip (eight rows of 2560: five, against one per row and
+  // chunk). A token out of range loads row 0 and stores a NaN row.
   constexpr int kChunks = 4;
-  for (int b = 0; b < batch; ++b) {
-    // the token is the same in every lane: one uniform branch on its range, then straight-line
-    // loads for all chunks
-    const int t = __builtin_amdgcn_readfirstlane(s_tok[b]);
-    const bool valid = t >= 0 && t < vocab;
-    for (int c0 = 0; c0 < hidden; c0 += 1024 * kChunks) {
-      float v[kChunks];
-      if (valid) {
+  const int total = batch * hidden;
+  for (int f0 = 0; f0 < total; f0 += 1024 * kChunks) {
+    float v[kChunks];
 #pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-          const int c = c0 + 1024 * j + (int)threadIdx.x;
-          v[j] = embed_value_of<KIND>(table, t, c < hidden ? c : 0, hidden);
-        }
-      } else {
+    for (int j = 0; j < kChunks; ++j) {
+      const int f = f0 + 1024 * j + (int)threadIdx.x;
+      const int b = f < total ? f / hidden : 0;
+      const int c = f < total ? f - b * hidden : 0;
+      const int t = s_tok[b];
+      const bool ok = t >= 0 && t < vocab;
+      v[j] = embed_value_of<KIND>(table, ok ? t : 0, c, hidden);
+      if (!ok) v[j] = __builtin_nanf("");
+    }
+    // h and ssq_out are [batch][hidden] and [batch][hidden / 16], so entry f is h[f] and its
+    // 16-entry group ssq_out[f / 16]; hidden % 256 == 0 keeps a 16-lane group inside a row
 #pragma unroll
-        for (int j = 0; j < kChunks; ++j) v[j] = __builtin_nanf("");
-      }
-      // hidden % 256 == 0: a 16-lane group is either all inside the row or all past it
-#pragma unroll
-      for (int j = 0; j < kChunks; ++j) {
-        const int c = c0 + 1024 * j + (int)threadIdx.x;
-        const bool in = c < hidden;
-        if (in) h[(size_t)b * hidden + c] = v[j];
-        if (ssq_out != nullptr) {
-          const float s16 = group16_sum(v[j] * v[j]);
-          if (in && (c & 15) == 0) ssq_out[(size_t)b * (hidden / 16) + (c >> 4)] = s16;
-        }
+    for (int j = 0; j < kChunks; ++j) {
+      const int f = f0 + 1024 * j + (int)threadIdx.x;
+      const bool in = f < total;
+      if (in) h[f] = v[j];
+      if (ssq_out != nullptr) {
+        const float s16 = group16_sum(v[j] * v[j]);
+        if (in && (f & 15) == 0) ssq_out[f >> 4] = s16;
       }
     }
   }
@@ -461,7 +461,7 @@ int q4nx_decode_advance_embed(const uint64_t* keys, int n_slots, int32_t* tokens
   Q4NX_REQUIRE(batch >= 1 && batch <= kAdvanceEmbedMaxBatch && n_slots >= 1, Q4NX_ERR_SHAPE,
                "%s: batch=%d (1..%d) n_slots=%d", what, batch, kAdvanceEmbedMaxBatch, n_slots);
   Q4NX_REQUIRE(vocab > 0 && (kind == Q4NX_KIND_BF16 || vocab % 32 == 0) && hidden > 0 &&
-                   hidden % 256 == 0,
+                   hidden % 256 == 0 && (int64_t)batch * hidden < ((int64_t)1 << 30),
                Q4NX_ERR_SHAPE, "%s: vocab=%d hidden=%d", what, vocab, hidden);
   const auto* k = (const unsigned long long*)keys;
   const uint8_t* w = (const uint8_t*)table;
