@@ -475,9 +475,10 @@ def main() -> int:
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     ap.add_argument("--only", default=None, metavar="GROUPS",
                     help="profiling: only these comma-separated groups (" +
-                         ",".join(SECONDARY_GROUPS + ("decode",)) +
-                         "; decode: the batch-1 decode at --ctx / --new-tokens); prints their "
-                         "JSON and exits")
+                         ",".join(SECONDARY_GROUPS + ("decode", "decode_batched")) +
+                         "; decode: the batch-1 decode at --ctx / --new-tokens; "
+                         "decode_batched: the same with --decode-batch sequences); prints "
+                         "their JSON and exits")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -495,9 +496,10 @@ def main() -> int:
         return copy_calibration(a.calibrate_copy, 10, dev)
     if a.only:
         groups = tuple(g for g in a.only.split(",") if g)
-        bad = [g for g in groups if g not in SECONDARY_GROUPS + ("decode",)]
+        dec_groups = ("decode", "decode_batched")
+        bad = [g for g in groups if g not in SECONDARY_GROUPS + dec_groups]
         if bad:
-            print(f"unknown groups {bad}; choose from {SECONDARY_GROUPS + ('decode',)}",
+            print(f"unknown groups {bad}; choose from {SECONDARY_GROUPS + dec_groups}",
                   file=sys.stderr)
             return 2
         out = {}
@@ -505,7 +507,11 @@ def main() -> int:
             d = decode_bench(a.ctx, a.new_tokens, dev, 0)
             d.pop("weights")
             out["decode"] = d
-        sec = tuple(g for g in groups if g != "decode")
+        if "decode_batched" in groups:
+            d = decode_bench(a.ctx, a.new_tokens, dev, 0, batch=a.decode_batch)
+            d.pop("weights")
+            out["decode_batched"] = d
+        sec = tuple(g for g in groups if g not in dec_groups)
         if sec:
             out["other_shapes"] = secondary_bench(dev, sec)
         print(json.dumps(out), flush=True)
