@@ -68,20 +68,34 @@ def gemv_bench(steps: int, warmup: int, rot: int, dev) -> dict:
     y_d = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     ws = ops.Workspace(8 << 20, device=dev)
 
-    def run(which: str):
-        for g, u, d in layers:
-            if which in ("all", "gate_up"):
-                ops.gemv(g, "q4", x, INTER // 32, HIDDEN // 256, out=y_gu, ws=ws)
-                ops.gemv(u, "q4", x, INTER // 32, HIDDEN // 256, out=y_gu, ws=ws)
-            if which in ("all", "down"):
-                ops.gemv(d, "q4", h, HIDDEN // 32, INTER // 256, out=y_d, ws=ws)
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    tiny = torch.zeros(16, dtype=torch.uint8, device=dev)
 
-    def timed(which: str, n_steps: int) -> float:
-        run(which)                              # eager warm-up (no allocation later)
+    def run(which: str, mode: str = "gemv"):
+        """One step: gate and up (2560->8192) and/or down (8192->2560) of every rotated layer,
+        as the GEMV, as the null kernel (same grid and loads, no arithmetic), or as a plain
+        read of the same weight bytes; "empty" launches a 16-byte read in place of each."""
+        for g, u, d in layers:
+            for w_, x_, y_, n_, k_, part in ((g, x, y_gu, INTER, HIDDEN, "gate_up"),
+                                             (u, x, y_gu, INTER, HIDDEN, "gate_up"),
+                                             (d, h, y_d, HIDDEN, INTER, "down")):
+                if which not in ("all", part):
+                    continue
+                if mode == "gemv":
+                    ops.gemv(w_, "q4", x_, n_ // 32, k_ // 256, out=y_, ws=ws)
+                elif mode == "null":
+                    ops.gemv_q4_null(w_, x_, n_ // 32, k_ // 256, out=y_)
+                elif mode == "read":
+                    ops.stream_read(w_, sink)
+                else:
+                    ops.stream_read(tiny, sink)
+
+    def timed(which: str, n_steps: int, mode: str = "gemv") -> float:
+        run(which, mode)                        # eager warm-up (no allocation later)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            run(which)
+            run(which, mode)
         for _ in range(warmup):
             g.replay()
         torch.cuda.synchronize()
@@ -97,6 +111,13 @@ def gemv_bench(steps: int, warmup: int, rot: int, dev) -> dict:
     t_all = timed("all", steps)
     t_gu = timed("gate_up", steps)
     t_d = timed("down", steps)
+    # the floors of the same launches: the null kernel per shape, a plain read of the same
+    # 13,107,200-byte tensors, and a near-empty launch (one 16-byte read)
+    f_gu = timed("gate_up", steps, "null") / (2 * rot)
+    f_d = timed("down", steps, "null") / rot
+    f_all = timed("all", steps, "null") / (3 * rot)
+    r_all = timed("all", steps, "read") / (3 * rot)
+    e_all = timed("all", steps, "empty") / (3 * rot)
     step_bytes = rot * (2 * b_gu + b_d)
     return {
         "t_step": t_all,
@@ -110,6 +131,11 @@ def gemv_bench(steps: int, warmup: int, rot: int, dev) -> dict:
         "down_us": t_d / rot * 1e6,
         "bytes_gate_up": b_gu,
         "bytes_down": b_d,
+        "null_gate_up_us": f_gu * 1e6,
+        "null_down_us": f_d * 1e6,
+        "null_us_per_launch": f_all * 1e6,
+        "read_us_per_launch": r_all * 1e6,
+        "empty_us_per_launch": e_all * 1e6,
     }
 
 
@@ -475,8 +501,9 @@ def main() -> int:
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     ap.add_argument("--only", default=None, metavar="GROUPS",
                     help="profiling: only these comma-separated groups (" +
-                         ",".join(SECONDARY_GROUPS + ("decode", "decode_batched")) +
-                         "; decode: the batch-1 decode at --ctx / --new-tokens; "
+                         ",".join(SECONDARY_GROUPS + ("gemv", "decode", "decode_batched")) +
+                         "; gemv: the headline GEMV steps and their floors; "
+                         "decode: the batch-1 decode at --ctx / --new-tokens; "
                          "decode_batched: the same with --decode-batch sequences); prints "
                          "their JSON and exits")
     a = ap.parse_args()
@@ -496,13 +523,16 @@ def main() -> int:
         return copy_calibration(a.calibrate_copy, 10, dev)
     if a.only:
         groups = tuple(g for g in a.only.split(",") if g)
-        dec_groups = ("decode", "decode_batched")
+        dec_groups = ("gemv", "decode", "decode_batched")
         bad = [g for g in groups if g not in SECONDARY_GROUPS + dec_groups]
         if bad:
             print(f"unknown groups {bad}; choose from {SECONDARY_GROUPS + dec_groups}",
                   file=sys.stderr)
             return 2
         out = {}
+        if "gemv" in groups:
+            out["gemv"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                           for k, v in gemv_bench(a.steps, a.warmup, a.rot, dev).items()}
         if "decode" in groups:
             d = decode_bench(a.ctx, a.new_tokens, dev, 0)
             d.pop("weights")
@@ -557,9 +587,24 @@ def main() -> int:
             "traffic": measured_traffic(),
         },
         "per_shape": {
-            "gate_up_2560x8192": {"GB/s": round(r["gate_up_gbs"], 1), "us": round(r["gate_up_us"], 3)},
-            "down_8192x2560": {"GB/s": round(r["down_gbs"], 1), "us": round(r["down_us"], 3)},
+            "gate_up_2560x8192": {"GB/s": round(r["gate_up_gbs"], 1), "us": round(r["gate_up_us"], 3),
+                                  "floor_us": round(r["null_gate_up_us"], 3),
+                                  "frac_of_floor": round(r["null_gate_up_us"] / r["gate_up_us"], 4)},
+            "down_8192x2560": {"GB/s": round(r["down_gbs"], 1), "us": round(r["down_us"], 3),
+                               "floor_us": round(r["null_down_us"], 3),
+                               "frac_of_floor": round(r["null_down_us"] / r["down_us"], 4)},
             "us_per_launch": round(r["us_per_launch"], 3),
+        },
+        # the same 48 launches per step as floors: the null kernel (the GEMV's grid and loads,
+        # no arithmetic; the reference's --null design), a plain read of the same weight
+        # tensors, and a 16-byte read (what a launch costs with no bytes to move)
+        "floors": {
+            "null_us_per_launch": round(r["null_us_per_launch"], 3),
+            "null_GB/s": round(r["step_bytes"] / (3 * a.rot) / r["null_us_per_launch"] / 1e3, 1),
+            "gemv_frac_of_null": round(r["null_us_per_launch"] / r["us_per_launch"], 4),
+            "read_13MB_us_per_launch": round(r["read_us_per_launch"], 3),
+            "read_GB/s": round(q4_bytes(INTER, HIDDEN) / r["read_us_per_launch"] / 1e3, 1),
+            "empty_us_per_launch": round(r["empty_us_per_launch"], 3),
         },
         "cpu_baseline": cpu,
     }

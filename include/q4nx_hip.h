@@ -72,7 +72,9 @@ typedef struct q4nx_policy {
                          0: on the general VALU GEMV */
   int gemv_ksplit;    /* general VALU GEMV: workgroups per output group along K, 1..8;
                          0 = automatic (default) */
-  int gemv_tiles_per_wave; /* general VALU GEMV: K-tiles per wave, 1, 2 or 4; 0 = automatic */
+  int gemv_tiles_per_wave; /* K-tiles per wave, 1, 2 or 4, of the general VALU GEMV and of the
+                         row-block kernels (where it must leave at most 16 waves per
+                         workgroup, else Q4NX_ERR_ARG); 0 = automatic (default) */
   int gemm_ksplit;    /* matrix-core contraction: workgroups along K, 1..8; 0 = automatic */
   int attn_mfma;      /* 1 (default): attention on the matrix cores; 0: on the VALU kernel */
 } q4nx_policy;
@@ -284,6 +286,22 @@ int q4nx_gqa_decode_records(const uint16_t *q, const uint16_t *k_cache,
                             int64_t kv_b_stride, int64_t kv_h_stride, float scale, int n_split,
                             void *ws, size_t ws_bytes, const q4nx_policy *policy,
                             void *stream);
+
+/* ---------------------------------------------------------------- weight-stream floors
+ * The null GEMV: exactly the grid, workgroup size and per-lane loads of the batch-1 q4 GEMV
+ * (q4nx_gemv_q4 at batch 1 under the default policy: the row-block kernel) and its 16
+ * output stores per workgroup, with no arithmetic: y receives XOR folds of the loaded bits,
+ * not a GEMV. It times what the weight stream alone costs at a shape. Replaces the
+ * reference's null design (designs/granite_gemv/granite_gemv.py:105-121, NULL_SRC; run by
+ * --null at :315-321: "separates 'the kernel is slow' from 'the memory path is slow'").
+ * Shapes as q4nx_gemv_q4; x 8-byte aligned; y fp32 [32*n_tile_rows]. */
+int q4nx_gemv_q4_null(const uint8_t *w, const uint16_t *x, float *y, int n_tile_rows,
+                      int k_tiles, void *stream);
+/* A plain streaming read of bytes (a positive multiple of 16) at buf (16-byte aligned): every
+ * byte loaded once, nothing written unless the fold of a workgroup's bytes hits a fixed
+ * value (then one word of sink[64]). The device counterpart of the STREAM read floor of
+ * designs/granite_gemv/cpu_baseline.cpp:157-166. */
+int q4nx_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream);
 
 /* y[i] = bf16(x[i]), round to nearest even, NaN kept quiet: the device form of the bf16
  * rounding every kernel applies to its outputs (tools/q4nx.py:97-111 rounds the same way

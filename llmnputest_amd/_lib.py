@@ -28,7 +28,7 @@ class Policy(C.Structure):
         ("mfma_rows_q8", c_i),          # the same for q8
         ("rowblock", c_i),              # one-row calls on the row-block kernels
         ("gemv_ksplit", c_i),           # general VALU GEMV: K parts per group, 0 automatic
-        ("gemv_tiles_per_wave", c_i),   # general VALU GEMV: K-tiles per wave, 0 automatic
+        ("gemv_tiles_per_wave", c_i),   # K-tiles per wave (general and row-block), 0 automatic
         ("gemm_ksplit", c_i),           # matrix-core contraction: K parts, 0 automatic
         ("attn_mfma", c_i),             # attention on the matrix cores
     ]
@@ -88,6 +88,8 @@ SIGNATURES: dict[str, tuple] = {
     "q4nx_gqa_decode_records": (c_i, [c_p, c_p, c_p, c_i, c_i, c_i, c_i, c_p, c_i, c_i64,
                                       c_i64, c_f, c_i, c_p, c_sz, c_pol, c_p]),
     "q4nx_gemv_attn_q4": (c_i, [c_p, c_i, c_p, c_i, c_i, c_i, c_p, c_p, c_p, c_p]),
+    "q4nx_gemv_q4_null": (c_i, [c_p, c_p, c_p, c_i, c_i, c_p]),
+    "q4nx_stream_read": (c_i, [c_p, c_sz, c_p, c_p]),
     "q4nx_round_bf16": (c_i, [c_p, c_p, c_i64, c_p]),
     "q4nx_embed": (c_i, [c_i, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p]),
     "q4nx_argmax": (c_i, [c_p, c_i, c_i, c_i64, c_p, c_p, c_p]),

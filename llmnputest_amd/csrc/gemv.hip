@@ -919,7 +919,7 @@ static int gemv_plain(int kind, const uint8_t* w, const void* x, const uint16_t*
     g.residual = residual;
     g.ssq_out = ssq_out;
     g.keys = argmax_keys;
-    return gemv1_launch(G1_PLAIN, g, (hipStream_t)stream, what, kind);
+    return gemv1_launch(G1_PLAIN, g, (hipStream_t)stream, what, kind, P.gemv_tpw);
   }
   GemvArgs a{};
   a.w[0] = w;
@@ -1138,7 +1138,7 @@ int q4nx_qkv_rope(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int n
     g.n_q_heads = n_q_heads;
     g.n_kv_heads = n_kv_heads;
     g.raw_out = raw_out;
-    return gemv1_launch(G1_QKV, g, (hipStream_t)stream, what);
+    return gemv1_launch(G1_QKV, g, (hipStream_t)stream, what, 4, P.gemv_tpw);
   }
   GemvArgs a{};
   a.w[0] = wq;
@@ -1250,7 +1250,7 @@ int q4nx_gate_up_swiglu(const uint8_t* wg, const uint8_t* wu, int n_tile_rows, i
     }
     g.h_out = h_out;
     g.raw_out = raw_out;
-    return gemv1_launch(G1_GATEUP, g, (hipStream_t)stream, what);
+    return gemv1_launch(G1_GATEUP, g, (hipStream_t)stream, what, 4, P.gemv_tpw);
   }
   GemvArgs a{};
   a.w[0] = wg;

@@ -46,8 +46,10 @@ struct Gemv1Args {
 
 int gemv1_tpw(int G, int k_t);
 bool gemv1_fits(int G, int k_t, bool norm);
-int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what,
-                 int kind = 4);   // kind 8 (q8 tiles): plain GEMV only
+// kind 8 (q8 tiles): plain GEMV only. tpw_req: K-tiles per wave (1, 2 or 4), 0 = the fewest
+// that fit the group's K into 16 waves.
+int gemv1_launch(int op, const Gemv1Args& a, hipStream_t s, const char* what, int kind = 4,
+                 int tpw_req = 0);
 int gemv1_attn_launch(const Gemv1Args& a, hipStream_t s, const char* what);
 
 }  // namespace q4nx

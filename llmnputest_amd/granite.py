@@ -264,9 +264,11 @@ class GraniteDecoder:
         ops.embed(table, kind, self.tokens[:b], self.cfg.vocab, self.cfg.hidden, out=self.h[:b],
                   ssq_out=self.ssq[:b])
 
-    def _launch_step(self, b: int, embed: bool = True) -> None:
+    def _launch_step(self, b: int, embed: bool = True, trace: list | None = None) -> None:
         """Every kernel of one decode step for the first b sequences (no allocation); without
-        `embed` the step starts from h as the previous step's advance left it."""
+        `embed` the step starts from h as the previous step's advance left it. With `trace`
+        (eager steps only) the same launches also write their bf16 narrowing points, which are
+        appended per layer as host arrays (see `step`)."""
         c, w = self.cfg, self.w
         kt_h, kt_q, kt_i = c.hidden // 256, c.q_dim // 256, c.inter // 256
         h, q, attn, mlp = self.h[:b], self.q[:b], self.attn[:b], self.mlp[:b]
@@ -277,25 +279,43 @@ class GraniteDecoder:
         fuse_o = self.fuses_attn_o(b, n_split)
         if embed:
             self._embed(b)
+        tr = None
+        if trace is not None:
+            tr = {"raw": torch.empty((b, (c.n_q + 2 * c.n_kv) * c.head_dim), dtype=torch.float32,
+                                     device=self.dev),
+                  "xn": torch.empty((b, c.hidden), dtype=torch.bfloat16, device=self.dev),
+                  "gu": torch.empty((b, 2 * c.inter), dtype=torch.float32, device=self.dev),
+                  "xn2": torch.empty((b, c.hidden), dtype=torch.bfloat16, device=self.dev),
+                  "attn": torch.empty((b, c.n_q, c.head_dim), dtype=torch.bfloat16,
+                                      device=self.dev)}
+            pos_host = self.pos[:b].cpu().numpy()
         for li, L in enumerate(w.layers):
             kc, vc = self.k_cache[li], self.v_cache[li]
             ops.qkv_rope(L["q"], L["k"], L["v"], c.n_q, c.n_kv, kt_h, h, self.pos[:b], self.rope,
                          kc, vc, q_out=q, norm_w=L["norm_in"], eps=c.eps, ws=self.ws,
-                         ssq_in=ssq, policy=pol)
+                         ssq_in=ssq, policy=pol, raw_out=tr and tr["raw"], xn_out=tr and tr["xn"])
             if fuse_o:
                 rec = ops.gqa_decode_records(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b],
                                              n_split, c.scale, max_len=self.max_len, ws=self.ws,
                                              policy=pol)
                 ops.gemv_attn_q4(L["o"], c.hidden // 32, rec, residual=h, out=h, ssq_out=ssq)
+                if tr is not None:   # what the o-projection's merge read: the same bits
+                    ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
+                                   max_len=self.max_len, n_split=n_split, out=tr["attn"],
+                                   ws=self.ws, policy=pol)
             else:
                 ops.gqa_decode(q.view(b, c.n_q, c.head_dim), kc, vc, self.lens[:b], c.scale,
                                max_len=self.max_len, n_split=self.attn_splits, out=attn,
                                ws=self.ws, policy=pol)
                 ops.gemv_ex(L["o"], "q4", attn.view(b, c.q_dim), c.hidden // 32, kt_q,
                             residual=h, out=h, ssq_out=ssq, ws=self.ws, policy=pol)
+                if tr is not None:
+                    tr["attn"].copy_(attn)
             ops.gate_up_swiglu(L["gate"], L["up"], c.inter // 32, kt_h, h, h_out=mlp,
                                norm_w=L["norm_post"], eps=c.eps, ws=self.ws, ssq_in=ssq,
-                               policy=pol)
+                               policy=pol, raw_out=tr and tr["gu"], xn_out=tr and tr["xn2"])
+            if tr is not None:
+                trace.append(self._trace_layer(tr, li, b, pos_host, mlp))
             ops.gemv_ex(L["down"], "q4", mlp, c.hidden // 32, kt_i, residual=h, out=h,
                         ssq_out=ssq, ws=self.ws, policy=pol)
         # final RMSNorm fused into the lm_head prologue, greedy argmax into its epilogue
@@ -303,8 +323,35 @@ class GraniteDecoder:
                     eps=c.eps, out=self.logits[:b], argmax_keys=self.keys[:b], ssq_in=ssq,
                     ws=self.ws, policy=pol)
 
-    def step(self, tokens, positions) -> torch.Tensor:
-        """One decode step, eager: tokens/positions for B sequences -> fp32 logits [B, V]."""
+    def _trace_layer(self, tr: dict, li: int, b: int, pos_host, mlp) -> dict:
+        """Host copies of one layer's bf16 narrowing points (uint16 bits): the normalised
+        inputs, q and k narrowed before the rotation (from the fp32 GEMV outputs), q after
+        it, the k and v rows appended at each sequence's position, the attention output,
+        gate and up narrowed, and the SwiGLU product."""
+        c = self.cfg
+        bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        rnd = lambda t: bits(ops.round_bf16(t.contiguous()))
+        qd, kd = c.n_q * c.head_dim, c.n_kv * c.head_dim
+        raw = tr["raw"]
+        kc, vc = bits(self.k_cache[li][:b]), bits(self.v_cache[li][:b])
+        return {
+            "xn": bits(tr["xn"]), "xn2": bits(tr["xn2"]),
+            "q_pre": rnd(raw[:, :qd]).reshape(b, c.n_q, c.head_dim),
+            "k_pre": rnd(raw[:, qd:qd + kd]).reshape(b, c.n_kv, c.head_dim),
+            "q": bits(self.q[:b]).reshape(b, c.n_q, c.head_dim),
+            "k": np.stack([kc[i, :, pos_host[i]] for i in range(b)]),
+            "v": np.stack([vc[i, :, pos_host[i]] for i in range(b)]),
+            "attn": bits(tr["attn"]),
+            "g": rnd(tr["gu"][:, :c.inter]), "u": rnd(tr["gu"][:, c.inter:]),
+            "m": bits(mlp),
+        }
+
+    def step(self, tokens, positions, trace: list | None = None) -> torch.Tensor:
+        """One decode step, eager: tokens/positions for B sequences -> fp32 logits [B, V].
+        With `trace` (a list), one dict per layer of the step's bf16 narrowing points is
+        appended to it (uint16 bits, keys as DecodeOracle's forced points: "xn", "q_pre",
+        "k_pre", "q", "k", "v", "attn", "xn2", "g", "u", "m"); the step's launches and results
+        are those of an untraced step."""
         tokens = torch.as_tensor(tokens, dtype=torch.int32).reshape(-1)
         positions = torch.as_tensor(positions, dtype=torch.int32).reshape(-1)
         b = tokens.numel()
@@ -315,7 +362,7 @@ class GraniteDecoder:
         self.tokens[:b].copy_(tokens)
         self.pos[:b].copy_(positions)
         self.lens[:b].copy_(positions + 1)
-        self._launch_step(b)
+        self._launch_step(b, trace=trace)
         return self.logits[:b]
 
     # ------------------------------------------------------------ graph + greedy loop

@@ -277,6 +277,36 @@ def decode_advance_embed(keys: torch.Tensor, n_slots: int, tokens: torch.Tensor,
               hidden, _ptr(h), _ptr(ssq_out), _stream())
 
 
+def gemv_q4_null(tiles: torch.Tensor, x: torch.Tensor, n_tile_rows: int, k_tiles: int,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """The weight-stream floor of the batch-1 q4 GEMV: the row-block kernel's grid and loads
+    with no arithmetic (the reference's --null design, designs/granite_gemv/granite_gemv.py:
+    105-121). `out` receives XOR folds of the loaded bits, not y."""
+    _tiles(tiles, "q4", n_tile_rows, k_tiles)
+    _dev(x, "x", torch.bfloat16)
+    if x.numel() != k_tiles * 256:
+        raise Q4NXFormatError(f"x has {x.numel()} values, tiles have K={k_tiles * 256}")
+    if out is None:
+        out = torch.empty(n_tile_rows * 32, dtype=torch.float32, device=x.device)
+    _dev(out, "out", torch.float32)
+    if out.numel() < n_tile_rows * 32:
+        raise ValueError("out must hold N values")
+    _lib.call("q4nx_gemv_q4_null", _ptr(tiles), _ptr(x), _ptr(out), n_tile_rows, k_tiles,
+              _stream())
+    return out
+
+
+def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    """A plain streaming read of every byte of `buf` (contiguous, 16-byte aligned, a multiple
+    of 16 bytes); sink: int32 [64] on the same device, written only on a fixed fold value."""
+    _dev(buf, "buf")
+    _dev(sink, "sink", torch.int32)
+    if sink.numel() < 64:
+        raise ValueError("sink must hold 64 words")
+    nbytes = buf.numel() * buf.element_size()
+    _lib.call("q4nx_stream_read", _ptr(buf), nbytes, _ptr(sink), _stream())
+
+
 def round_bf16(x: torch.Tensor) -> torch.Tensor:
     """bf16 rounding of an fp32 device tensor on the GPU (round to nearest even)."""
     _dev(x, "x", torch.float32)

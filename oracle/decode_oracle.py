@@ -22,6 +22,14 @@ Conventions the reference leaves open and the build fixes:
     token t is row t of a stored embedding matrix when the model has one, else row t of
     the dequantised (tied) lm_head.
 
+`DecodeOracle.step(..., forced=...)` runs the step teacher-forced at its bf16 narrowing
+points: where the caller supplies another implementation's bf16 bits for a point (the GPU's
+normalised inputs, q/k before and after the rotation, the appended v, the attention output,
+gate/up and the SwiGLU product), the oracle checks that they are within one bf16 ulp of its
+own rounding there, counts the one-ulp flips, and continues from those bits. Two correct
+implementations then differ only by floating-point arithmetic error between narrowing
+points, with no flip carried into the next layer.
+
 `DecodeOracle(narrow=False)` runs the same step with every bf16 narrowing point removed
 (float64 throughout); that mode is what the composition is pinned with: it must equal a
 float64 transformers Llama decoder built from the same dequantised weights
@@ -232,8 +240,35 @@ class DecodeOracle:
         # float64 GEMV from tile bytes: the numpy restatement, or the equal C one
         self.gemv = gemv or (lambda raw, kind, x, n_t, k_t: qo.gemv(raw, kind, x, n_t, k_t, acc=np.float64))
         self._mats = {} if mats is None else mats   # float64 matrices (narrow=False), shareable
+        self._forced = None     # {(point, layer): bf16 bits} during a forced step
+        self.flips: dict = {}   # one-ulp flips met at forced points, by point
+        self.recorded: dict | None = None   # set to {} to keep each point's own bf16 bits
 
     # ---- the narrowing points and the GEMV on values
+    def _nb(self, a, name: str, layer: int) -> np.ndarray:
+        """Narrowing point `name` of `layer`: the value rounded to bf16, or, when the step is
+        forced at this point, the given bf16 bits after checking that each is within one
+        ulp of the oracle's own rounding (one-ulp flips counted in self.flips)."""
+        v = self._bf(a)
+        if self.recorded is not None:   # the bits this step narrows to, for a later forcing
+            self.recorded[(name, layer)] = qo.bf16_round(np.asarray(a, np.float64).astype(np.float32))
+        f = None if self._forced is None else self._forced.get((name, layer))
+        if f is None:
+            return v
+        own = qo.bf16_round(np.asarray(a, np.float64).astype(np.float32)).reshape(-1)
+        got = np.asarray(f, np.uint16).reshape(-1)
+        if own.size != got.size:
+            raise ValueError(f"forced {name}[{layer}]: {got.size} values, the step has {own.size}")
+        ordered = lambda b: np.where(b & 0x8000, -(b & 0x7FFF).astype(np.int64),
+                                     (b & 0x7FFF).astype(np.int64))
+        d = np.abs(ordered(own) - ordered(got))
+        if int(d.max(initial=0)) > 1:
+            i = int(np.argmax(d))
+            raise AssertionError(f"forced {name}[{layer}] differs by {int(d[i])} bf16 ulps at "
+                                 f"{i}: {own[i]:#06x} vs {got[i]:#06x}")
+        self.flips[name] = self.flips.get(name, 0) + int((d > 0).sum())
+        return f64(qo.bf16_to_f32(got)).reshape(np.shape(a))
+
     def _bf(self, a) -> np.ndarray:
         """A bf16 narrowing point: the value rounded to bf16 (narrow) or kept (float64)."""
         a = np.asarray(a)
@@ -255,9 +290,21 @@ class DecodeOracle:
             m = self._mats[key] = f64(qo.dequant_matrix(raw, kind, n_t, k_t))
         return f64(xv) @ m.T
 
-    def step(self, tokens, pos) -> np.ndarray:
+    def step(self, tokens, pos, forced: dict | None = None) -> np.ndarray:
         """One decode step for B sequences at positions pos[b]; returns the float64 logits
-        [B, V] and appends this step's k, v to the caches."""
+        [B, V] and appends this step's k, v to the caches. `forced` maps (point, layer) to
+        bf16 bits for a teacher-forced step (see the module docstring); points: "xn", "q_pre",
+        "k_pre", "q", "k", "v", "attn", "xn2", "g", "u", "m" (shapes as the step's values,
+        [B, ...] in the step's order)."""
+        if forced is not None and not self.narrow:
+            raise ValueError("a forced step needs the narrowing oracle")
+        self._forced = forced
+        try:
+            return self._step(tokens, pos)
+        finally:
+            self._forced = None
+
+    def _step(self, tokens, pos) -> np.ndarray:
         c = self.cfg
         w = self.w
         tokens = np.asarray(tokens).ravel()
@@ -269,16 +316,18 @@ class DecodeOracle:
         kt_q = c.n_q * hd // 256
         h = self._res(embedding(w, tokens))
         for layer in range(c.n_layers):
-            xn = self._bf(rmsnorm(h, w.norm_in[layer], c.eps).astype(np.float32)
-                          if self.narrow else rmsnorm(h, w.norm_in[layer], c.eps))
+            xn = self._nb(rmsnorm(h, w.norm_in[layer], c.eps).astype(np.float32)
+                          if self.narrow else rmsnorm(h, w.norm_in[layer], c.eps), "xn", layer)
             q_raw = self._mv(w.wq[layer], "q4", xn, c.n_q * hd // 32, kt_h).reshape(b_n, -1, hd)
             k_raw = self._mv(w.wk[layer], "q4", xn, c.n_kv * hd // 32, kt_h).reshape(b_n, -1, hd)
             v_raw = self._mv(w.wv[layer], "q4", xn, c.n_kv * hd // 32, kt_h).reshape(b_n, -1, hd)
             # q and k narrowed before the rotation, the rotated values narrowed again
             # (designs/granite_gemv/granite_qkv_rope.h:37-69); v only narrowed
-            qr = np.stack([rope(self._bf(q_raw[b]), pos[b], self.table) for b in range(b_n)])
-            kr = np.stack([rope(self._bf(k_raw[b]), pos[b], self.table) for b in range(b_n)])
-            qv, kv, vv = self._bf(qr), self._bf(kr), self._bf(v_raw)
+            q_pre, k_pre = self._nb(q_raw, "q_pre", layer), self._nb(k_raw, "k_pre", layer)
+            qr = np.stack([rope(q_pre[b], pos[b], self.table) for b in range(b_n)])
+            kr = np.stack([rope(k_pre[b], pos[b], self.table) for b in range(b_n)])
+            qv, kv = self._nb(qr, "q", layer), self._nb(kr, "k", layer)
+            vv = self._nb(v_raw, "v", layer)
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             for b in range(b_n):
                 if self.narrow:
@@ -291,15 +340,16 @@ class DecodeOracle:
             kval = qo.bf16_to_f32(kc) if self.narrow else kc
             vval = qo.bf16_to_f32(vc) if self.narrow else vc
             att = gqa_attention(qv, kval, vval, lens, c.scale)
-            ab = self._bf(att.astype(np.float32) if self.narrow else att).reshape(b_n, -1)
+            ab = self._nb(att.astype(np.float32) if self.narrow else att, "attn",
+                          layer).reshape(b_n, -1)
             o = self._mv(w.wo[layer], "q4", ab, c.hidden // 32, kt_q)
             h = self._res(h + o.reshape(b_n, -1))          # residual add (fp32 when narrowing)
-            xn2 = self._bf(rmsnorm(h, w.norm_post[layer], c.eps).astype(np.float32)
-                           if self.narrow else rmsnorm(h, w.norm_post[layer], c.eps))
+            xn2 = self._nb(rmsnorm(h, w.norm_post[layer], c.eps).astype(np.float32)
+                           if self.narrow else rmsnorm(h, w.norm_post[layer], c.eps), "xn2", layer)
             g_raw = self._mv(w.wg[layer], "q4", xn2, c.inter // 32, kt_h)
             u_raw = self._mv(w.wu[layer], "q4", xn2, c.inter // 32, kt_h)
-            sw = swiglu(self._bf(g_raw), self._bf(u_raw))
-            m = self._bf(sw.astype(np.float32) if self.narrow else sw).reshape(b_n, -1)
+            sw = swiglu(self._nb(g_raw, "g", layer), self._nb(u_raw, "u", layer))
+            m = self._nb(sw.astype(np.float32) if self.narrow else sw, "m", layer).reshape(b_n, -1)
             dn = self._mv(w.wd[layer], "q4", m, c.hidden // 32, kt_i)
             h = self._res(h + dn.reshape(b_n, -1))
         hf = self._bf(rmsnorm(h, w.norm_final, c.eps).astype(np.float32)

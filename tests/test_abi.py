@@ -80,6 +80,26 @@ def test_gemv_argument_errors():
     assert rc == ERR_ARG and "ssq_in" in msg               # partial sums without a norm
 
 
+def test_floor_and_tiles_per_wave_errors():
+    """The weight-stream floors validate as the GEMV does; a K-tiles-per-wave request that
+    would need more than 16 waves in a row-block workgroup is refused before any launch."""
+    fake = C.c_void_p(0x10000)
+    rc, msg = rc_msg("q4nx_gemv_q4_null", None, fake, fake, 8, 10, None)
+    assert rc == ERR_ARG and "w must" in msg
+    rc, msg = rc_msg("q4nx_gemv_q4_null", fake, fake, fake, 8, 65, None)
+    assert rc == ERR_SHAPE and "k_tiles" in msg
+    rc, msg = rc_msg("q4nx_gemv_q4_null", fake, fake, fake, 0, 10, None)
+    assert rc == ERR_SHAPE and "n_tile_rows" in msg
+    rc, msg = rc_msg("q4nx_stream_read", fake, 24, fake, None)
+    assert rc == ERR_SHAPE and "multiple of 16" in msg
+    rc, msg = rc_msg("q4nx_stream_read", C.c_void_p(0x10008), 32, fake, None)
+    assert rc == ERR_ARG
+    # K = 8192 (32 K-tiles) at one K-tile per wave would need 32 waves
+    rc, msg = rc_msg("q4nx_gemv_q4", fake, fake, fake, 80, 32, 1, 8192, 2560, None, None, 0,
+                     pol(gemv_tiles_per_wave=1), None)
+    assert rc == ERR_ARG and "16 waves" in msg
+
+
 def test_fused_and_attention_argument_errors():
     fake = C.c_void_p(0x10000)
     rc, msg = rc_msg("q4nx_qkv_rope", fake, fake, fake, 40, 7, 10, fake, 2560, None,

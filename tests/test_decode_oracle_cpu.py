@@ -124,6 +124,57 @@ def test_tiny_decode_step_numpy_equals_c_gemv():
     assert rel < 1e-6 and cos > 0.999999
 
 
+def _tiny_weights(seed=4):
+    cfg = do.DecodeConfig(hidden=256, inter=512, n_layers=2, n_q=4, n_kv=2, head_dim=64,
+                          vocab=96)
+    rng = np.random.default_rng(seed)
+    w = do.DecodeWeights(cfg)
+    h, i, q, kv = cfg.hidden, cfg.inter, cfg.n_q * 64, cfg.n_kv * 64
+    for _ in range(cfg.n_layers):
+        for dst, n, k in ((w.wq, q, h), (w.wk, kv, h), (w.wv, kv, h), (w.wo, h, q), (w.wg, i, h),
+                          (w.wu, i, h), (w.wd, h, i)):
+            dst.append(synth.q4_tiles(rng, n, k).reshape(-1, 5120))
+        w.norm_in.append(synth.f32_to_bf16_bits(1 + 0.1 * rng.standard_normal(h).astype(np.float32)))
+        w.norm_post.append(synth.f32_to_bf16_bits(1 + 0.1 * rng.standard_normal(h).astype(np.float32)))
+    w.norm_final = synth.f32_to_bf16_bits(np.ones(h, np.float32))
+    w.lm_head = synth.q8_tiles(rng, cfg.vocab, h).reshape(-1, 8704)
+    return w
+
+
+def test_forced_step_takes_over_one_ulp_flips_and_rejects_more():
+    """The teacher-forced step (DecodeOracle.step(forced=...)): forced with its own bits it is
+    the unforced step exactly; a one-ulp flip at a point is taken over and counted; a value two
+    ulps away, or a point fed another layer's values (a plausible wiring mistake of the
+    caller), is refused."""
+    w = _tiny_weights()
+    caches = lambda: [synth.random_bf16(np.random.default_rng(9), (1, 2, 40, 64)) for _ in range(2)]
+    own = do.DecodeOracle(w, caches(), caches(), 40)
+    own.recorded = {}
+    ref = own.step([5], [30])
+    rec = own.recorded
+    assert {k[0] for k in rec} == {"xn", "q_pre", "k_pre", "q", "k", "v", "attn", "xn2", "g",
+                                   "u", "m"} and {k[1] for k in rec} == {0, 1}
+    o = do.DecodeOracle(w, caches(), caches(), 40)
+    assert np.array_equal(o.step([5], [30], forced=dict(rec)), ref) and sum(o.flips.values()) == 0
+    m = rec[("m", 0)].copy()
+    m.reshape(-1)[7] += 1
+    flipped = {("m", 0): m}    # only this point forced: the flip then flows into layer 1
+    o = do.DecodeOracle(w, caches(), caches(), 40)
+    got = o.step([5], [30], forced=flipped)
+    assert o.flips["m"] == 1 and not np.array_equal(got, ref)
+    rel, cos = qo.metrics(got, ref)
+    assert rel < 1e-2 and cos > 0.999
+    m2 = rec[("m", 0)].copy()
+    m2.reshape(-1)[7] += 2
+    two = {("m", 0): m2}
+    with pytest.raises(AssertionError, match="2 bf16 ulps"):
+        do.DecodeOracle(w, caches(), caches(), 40).step([5], [30], forced=two)
+    crossed = dict(rec)
+    crossed[("xn", 1)] = rec[("xn", 0)]
+    with pytest.raises(AssertionError, match="xn"):
+        do.DecodeOracle(w, caches(), caches(), 40).step([5], [30], forced=crossed)
+
+
 # ------------------------------------------------------------------ decode-step composition
 
 def _granite_weights(n_layers, vocab, lm_kind, stored_embed, seed, hidden=2560, inter=8192,

@@ -52,6 +52,23 @@ def test_dequant_bitexact(dev, kind, untile):
     assert np.array_equal(got16, qo.bf16_round(f32))
 
 
+@pytest.mark.parametrize("n,k", [(8192, 2560), (2560, 8192)])
+def test_dequant_bitexact_full_granite(dev, n, k):
+    """Config 2's weights dequantised in full: the gate/up 2560->8192 and down 8192->2560
+    tensors (2560 q4 tiles each), fp32 bits and bf16 bits against the oracle's numpy dequant,
+    tiled and un-tiled."""
+    raw, _ = _tiles("q4", n, k, 8)
+    w = _dev_u8(raw, dev)
+    n_t, k_t = n // 32, k // 256
+    f32 = qo.q4_tiles_f32(raw)
+    for untile in (False, True):
+        want = qo.untile(f32, n_t, k_t) if untile else f32
+        got32 = ops.dequant(w, "q4", n_t, k_t, torch.float32, untile).cpu().numpy()
+        assert np.array_equal(got32.view(np.uint32), want.view(np.uint32)), untile
+        got16 = _bits(ops.dequant(w, "q4", n_t, k_t, torch.bfloat16, untile))
+        assert np.array_equal(got16, qo.bf16_round(want)), untile
+
+
 @pytest.mark.parametrize("kind", ["q4", "q8"])
 def test_onehot_exact(dev, kpath, kind):
     n, k = 64, 1024
@@ -122,6 +139,24 @@ def test_gemv_tiles_per_wave(dev, general, k, tiles_per_wave):
     rel, cos = qo.metrics(y1, ref)
     assert rel < REL and cos > COS, (rel, cos)
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))  # deterministic
+
+
+@pytest.mark.parametrize("kind,n,k,tiles_per_wave", [("q4", 8192, 2560, 1), ("q4", 8192, 2560, 2),
+                                                     ("q4", 8192, 2560, 4), ("q4", 2560, 8192, 2),
+                                                     ("q4", 2560, 8192, 4), ("q8", 4096, 1024, 2)])
+def test_rowblock_tiles_per_wave(dev, valu, kind, n, k, tiles_per_wave):
+    """The row-block kernel at every K-tiles-per-wave the policy may ask for: the oracle's
+    answer, and the same bits run after run."""
+    raw, rng = _tiles(kind, n, k, 7)
+    x = synth.random_bf16(rng, k)
+    w, xd = _dev_u8(raw, dev), _dev_bf16(x, dev)
+    ref = qo.gemv(raw, kind, x, n // 32, k // 256, acc=np.float64)
+    pol = ops.current_policy().replace(gemv_tiles_per_wave=tiles_per_wave)
+    y1 = ops.gemv(w, kind, xd, n // 32, k // 256, policy=pol).cpu().numpy()
+    y2 = ops.gemv(w, kind, xd, n // 32, k // 256, policy=pol).cpu().numpy()
+    rel, cos = qo.metrics(y1, ref)
+    assert rel < REL and cos > COS, (rel, cos)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
 @pytest.mark.parametrize("kind", ["q4", "q8"])

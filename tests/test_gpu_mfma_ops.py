@@ -227,3 +227,46 @@ def test_mfma_and_valu_agree(dev):
     for path, (raw_np, hb) in outs.items():   # each path's epilogue on its own accumulators
         rows_close(raw_np, ref, REL, COS)
         assert_bf16_close(hb, do.swiglu_from_raw(raw_np[:, :inter], raw_np[:, inter:]))
+
+
+def test_config3_mlp_batch8_default_policy(dev):
+    """Config 3's MLP at batch 8 as the decode step runs it, under the library's default policy
+    (8 rows go to the matrix cores): [RMSNorm from the producer's sums of squares, gate, up,
+    SwiGLU] on 2560 -> 8192, then down 8192 -> 2560 with the residual added and the sums of
+    squares of the result written. Each stage is held to its own bar on its own input (the
+    reference checks the intermediate h separately, designs/granite_gemv/granite_mlp_full.py:
+    231-254): the normalised input to bf16 rounding, gate/up fp32 accumulators and the down
+    output at 1e-5 of the float64 oracle, h to the oracle's rounding of SwiGLU on the kernel's
+    own accumulators."""
+    rng = np.random.default_rng(88)
+    batch, hid, inter = 8, 2560, 8192
+    pol = ops.Policy()
+    assert pol.mfma_rows_q4 <= batch
+    wg = synth.q4_tiles(rng, inter, hid).reshape(-1, 5120)
+    wu = synth.q4_tiles(rng, inter, hid).reshape(-1, 5120)
+    wd = synth.q4_tiles(rng, hid, inter).reshape(-1, 5120)
+    x_dev, ss_in, nwd, x64 = normed_input(rng, batch, hid, dev)
+    d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
+    raw = torch.empty((batch, 2 * inter), dtype=torch.float32, device=dev)
+    xn = torch.zeros((batch, hid), dtype=torch.bfloat16, device=dev)
+    hb = ops.gate_up_swiglu(d(wg), d(wu), inter // 32, hid // 256, x_dev, norm_w=nwd,
+                            raw_out=raw, ssq_in=ss_in, xn_out=xn, policy=pol)
+    y = torch.empty((batch, hid), dtype=torch.float32, device=dev)
+    ss_out = torch.empty((batch, hid // 16), dtype=torch.float32, device=dev)
+    ops.gemv_ex(d(wd), "q4", hb, hid // 32, inter // 256, residual=x_dev, out=y, ssq_out=ss_out,
+                policy=pol)
+    torch.cuda.synchronize()
+    assert_bf16_close(bits(xn), x64, max_frac=2e-3)
+    x_used = bits(xn)
+    raw_np = raw.cpu().numpy()
+    ref = np.concatenate([qo.gemv(wg, "q4", x_used, inter // 32, hid // 256, acc=np.float64),
+                          qo.gemv(wu, "q4", x_used, inter // 32, hid // 256, acc=np.float64)],
+                         axis=1).reshape(batch, -1)
+    rows_close(raw_np, ref, REL, COS)
+    h_bits = bits(hb)
+    assert_bf16_close(h_bits, do.swiglu_from_raw(raw_np[:, :inter], raw_np[:, inter:]))
+    ref_y = (x_dev.cpu().numpy().astype(np.float64)
+             + qo.gemv(wd, "q4", h_bits, hid // 32, inter // 256, acc=np.float64).reshape(batch, -1))
+    y_np = y.cpu().numpy()
+    rows_close(y_np, ref_y, REL, COS)
+    rows_close(ss_out.cpu().numpy(), ssq16(y_np), REL, COS)
