@@ -405,6 +405,83 @@ def blas_threads() -> tuple[str, int | None]:
     return "unknown", None
 
 
+COLD_COPIES = 3   # q8 head copies rotated by the CPU legs: 3 x 270 MB, past a host's caches
+
+
+def _cpu_time(fn, iters: int) -> float:
+    """Seconds per call of fn after one untimed call."""
+    fn()
+    s = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    return (time.perf_counter() - s) / iters
+
+
+def _q8_cold(w, x, n_t, k_t, threads, copies) -> float:
+    """Seconds per q8 CPU GEMV, rotating `copies` distinct copies of the tiles so that no
+    pass finds its bytes in a cache the previous pass filled."""
+    from oracle import cpu_oracle
+    ws = [w] + [w.copy() for _ in range(copies - 1)]
+    cpu_oracle.q8_baseline_gemv(ws[-1], x, n_t, k_t, threads)
+    s = time.perf_counter()
+    for i in range(3 * copies):
+        cpu_oracle.q8_baseline_gemv(ws[i % copies], x, n_t, k_t, threads)
+    return (time.perf_counter() - s) / (3 * copies)
+
+
+def decode_cpu_composed(ctx: int, threads: int, iters: int = 50) -> dict | None:
+    """A like-for-like CPU decode step of the granite-3B workload, composed from the CPU
+    paths timed on this host: every q4 projection shape (q and o 2560x2560, k and v
+    512x2560, gate and up 8192x2560, down 2560x8192) on the reference's own CPU GEMV
+    (designs/granite_gemv/cpu_baseline.cpp, built into oracle/_ref/, its own timing loop),
+    GQA attention over a context-`ctx` bf16 cache per layer (oracle/cpu_attn.c, rotating 40
+    distinct layer caches), and the q8 lm_head 100352x2560 (oracle/cpu_q8_baseline.c,
+    copies rotated cold). Per token: 40 x (2 q/o + 2 k/v + 2 gate/up + down + attention) +
+    head; the elementwise ops (RMSNorm, RoPE, SwiGLU: about 40 KB per layer) are left out,
+    in the CPU's favour."""
+    try:
+        from oracle import cpu_oracle
+        from llmnputest_amd import synth
+    except Exception as e:  # pragma: no cover
+        print(f"cpu decode baseline unavailable: {e}", file=sys.stderr)
+        return None
+    if not cpu_oracle.REF_BASELINE.exists():
+        return None
+    rng = np.random.default_rng(17)
+    legs = {}
+    for name, (n, k) in (("q_o_2560x2560", (HIDDEN, HIDDEN)), ("k_v_512x2560", (512, HIDDEN)),
+                         ("gate_up_8192x2560", (INTER, HIDDEN)), ("down_2560x8192", (HIDDEN, INTER))):
+        raw = synth.q4_tiles(rng, n, k).reshape(-1)
+        r = cpu_oracle.run_ref_baseline(raw, n // 32, k // 256, threads, iters)
+        legs[name] = r["gemv_ms"]
+    gemv_ms = 2 * legs["q_o_2560x2560"] + 2 * legs["k_v_512x2560"] + \
+        2 * legs["gate_up_8192x2560"] + legs["down_2560x8192"]
+    cfg = GraniteConfig()
+    caches = [(synth.random_bf16(rng, (cfg.n_kv, ctx, 64)), synth.random_bf16(rng, (cfg.n_kv, ctx, 64)))
+              for _ in range(cfg.n_layers)]
+    q = rng.standard_normal((cfg.n_q, 64)).astype(np.float32)
+    cpu_oracle.gqa_decode(q, *caches[-1], ctx, 0.125, threads)
+    s = time.perf_counter()
+    for kc, vc in caches:
+        cpu_oracle.gqa_decode(q, kc, vc, ctx, 0.125, threads)
+    attn_ms = (time.perf_counter() - s) / len(caches) * 1e3
+    del caches
+    wh = synth.q8_tiles(rng, cfg.vocab, cfg.hidden).reshape(-1)
+    xh = synth.random_bf16(rng, cfg.hidden)
+    head_ms = _q8_cold(wh, xh, cfg.vocab // 32, cfg.hidden // 256, threads, COLD_COPIES) * 1e3
+    tok_ms = cfg.n_layers * (gemv_ms + attn_ms) + head_ms
+    return {"value": round(1e3 / tok_ms, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "ms_per_token": round(tok_ms, 3),
+            "legs_ms": {**{k: round(v, 4) for k, v in legs.items()},
+                        "attention_L%d" % ctx: round(attn_ms, 4),
+                        "lm_head_q8_100352x2560_cold": round(head_ms, 3)},
+            "sample": f"per token: 40 x (2 q/o + 2 k/v + 2 gate/up + down on the reference's "
+                      f"cpu_baseline.cpp, {iters} iterations each, + GQA attention at context "
+                      f"{ctx}, oracle/cpu_attn.c over 40 distinct caches) + q8 lm_head "
+                      f"100352x2560 (oracle/cpu_q8_baseline.c, {COLD_COPIES} rotated copies); "
+                      f"{threads} threads"}
+
+
 def cpu_baseline(sample_iters: int) -> dict | None:
     """The reference's own CPU GEMV (designs/granite_gemv/cpu_baseline.cpp, built from its
     source into oracle/_ref/) on the same shapes, all host cores; else the C port."""
@@ -456,17 +533,15 @@ def cpu_baseline(sample_iters: int) -> dict | None:
     w8 = synth.q8_tiles(rng, n8, k8).reshape(-1)
     x8 = synth.random_bf16(rng, k8)
     b8 = w8.size + 2 * k8 + 4 * n8
-    cpu_oracle.q8_baseline_gemv(w8, x8, n8 // 32, k8 // 256, threads)   # warm
-    it8 = 20
-    s = time.perf_counter()
-    for _ in range(it8):
-        cpu_oracle.q8_baseline_gemv(w8, x8, n8 // 32, k8 // 256, threads)
-    t8 = (time.perf_counter() - s) / it8
+    t8w = _cpu_time(lambda: cpu_oracle.q8_baseline_gemv(w8, x8, n8 // 32, k8 // 256, threads), 20)
+    t8 = _q8_cold(w8, x8, n8 // 32, k8 // 256, threads, COLD_COPIES)
     out["lm_head_q8"] = {"value": round(b8 / t8 / 1e9, 2), "unit": "GB/s", "cores": threads,
                          "kind": "port",
                          "sample": f"oracle/cpu_q8_baseline.c (AVX2 + FMA, {threads} threads on "
                                    f"an atomic tile-row counter) on 248320x1024 q8 tiles, "
-                                   f"{it8} iterations"}
+                                   f"{COLD_COPIES} copies (813 MB) rotated so each pass reads "
+                                   f"its 270 MB cold, {3 * COLD_COPIES} passes",
+                         "warm_same_buffer_GBs": round(b8 / t8w / 1e9, 2)}
     from oracle import q4nx_oracle as qo
     s = time.perf_counter()
     qo.gemv(w8, "q8", x8, n8 // 32, k8 // 256)
@@ -557,6 +632,12 @@ def main() -> int:
                                 w=dec["weights"])
         dec.pop("weights")
     sec = None if a.no_secondary else secondary_bench(dev)
+    dec_cpu = None
+    if dec is not None and not a.no_cpu:
+        from oracle import cpu_oracle
+        dec_cpu = decode_cpu_composed(a.ctx, cpu_oracle.host_threads())
+        if dec_cpu is None:
+            dec_cpu = dec.get("cpu")
     gbs = r["gbs"]
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) + decode tok/s, granite-3B shape, batch 1",
@@ -617,8 +698,12 @@ def main() -> int:
             "bytes_per_token": dec["bytes_per_token"],
             "GB/s": round(dec["gbs"], 1),
             "roofline_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
-            "cpu_baseline": dec.get("cpu"),
+            "cpu_baseline": dec_cpu,
         }
+        if dec_cpu is not None and dec.get("cpu") is not None:
+            # the float64 checker's own rate on the same workload, kept apart: it is the
+            # oracle, not a CPU decoder
+            dec_cpu["float64_checker"] = dec["cpu"]
     if dec8 is not None:
         line["decode_batched"] = {
             "workload": f"the same decode with {dec8['batch']} sequences per step (weights read "

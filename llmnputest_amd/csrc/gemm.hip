@@ -32,13 +32,16 @@
 
 namespace q4nx {
 
-// One workgroup of 4 waves owns RT tile-rows x (16 MT WM) rows of X over the K-tiles of its
-// part; WK waves split those K-tiles round-robin and WM = 4 / WK waves take different m-tiles.
-// Each wave stages one tile per tile-row at a time in its own LDS slot while the next tile's
-// bytes are in flight to registers.
-template <int KIND, int OP, int RT, int MT, int WK>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-  constexpr int WM = 4 / WK;
+// One workgroup of NWV waves owns RT tile-rows x (16 MT WM) rows of X over the K-tiles of its
+// part; WK waves split those K-tiles round-robin and WM = NWV / WK waves take different
+// m-tiles. Each wave stages one tile per tile-row at a time in its own LDS slot while the next
+// tile's bytes are in flight to registers. With one m-tile (decode batches) the workgroup has
+// as many waves as its part has K-tiles (up to 10 or 16), so every wave issues all of its
+// loads at once, as the one-row kernels do.
+template <int KIND, int OP, int RT, int MT, int WK, int NWV>
+__global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
+  constexpr int WM = NWV / WK;
+  constexpr int NT = 64 * NWV;              // threads
   constexpr int SLOT = GemmFmt<KIND>::kSlot;
   constexpr int NLD = GemmFmt<KIND>::kLoads;
   constexpr int TB = GemmFmt<KIND>::kTile;
@@ -135,8 +138,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
     asm volatile("" ::: "memory");
-    {  // the last iteration re-reads its own tile (an L2 hit) so the load count stays static
-      const size_t off = (size_t)(it + 1 < n_it ? kt + WK : kt) * TB;
+    if (it + 1 < n_it) {   // wave-uniform: a one-iteration wave issues no second tile
+      const size_t off = (size_t)(kt + WK) * TB;
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     return red + ((m / (16 * MT)) * WK) * RED + (m % (16 * MT)) * NW + n;
   };
   if constexpr (WK > 1) {
-    for (int e = tid; e < MB * NW / 4; e += 256) {
+    for (int e = tid; e < MB * NW / 4; e += NT) {
       const int m = (4 * e) / NW, n = (4 * e) % NW;
       float* dst = outp(m, n);
       float4 v = *(const float4*)dst;
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const uint32_t nrec = MB * NW;           // floats per part record
     const int cnt = group * gridDim.y + mblk;
     const uint32_t rec0 = (uint32_t)(cnt * a.ksplit) * nrec * 4u;
-    for (int e = tid; e < (int)nrec / 4; e += 256)
+    for (int e = tid; e < (int)nrec / 4; e += NT)
       st16_sys(pr, rec0 + (uint32_t)kpart * nrec * 4u + 16u * e,
                *(const uint4*)outp((4 * e) / NW, (4 * e) % NW));
     wait_vm();
@@ -240,7 +243,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     if (tid == 0) s_last = atomicAdd(&a.counters[cnt], 1u) == (unsigned)(a.ksplit - 1) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
-    for (int e = tid; e < (int)nrec / 4; e += 256) {
+    for (int e = tid; e < (int)nrec / 4; e += NT) {
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       for (int p = 0; p < a.ksplit; ++p) {
         const uint4 u = ld16_sys(pr, rec0 + (uint32_t)p * nrec * 4u + 16u * e);
@@ -261,10 +264,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int n_tr = a.n_tr[0];
     const int tr0 = group * RT;
     if (a.argmax_keys != nullptr) {
-      for (int e = tid; e < MB * RT * 2; e += 256) skey[e] = 0ull;
+      for (int e = tid; e < MB * RT * 2; e += NT) skey[e] = 0ull;
       __syncthreads();
     }
-    for (int e0 = 0; e0 < MB * NW; e0 += 256) {   // MB * NW is a multiple of 256
+    for (int e0 = 0; e0 < MB * NW; e0 += NT) {   // MB * NW is a multiple of NT
       const int e = e0 + tid;
       const int m = e / NW, n = e % NW;
       const int gm = mblk * MB + m;
@@ -284,14 +287,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     }
     if (a.argmax_keys != nullptr) {
       __syncthreads();
-      for (int e = tid; e < MB * RT * 2; e += 256) {
+      for (int e = tid; e < MB * RT * 2; e += NT) {
         const int gm = mblk * MB + e / (RT * 2);
         if (gm < a.m_rows) a.argmax_keys[(int64_t)gm * n_tr * 2 + tr0 * 2 + e % (RT * 2)] = skey[e];
       }
     }
   } else if constexpr (OP == GOP_GATEUP) {
     const int64_t N = (int64_t)a.n_tr[0] * 32;
-    for (int e = tid; e < MB * 32; e += 256) {
+    for (int e = tid; e < MB * 32; e += NT) {
       const int m = e >> 5, j = e & 31;
       const int gm = mblk * MB + m;
       if (gm >= a.m_rows) continue;
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     if (seg == 1) seg_off = a.n_q_heads * 64;
     else if (seg == 2) seg_off = (a.n_q_heads + a.n_kv_heads) * 64;
     const int64_t Wd = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
-    for (int e = tid; e < MB * 32; e += 256) {
+    for (int e = tid; e < MB * 32; e += NT) {
       const int m = e >> 5, d = e & 31;
       const int gm = mblk * MB + m;
       if (gm >= a.m_rows) continue;
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h,
 // ---------------------------------------------------------------- host side
 
 struct GemmPlan {
-  int rt, mt, wk, ksplit, kpp, mb, m_blocks, groups;
+  int rt, mt, wk, nwv, ksplit, kpp, mb, m_blocks, groups;
 };
 
 // Workgroup shape by row count: up to 16 rows the four waves split K; more rows go to more
@@ -400,6 +403,7 @@ struct GemmPlan {
 // n_units: tile-rows for PLAIN, output groups (of two tile-rows) for GATEUP and QKV.
 static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows, const Policy& P) {
   GemmPlan p{};
+  p.nwv = 4;
   if (m_rows <= 16) {
     p.mt = 1; p.wk = 4;
   } else if (m_rows <= 32) {
@@ -419,10 +423,21 @@ static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows, co
   p.mb = 16 * p.mt * (4 / p.wk);
   p.m_blocks = (m_rows + p.mb - 1) / p.mb;
   const int wgs = p.groups * p.m_blocks;
+  // one m-tile on a grid that does not fill the chip by itself: as many waves per workgroup
+  // as K-tiles in its part (below), so its K parts follow from that wave count
+  const bool deep = p.mt == 1 && wgs < 512;
+  const int cap = (p.rt == 1 && kind == Q4NX_KIND_Q4) ? 16 : 10;   // waves (LDS, registers)
   int ks = 1;
   const int forced = P.gemm_ksplit;
   if (forced > 0) {
     ks = forced;
+  } else if (deep) {
+    // measured at 8 rows (granite-3B decode): one tile-row per workgroup takes the fewest
+    // parts whose K-tiles fit its waves (o 2560->2560 unsplit 6.1 us against 6.7 with 3
+    // parts, down 8192->2560 in 2 parts 9.8 us); a pair of tile-rows stays whole when the
+    // groups cover the chip ([gate, up] 10.2 us; split 2-3 ways 12-17 us) and else takes
+    // parts of at most 4 K-tiles ([q, k, v]: 3 parts 8.1 us, 1 part 8.5, 5 parts 9.3)
+    ks = p.rt == 1 ? (k_t + cap - 1) / cap : (wgs >= 192 ? 1 : (k_t + 3) / 4);
   } else if (wgs < 192 && k_t >= 4) {
     ks = (240 + wgs - 1) / wgs;
     const int cap = k_t / 2;                 // >= 2 K-tiles per workgroup
@@ -432,6 +447,18 @@ static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows, co
   ks = ks > k_t ? k_t : ks;
   p.kpp = (k_t + ks - 1) / ks;
   p.ksplit = (k_t + p.kpp - 1) / p.kpp;      // no empty parts
+  // one m-tile: the fewest of 4, 8, 10 or 16 waves that give every wave at most one K-tile
+  // of the part (16 only for one q4 tile-row: its LDS slots and registers), so all of a
+  // wave's loads are in flight at once. A grid of 512 workgroups or more keeps 4 waves:
+  // there the LDS of more waves would cost resident workgroups (the q8 lm_head 100352 x 2560
+  // at 8 rows: 64 us with 4 waves, 84 us with 10).
+  if (deep) {
+    for (int w : {4, 8, 10, 16})
+      if (w <= cap && (w >= p.kpp || w == cap)) {
+        p.nwv = p.wk = w;
+        break;
+      }
+  }
   return p;
 }
 
@@ -451,17 +478,22 @@ static size_t gemm_split_bytes(const GemmPlan& p) {
   return part ? Q4NX_WS_COUNTER_BYTES + align256(part) : 0;
 }
 
-template <int KIND, int OP, int RT, int MT, int WK>
+template <int KIND, int OP, int RT, int MT, int WK, int NWV = 4>
 static void gemm_launch_t(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
-  constexpr int lds = 4 * RT * GemmFmt<KIND>::kSlot;
-  static_assert(4 * 16 * MT * RT * 32 * 4 <= lds, "reduction does not fit the staging slots");
+  constexpr int lds = NWV * RT * GemmFmt<KIND>::kSlot;
+  static_assert(NWV * 16 * MT * RT * 32 * 4 <= lds, "reduction does not fit the staging slots");
   const dim3 grid((unsigned)(p.groups * p.ksplit), (unsigned)p.m_blocks);
-  hipLaunchKernelGGL((gemm_kernel<KIND, OP, RT, MT, WK>), grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((gemm_kernel<KIND, OP, RT, MT, WK, NWV>), grid, dim3(64 * NWV), lds, st, a);
 }
 
 template <int KIND, int OP>
 static void gemm_launch_op(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
-  if (p.mt == 1) gemm_launch_t<KIND, OP, (OP == GOP_PLAIN ? 1 : 2), 1, 4>(a, p, st);
+  constexpr int R1 = OP == GOP_PLAIN ? 1 : 2;
+  if (p.mt == 1 && p.nwv == 8) gemm_launch_t<KIND, OP, R1, 1, 8, 8>(a, p, st);
+  else if (p.mt == 1 && p.nwv == 10) gemm_launch_t<KIND, OP, R1, 1, 10, 10>(a, p, st);
+  else if (p.mt == 1 && p.nwv == 16) {
+    if constexpr (KIND == 4 && OP == GOP_PLAIN) gemm_launch_t<KIND, OP, 1, 1, 16, 16>(a, p, st);
+  } else if (p.mt == 1) gemm_launch_t<KIND, OP, R1, 1, 4>(a, p, st);
   else if (p.wk == 4) gemm_launch_t<KIND, OP, (OP == GOP_PLAIN ? 1 : 2), 2, 4>(a, p, st);
   else if (p.wk == 2) gemm_launch_t<KIND, OP, (OP == GOP_PLAIN ? 1 : 2), 2, 2>(a, p, st);
   else if (OP != GOP_PLAIN || p.rt == 2) gemm_launch_t<KIND, OP, 2, 2, 1>(a, p, st);

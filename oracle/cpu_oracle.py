@@ -37,6 +37,9 @@ def lib():
                                   C.c_void_p, C.c_int]
         h.cpu_q8_gemv.restype = C.c_int
         h.cpu_q8_gemv.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int]
+        h.cpu_gqa_decode.restype = C.c_int
+        h.cpu_gqa_decode.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                     C.c_int, C.c_int, C.c_int, C.c_float, C.c_int]
         _lib = h
     return _lib
 
@@ -106,3 +109,22 @@ def q8_baseline_gemv(raw: np.ndarray, x_bf16: np.ndarray, n_t: int, k_t: int,
     if rc != 0:
         raise ValueError("cpu_q8_gemv: bad arguments")
     return y
+
+
+def gqa_decode(q: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, length: int,
+               scale: float = 0.125, threads: int | None = None) -> np.ndarray:
+    """fp32 GQA decode attention of one token on the CPU (cpu_attn.c, AVX2, one thread per
+    core over the query heads): q fp32 [Hq, 64]; K/V bf16 bits [Hkv, L, 64], positions
+    [0, length). Returns fp32 [Hq, 64]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    v = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    hq, hkv, lstride = q.shape[0], k.shape[0], k.shape[1]
+    if q.shape[1] != 64 or k.shape != v.shape or k.shape[2] != 64 or not 0 < length <= lstride:
+        raise ValueError("q [Hq, 64], K/V [Hkv, L, 64], 0 < length <= L")
+    out = np.empty((hq, 64), np.float32)
+    rc = lib().cpu_gqa_decode(q.ctypes.data, k.ctypes.data, v.ctypes.data, out.ctypes.data, hq,
+                              hkv, int(length), lstride, float(scale), threads or host_threads())
+    if rc != 0:
+        raise ValueError(f"cpu_gqa_decode: error {rc}")
+    return out
