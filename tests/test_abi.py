@@ -224,10 +224,11 @@ def test_ws_queries():
     # batch 9 runs on the matrix cores: no split, room for 9 normalised rows
     assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9, None) == 65536 + 9 * 2560 * 2
     # 56 heads of 2 tile-rows, batch 2 on the VALU kernel: 5 parts of 2 K-tiles,
-    # [56][5][batch 2][64]; on the matrix cores (the default from 2 rows): 5 parts of
-    # [16 rows][64] per head, then room for 2 normalised rows of 2560 bf16
+    # [56][5][batch 2][64]; on the matrix cores (the default from 2 rows): parts of at most
+    # 4 K-tiles for a pair of tile-rows on 56 workgroups, 3 of [16 rows][64] per head, then
+    # room for 2 normalised rows of 2560 bf16
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, pol(mfma_rows_q4=0)) == 65536 + 56 * 5 * 2 * 64 * 4
-    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, None) == 65536 + 56 * 5 * 16 * 64 * 4 + 2 * 2560 * 2
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, None) == 65536 + 56 * 3 * 16 * 64 * 4 + 2 * 2560 * 2
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 1, None) == 0     # one row: row-block kernel
     # q8 lm_head at one row: the row-block kernel (the default) needs nothing; on the matrix
     # cores 3136 workgroups, no split, one normalised row
@@ -237,8 +238,9 @@ def test_ws_queries():
     assert lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 64, None) == 0  # one split: no workspace
     big = lib.q4nx_gqa_decode_ws_bytes(1, 40, 8, 32768, pol(attn_mfma=0))   # 64 splits
     assert big == 65536 + 8 * 64 * 5 * 68 * 4
-    # batched contraction: 80 tile-rows x 1 block of 16 rows split 3 ways along K
-    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 8, None) == 65536 + 80 * 3 * 16 * 32 * 4
+    # batched contraction: 80 tile-rows x 1 block of 16 rows, one tile-row per workgroup of
+    # up to 16 waves: 32 K-tiles in 2 parts
+    assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 8, None) == 65536 + 80 * 2 * 16 * 32 * 4
     assert lib.q4nx_gemm_ws_bytes(4, 256, 10, 8, None) == 0      # 256 workgroups: no split
     # 512 rows: 40 pairs of tile-rows x 4 blocks of 128 rows, split 2 ways
     assert lib.q4nx_gemm_ws_bytes(4, 80, 32, 512, None) == 65536 + 160 * 2 * 128 * 64 * 4
