@@ -99,6 +99,22 @@ def test_gemv_parity(dev, kpath, kind, n, k):
     assert rel < REL and cos > COS, (rel, cos)
 
 
+@pytest.mark.parametrize("n,k", [(8192, 2560), (2560, 8192), (2560, 2560), (512, 2560)])
+def test_rowblock_q4_precision(dev, valu, n, k):
+    """The one-row q4 GEMV at the granite projection shapes stays at fp32 accuracy: max|y -
+    y_float64| below 2.5e-7 of max|y| over four seeds (measured 1.06-1.26e-7). Both nibbles
+    enter v_dot2_f32_f16 in bits 4-7 of their fp16 operand; with the low nibble left in bits
+    0-3 (a plausible saving of one instruction) the same shapes measured 3.7-6.3e-7, since the
+    instruction keeps fewer bits of subnormals with leading zeros."""
+    for seed in range(4):
+        rng = np.random.default_rng(100 + seed)
+        raw, _ = _tiles("q4", n, k, 100 + seed)
+        x = synth.random_bf16(rng, k)
+        y = ops.gemv(_dev_u8(raw, dev), "q4", _dev_bf16(x, dev), n // 32, k // 256).cpu().numpy()
+        rel, cos = qo.metrics(y, qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64))
+        assert rel < 2.5e-7 and cos > COS, (seed, rel, cos)
+
+
 def test_gemv_q8_lm_head_full(dev, kpath):
     """Config: y[248320] = W[248320, 1024] @ x, q8 tiles."""
     n, k = 248320, 1024
