@@ -192,3 +192,25 @@ def test_q8_cpu_baseline_vs_oracle():
     col = qo.dequant_matrix(raw, "q8", n // 32, k // 256)[:, 300]
     assert np.array_equal(cpu_oracle.q8_baseline_gemv(raw, xo, n // 32, k // 256, threads=3),
                           col)
+
+
+def test_cpu_attention_baseline_vs_oracle():
+    """The bench's AVX2 GQA decode attention (oracle/cpu_attn.c, the attention leg of the CPU
+    decode baseline) against the float64 oracle attention: fp32 accuracy at one position,
+    lengths that end inside and on a block of 8 positions, and a full context; the same
+    result on 1 and 5 threads; a constant key row gives the mean of V (uniform softmax)."""
+    from oracle import decode_oracle as do
+    rng = np.random.default_rng(31)
+    q = rng.standard_normal((40, 64)).astype(np.float32)
+    k = synth.random_bf16(rng, (8, 300, 64))
+    v = synth.random_bf16(rng, (8, 300, 64))
+    kf, vf = qo.bf16_to_f32(k), qo.bf16_to_f32(v)
+    for length in (1, 7, 8, 9, 257, 300):
+        got = cpu_oracle.gqa_decode(q, k, v, length, 0.125, threads=5)
+        ref = do.gqa_attention(q[None], kf[None], vf[None], [length], 0.125)[0]
+        rel, cos = qo.metrics(got.ravel(), ref.ravel())
+        assert rel < 1e-5 and cos > 0.9999999, (length, rel, cos)
+        assert np.array_equal(got, cpu_oracle.gqa_decode(q, k, v, length, 0.125, threads=1))
+    kc = np.broadcast_to(k[:, :1], k.shape).copy()      # every position the same key
+    got = cpu_oracle.gqa_decode(q, kc, v, 200, 0.125, threads=3)
+    assert np.allclose(got, np.repeat(vf[:, :200].mean(axis=1), 5, axis=0), rtol=1e-5, atol=1e-6)
