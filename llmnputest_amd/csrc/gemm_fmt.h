@@ -28,17 +28,26 @@ struct GemmFmt<8> {
 };
 
 // 8 transposed code bytes (k-slots 0..7 of one row pair) -> bf16 16 + c for the even row (low
-// nibbles) and the odd row (high nibbles).
+// nibbles) and the odd row (high nibbles). The bf16 bits of 16 + c are 0x41 : 0x80 | c << 3, so
+// one shift and mask per word moves every byte's nibble to bits 3-6 under the 0x80, and one
+// byte permute per operand word pairs two such bytes with the exponent byte 0x41.
 __device__ __forceinline__ void q4_operands(i32x2_t r, u32x4_t& ev, u32x4_t& od) {
   const uint32_t w[2] = {(uint32_t)r.x, (uint32_t)r.y};
+  // the mask and the 0x80 bytes as register operands, so each mask-and-set is one v_and_or_b32
+  // (a three-operand instruction takes no literal constant)
+  uint32_t msk, top;
+  asm("v_mov_b32 %0, 0x78787878" : "=v"(msk));
+  asm("v_mov_b32 %0, 0x80808080" : "=v"(top));
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    const uint32_t lo = ((w[h] << 3) & msk) | top;
+    const uint32_t hi = ((w[h] >> 1) & msk) | top;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      // [b(2q), 0, b(2q+1), 0]
-      const uint32_t t = perm(0u, w[h], q ? 0x0C030C02u : 0x0C010C00u);
-      ev[2 * h + q] = ((t & 0x000F000Fu) << 3) | 0x41804180u;
-      od[2 * h + q] = ((t >> 1) & 0x00780078u) | 0x41804180u;
+      // [b(2q), 0x41, b(2q+1), 0x41]
+      const uint32_t sel = q ? 0x04030402u : 0x04010400u;
+      ev[2 * h + q] = perm(0x41414141u, lo, sel);
+      od[2 * h + q] = perm(0x41414141u, hi, sel);
     }
   }
 }

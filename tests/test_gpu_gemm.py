@@ -185,6 +185,7 @@ def _pf_block_rows(m, n):
     (4100, 2016, 512),   # 63 tile-rows: the last workgroup's fourth wave has none; ragged rows
     (2048, 4096, 1024),
     (1544, 8192, 768),   # 128-row blocks; ragged rows, a partial chunk of groups (3 K-tiles)
+    (3100, 4064, 512),   # 128-row blocks, 127 tile-rows: the last workgroup's last wave has none
 ])
 def test_gemm_prefill_parity(dev, kind, m, n, k):
     """Every row against the float64 oracle at the GEMV bar."""
