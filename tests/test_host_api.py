@@ -94,3 +94,24 @@ def test_quantize_q8_roundtrip():
     assert (deq[3, 40:72] == 0).all()
     nat = qo.dequant_tile_bruteforce(t[1, 1], "q8")
     assert np.array_equal(nat, deq[32:64, 256:512])
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """No CPU fallback: with the HIP library absent, the first op raises and names the
+    missing file (checked in a fresh interpreter whose library path points nowhere)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import torch\n"
+            "from llmnputest_amd import ops\n"
+            "try:\n"
+            "    ops.Policy()\n"
+            "except RuntimeError as e:\n"
+            "    print('RAISED', e)\n"
+            "else:\n"
+            "    print('NO ERROR')\n")
+    env = dict(os.environ, Q4NX_LIB=str(tmp_path / "absent" / "libq4nx_hip.so"))
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True,
+                       text=True, timeout=300)
+    assert "RAISED" in r.stdout and "is missing" in r.stdout, (r.stdout, r.stderr[-2000:])
