@@ -44,7 +44,7 @@ struct GemmArgs {
   int max_pos, n_q_heads, n_kv_heads;
   // split K
   int ksplit, kpp;       // workgroups along K, K-tiles per part
-  float* part;           // [group][m_block][part][MB][RT*32] fp32
+  float* part;           // [unit][m_block][part][MB][NW] fp32 (NW: outputs per row)
   uint32_t part_bytes;
   unsigned* counters;    // one arrival counter per (group, m-block)
 };

@@ -37,24 +37,39 @@ namespace q4nx {
 // m-tiles. Each wave stages one tile per tile-row at a time in its own LDS slot while the next
 // tile's bytes are in flight to registers. With one m-tile (decode batches) the workgroup has
 // as many waves as its part has K-tiles (up to 10 or 16), so every wave issues all of its
-// loads at once, as the one-row kernels do.
-template <int KIND, int OP, int RT, int MT, int WK, int NWV>
+// loads at once, as the one-row kernels do. RB (one m-tile, small grids): the two 16-row
+// blocks of each group go to two workgroups, 8 apart (one XCD, so the metadata both stage
+// comes from one L2), each staging the metadata and its block's codes only and taking one
+// operand and one MFMA per tile-row and 32-K group.
+template <int KIND, int OP, int RT, int MT, int WK, int NWV, bool RB = false>
 __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
   constexpr int WM = NWV / WK;
   constexpr int NT = 64 * NWV;              // threads
-  constexpr int SLOT = GemmFmt<KIND>::kSlot;
-  constexpr int NLD = GemmFmt<KIND>::kLoads;
+  constexpr int SLOT = RB ? GemmFmt<KIND>::kSlotRB : GemmFmt<KIND>::kSlot;
+  constexpr int NLD = RB ? GemmFmt<KIND>::kLoadsRB : GemmFmt<KIND>::kLoads;
   constexpr int TB = GemmFmt<KIND>::kTile;
   constexpr int MB = 16 * MT * WM;          // rows of X per workgroup
-  constexpr int NW = RT * 32;               // outputs per row of X per workgroup
+  constexpr int TW = RB ? 16 : 32;          // outputs per tile-row per workgroup
+  constexpr int NW = RT * TW;               // outputs per row of X per workgroup
+  static_assert(!RB || MT == 1, "row-block workgroups: one m-tile");
   static_assert(OP == GOP_PLAIN || RT == 2, "fused epilogues pair two tile-rows");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ int s_last;
-  __shared__ unsigned long long skey[OP == GOP_PLAIN ? MB * RT * 2 : 1];
+  __shared__ unsigned long long skey[OP == GOP_PLAIN ? MB * NW / 16 : 1];
 
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int wk = wave % WK, wm = wave / WK;
-  const int group = blockIdx.x / a.ksplit, kpart = blockIdx.x % a.ksplit;
+  const int unit = blockIdx.x / a.ksplit, kpart = blockIdx.x % a.ksplit;
+  int group = unit, rb = 0;   // RB: the row block of the group's tile-rows
+  if constexpr (RB) {
+    if (((gridDim.x / a.ksplit) & 15) == 0) {
+      group = (unit >> 4) * 8 + (unit & 7);
+      rb = (unit >> 3) & 1;
+    } else {
+      group = unit >> 1;
+      rb = unit & 1;
+    }
+  }
   const int mblk = blockIdx.y;
   const int m0 = mblk * MB + wm * 16 * MT;  // first row of this wave's m-tiles
   const int kbeg = kpart * a.kpp;
@@ -86,12 +101,19 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
   const int c = l & 15, s = l >> 4;         // operand column / k-slot group
   // ds_read_b64_tr_b8 row addresses: lane c of a 16-lane group addresses row (2j + h) with
   // j = c/2, h = c%2 -> k = 8s + j of row-block h (q4) or row half h (q8)
+  // RB: the slot holds the metadata and one block's codes; for q4 both halves of a 16-lane
+  // group address that block, so lanes c and c + 8 receive the same bytes (row pair c % 8)
+  // and take their low / high nibbles
   const int tr_off = KIND == 4
-      ? GemmFmt<4>::kCodes + (c & 1) * 2048 + (8 * s + (c >> 1)) * 8
+      ? GemmFmt<4>::kCodes + (RB ? 0 : (c & 1) * 2048) + (8 * s + (c >> 1)) * 8
       : GemmFmt<8>::kCodes + (8 * s + (c >> 1)) * 16 + (c & 1) * 8;
   // this lane's output column within a tile-row, per operand: q4 even/odd row of pair p of
   // row-block h (c = 8h + p); q8 row c of row-block 0 / 1
-  const int meta_off = KIND == 4 ? 2 * ((c >> 3) * 16 + 2 * (c & 7)) : 2 * c;
+  // (RB: q4 rows 2p, 2p + 1 of the block, the lane keeping row 2p + c / 8; q8 row c of it)
+  const int meta_off = KIND == 4 ? 2 * ((RB ? rb : (c >> 3)) * 16 + 2 * (c & 7))
+                                 : 2 * c + (RB ? rb * 32 : 0);
+  const bool nib = RB && KIND == 4 && (c >> 3);   // RB q4: the high nibble's row
+  const uint32_t rot = nib ? 1u : 29u;
 
   f32x4_t acc[RT][MT][2];
 #pragma unroll
@@ -104,10 +126,18 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
 
   // this lane's 16-byte pieces of a tile: piece i at 16 (64 i + l); the last q8 piece of lanes
   // 32..63 re-reads bytes inside the tile (its LDS copy lands in the slot's padding)
+  // (RB: staged piece i is the metadata below kCodes, then the block's codes)
   int ld_off[NLD];
 #pragma unroll
-  for (int i = 0; i < NLD; ++i)
-    ld_off[i] = 16 * (64 * i + l) - ((KIND == 8 && i == NLD - 1 && l >= 32) ? 512 : 0);
+  for (int i = 0; i < NLD; ++i) {
+    const int o = 16 * (64 * i + l);
+    if constexpr (RB) {
+      constexpr int MC = GemmFmt<KIND>::kCodes, BC = GemmFmt<KIND>::kBlockCodes;
+      ld_off[i] = o < MC ? o : MC + rb * BC + min(o - MC, BC - 16);
+    } else {
+      ld_off[i] = o - ((KIND == 8 && i == NLD - 1 && l >= 32) ? 512 : 0);
+    }
+  }
 
   u32x4_t pf[RT][NLD];
   if (n_it > 0) {
@@ -155,6 +185,30 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         const uint8_t* sl = slot + r * SLOT;
+        if constexpr (RB) {   // one operand: this workgroup's 16 rows
+          u32x4_t op;
+          float dd, mm;
+          if constexpr (KIND == 4) {
+            const i32x2_t cb = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_i32x2_t*)(sl + tr_off + kb * 256));
+            op = q4_operand_rb(cb, rot);
+            const uint32_t dv = *(const uint32_t*)(sl + kb * 64 + meta_off);
+            const uint32_t mv = *(const uint32_t*)(sl + kMetaBytes + kb * 64 + meta_off);
+            dd = nib ? bf16hi(dv) : bf16lo(dv);
+            mm = fmaf(-16.f, dd, nib ? bf16hi(mv) : bf16lo(mv));
+          } else {
+            const i32x2_t cb = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_i32x2_t*)(sl + tr_off + kb * 512));
+            op = q8_operand(cb);
+            dd = bf16_to_f32(*(const uint16_t*)(sl + kb * 64 + meta_off));
+            mm = -128.f * dd;
+          }
+          const f32x4_t p = mfma_bf16(xa[kb][0], op, zero);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[r][0][0][e] = fmaf(mm, sx[0][e], fmaf(dd, p[e], acc[r][0][0][e]));
+          continue;
+        }
         u32x4_t op[2];
         float dd[2], mm[2];
         if constexpr (KIND == 4) {
@@ -199,11 +253,13 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < (RB ? 1 : 2); ++h)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int m = 16 * mt + 4 * s + e;
-          const int n = r * 32 + (KIND == 4 ? (c >> 3) * 16 + 2 * (c & 7) + h : h * 16 + c);
+          // RB: column c holds row 2 (c % 8) + c / 8 (q4) or row c (q8) of the block
+          const int n = RB ? r * 16 + (KIND == 4 ? 2 * (c & 7) + (c >> 3) : c)
+                           : r * 32 + (KIND == 4 ? (c >> 3) * 16 + 2 * (c & 7) + h : h * 16 + c);
           red[wave * RED + m * NW + n] = acc[r][mt][h][e];
         }
   __syncthreads();
@@ -233,7 +289,7 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
   if (a.ksplit > 1) {
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part, a.part_bytes);
     const uint32_t nrec = MB * NW;           // floats per part record
-    const int cnt = group * gridDim.y + mblk;
+    const int cnt = unit * gridDim.y + mblk;
     const uint32_t rec0 = (uint32_t)(cnt * a.ksplit) * nrec * 4u;
     for (int e = tid; e < (int)nrec / 4; e += NT)
       st16_sys(pr, rec0 + (uint32_t)kpart * nrec * 4u + 16u * e,
@@ -263,8 +319,10 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
   if constexpr (OP == GOP_PLAIN) {
     const int n_tr = a.n_tr[0];
     const int tr0 = group * RT;
+    constexpr int NB = NW / 16;               // 16-row blocks per row of X
+    const int blk0 = tr0 * 2 + rb;            // the first one's index along N
     if (a.argmax_keys != nullptr) {
-      for (int e = tid; e < MB * RT * 2; e += NT) skey[e] = 0ull;
+      for (int e = tid; e < MB * NB; e += NT) skey[e] = 0ull;
       __syncthreads();
     }
     for (int e0 = 0; e0 < MB * NW; e0 += NT) {   // MB * NW is a multiple of NT
@@ -272,34 +330,34 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       const int m = e / NW, n = e % NW;
       const int gm = mblk * MB + m;
       const bool live = gm < a.m_rows;
-      const int64_t gn = (int64_t)tr0 * 32 + n;
+      const int64_t gn = (int64_t)blk0 * 16 + n;
       float v = 0.f;
       if (live) {
         v = *outp(m, n);
         if (a.residual != nullptr) v += a.residual[gm * a.y_stride + gn];
         if (a.y != nullptr) a.y[gm * a.y_stride + gn] = v;
-        if (a.argmax_keys != nullptr) atomicMax(&skey[m * RT * 2 + n / 16], argmax_key(v, (uint32_t)gn));
+        if (a.argmax_keys != nullptr) atomicMax(&skey[m * NB + n / 16], argmax_key(v, (uint32_t)gn));
       }
       if (a.ssq_out != nullptr) {   // per 16-row block
         const float sq16 = group16_sum(v * v);
-        if (live && (n & 15) == 0) a.ssq_out[(int64_t)gm * n_tr * 2 + tr0 * 2 + n / 16] = sq16;
+        if (live && (n & 15) == 0) a.ssq_out[(int64_t)gm * n_tr * 2 + blk0 + n / 16] = sq16;
       }
     }
     if (a.argmax_keys != nullptr) {
       __syncthreads();
-      for (int e = tid; e < MB * RT * 2; e += NT) {
-        const int gm = mblk * MB + e / (RT * 2);
-        if (gm < a.m_rows) a.argmax_keys[(int64_t)gm * n_tr * 2 + tr0 * 2 + e % (RT * 2)] = skey[e];
+      for (int e = tid; e < MB * NB; e += NT) {
+        const int gm = mblk * MB + e / NB;
+        if (gm < a.m_rows) a.argmax_keys[(int64_t)gm * n_tr * 2 + blk0 + e % NB] = skey[e];
       }
     }
   } else if constexpr (OP == GOP_GATEUP) {
     const int64_t N = (int64_t)a.n_tr[0] * 32;
-    for (int e = tid; e < MB * 32; e += NT) {
-      const int m = e >> 5, j = e & 31;
+    for (int e = tid; e < MB * TW; e += NT) {   // gate in columns [0, TW), up in [TW, 2 TW)
+      const int m = e / TW, j = e % TW;
       const int gm = mblk * MB + m;
       if (gm >= a.m_rows) continue;
-      const int64_t n = (int64_t)group * 32 + j;
-      const float gr = *outp(m, j), ur = *outp(m, 32 + j);
+      const int64_t n = (int64_t)group * 32 + rb * 16 + j;
+      const float gr = *outp(m, j), ur = *outp(m, TW + j);
       const float h = swiglu(round_bf16_op(gr), round_bf16_op(ur));
       a.h_out[gm * a.h_stride + n] = f32_to_bf16(h);
       if (a.raw_out != nullptr) {
@@ -312,11 +370,12 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
     if (seg == 1) seg_off = a.n_q_heads * 64;
     else if (seg == 2) seg_off = (a.n_q_heads + a.n_kv_heads) * 64;
     const int64_t Wd = (int64_t)(a.n_q_heads + 2 * a.n_kv_heads) * 64;
-    for (int e = tid; e < MB * 32; e += NT) {
-      const int m = e >> 5, d = e & 31;
+    // a head's dims d and d + 32 are rows d of its two tile-rows (RB: d in this block's 16)
+    for (int e = tid; e < MB * TW; e += NT) {
+      const int m = e / TW, d = rb * 16 + e % TW;
       const int gm = mblk * MB + m;
       if (gm >= a.m_rows) continue;
-      const float r0 = *outp(m, d), r1 = *outp(m, 32 + d);
+      const float r0 = *outp(m, e % TW), r1 = *outp(m, TW + e % TW);
       if (a.raw_out != nullptr) {
         a.raw_out[gm * Wd + seg_off + hg * 64 + d] = r0;
         a.raw_out[gm * Wd + seg_off + hg * 64 + 32 + d] = r1;
@@ -394,6 +453,8 @@ __global__ __launch_bounds__(256) void xnorm_kernel(const float* __restrict__ h,
 
 struct GemmPlan {
   int rt, mt, wk, nwv, ksplit, kpp, mb, m_blocks, groups;
+  bool rb;     // one m-tile: a workgroup per 16-row block of each group
+  int units;   // workgroups along N (groups, or twice that with rb)
 };
 
 // Workgroup shape by row count: up to 16 rows the four waves split K; more rows go to more
@@ -459,6 +520,13 @@ static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows, co
         break;
       }
   }
+  // Row-block workgroups when the doubled grid still fits one workgroup per CU (measured at
+  // 8 rows: the o-projection 2560->2560, 80 -> 160 workgroups, 6.79 -> 5.97 us and batch-8
+  // decode 3736 -> 3790 tok/s; launches that already fill the chip lose, as each group's
+  // activation loads, S sums and reduction are then done twice: [gate, up] 9.54 -> 12.47,
+  // down 9.68 -> 14.65 us)
+  p.rb = p.mt == 1 && 2 * p.groups * p.m_blocks * p.ksplit <= 256;
+  p.units = p.groups * (p.rb ? 2 : 1);
   return p;
 }
 
@@ -466,9 +534,9 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // fp32 part records of a split-K launch (0 without a split or with too many counters)
 static size_t split_part_bytes(const GemmPlan& p) {
-  const size_t cnt = (size_t)p.groups * p.m_blocks;
+  const size_t cnt = (size_t)p.units * p.m_blocks;
   if (p.ksplit <= 1 || cnt > Q4NX_WS_COUNTER_BYTES / 4) return 0;
-  return cnt * p.ksplit * p.mb * p.rt * 32 * 4;
+  return cnt * p.ksplit * p.mb * p.rt * (p.rb ? 16 : 32) * 4;
 }
 
 // Workspace layout: arrival counters, the split-K part records, then (for an RMSNorm
@@ -482,7 +550,16 @@ template <int KIND, int OP, int RT, int MT, int WK, int NWV = 4>
 static void gemm_launch_t(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
   constexpr int lds = NWV * RT * GemmFmt<KIND>::kSlot;
   static_assert(NWV * 16 * MT * RT * 32 * 4 <= lds, "reduction does not fit the staging slots");
-  const dim3 grid((unsigned)(p.groups * p.ksplit), (unsigned)p.m_blocks);
+  const dim3 grid((unsigned)(p.units * p.ksplit), (unsigned)p.m_blocks);
+  if constexpr (MT == 1) {
+    if (p.rb) {
+      constexpr int lds_rb = NWV * RT * GemmFmt<KIND>::kSlotRB;
+      static_assert(NWV * 16 * RT * 16 * 4 <= lds_rb, "reduction does not fit the staging slots");
+      hipLaunchKernelGGL((gemm_kernel<KIND, OP, RT, MT, WK, NWV, true>), grid, dim3(64 * NWV),
+                         lds_rb, st, a);
+      return;
+    }
+  }
   hipLaunchKernelGGL((gemm_kernel<KIND, OP, RT, MT, WK, NWV>), grid, dim3(64 * NWV), lds, st, a);
 }
 
