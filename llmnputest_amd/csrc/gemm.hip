@@ -496,9 +496,12 @@ static GemmPlan plan_gemm(int kind, int op, int n_units, int k_t, int m_rows, co
     // measured at 8 rows (granite-3B decode): one tile-row per workgroup takes the fewest
     // parts whose K-tiles fit its waves (o 2560->2560 unsplit 6.1 us against 6.7 with 3
     // parts, down 8192->2560 in 2 parts 9.8 us); a pair of tile-rows stays whole when the
-    // groups cover the chip ([gate, up] 10.2 us; split 2-3 ways 12-17 us) and else takes
-    // parts of at most 4 K-tiles ([q, k, v]: 3 parts 8.1 us, 1 part 8.5, 5 parts 9.3)
-    ks = p.rt == 1 ? (k_t + cap - 1) / cap : (wgs >= 192 ? 1 : (k_t + 3) / 4);
+    // groups cover the chip ([gate, up] 10.2 us; split 2-3 ways 12-17 us) or when twice its
+    // groups fit one workgroup per CU, which then runs row-block workgroups ([q, k, v]: whole
+    // on 112 row-block workgroups 6.9 us, in 3 parts of 4 K-tiles 8.2 us, 2 parts 7.7), and
+    // else takes parts of at most 4 K-tiles
+    ks = p.rt == 1 ? (k_t + cap - 1) / cap
+                   : (wgs >= 192 || 2 * wgs <= 256 ? 1 : (k_t + 3) / 4);
   } else if (wgs < 192 && k_t >= 4) {
     ks = (240 + wgs - 1) / wgs;
     const int cap = k_t / 2;                 // >= 2 K-tiles per workgroup

@@ -224,11 +224,12 @@ def test_ws_queries():
     # batch 9 runs on the matrix cores: no split, room for 9 normalised rows
     assert lib.q4nx_gemv_ws_bytes(4, 256, 10, 9, None) == 65536 + 9 * 2560 * 2
     # 56 heads of 2 tile-rows, batch 2 on the VALU kernel: 5 parts of 2 K-tiles,
-    # [56][5][batch 2][64]; on the matrix cores (the default from 2 rows): parts of at most
-    # 4 K-tiles for a pair of tile-rows on 56 workgroups, 3 of [16 rows][64] per head, then
-    # room for 2 normalised rows of 2560 bf16
+    # [56][5][batch 2][64]; on the matrix cores (the default from 2 rows) the heads run whole
+    # on 112 row-block workgroups: no split records, room for the normalised rows of 2560
+    # bf16. Up to 8 rows the query also sizes for the VALU kernel, whose records are larger.
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, pol(mfma_rows_q4=0)) == 65536 + 56 * 5 * 2 * 64 * 4
-    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, None) == 65536 + 56 * 3 * 16 * 64 * 4 + 2 * 2560 * 2
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 2, None) == 65536 + 56 * 5 * 2 * 64 * 4
+    assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 12, None) == 65536 + 12 * 2560 * 2
     assert lib.q4nx_qkv_rope_ws_bytes(40, 8, 10, 1, None) == 0     # one row: row-block kernel
     # q8 lm_head at one row: the row-block kernel (the default) needs nothing; on the matrix
     # cores 3136 workgroups, no split, one normalised row
