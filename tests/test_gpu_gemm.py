@@ -115,10 +115,12 @@ def test_gemm_residual_strided_x(dev):
 
 
 @pytest.mark.parametrize("parts", [1, 2, 3, 5])
-@pytest.mark.parametrize("m", [3, 30, 100])
-def test_gemm_ksplit_deterministic(dev, parts, m):
-    """Any split of K gives the oracle's result, and the same bits on every call."""
-    n, k = 2560, 8192
+@pytest.mark.parametrize("n,m", [(2560, 3), (2560, 30), (2560, 100),
+                                 (512, 3), (512, 12)])   # 16 tile-rows: row-block workgroups
+def test_gemm_ksplit_deterministic(dev, parts, m, n):
+    """Any split of K gives the oracle's result, and the same bits on every call (with 16
+    tile-rows and one m-tile the parts are row-block workgroups, two per tile-row)."""
+    k = 8192
     raw, rng = _tiles("q4", n, k, 12)
     w = _dev_u8(raw, dev)
     x = synth.random_bf16(rng, (m, k))
@@ -129,6 +131,19 @@ def test_gemm_ksplit_deterministic(dev, parts, m):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
     ref = qo.gemv(raw, "q4", x, n // 32, k // 256, acc=np.float64)
     _check_rows(y1, ref)
+
+
+@pytest.mark.parametrize("parts", [1, 3])
+def test_gemm_q8_rowblock_split(dev, parts):
+    """q8 tiles on row-block workgroups (16 tile-rows, 3 rows), whole and with K in 3 parts:
+    each workgroup stages the scales and its block's 4096 code bytes (the last load of lanes
+    32..63 lands in the slot's padding)."""
+    n, k, m = 512, 8192, 3
+    raw, rng = _tiles("q8", n, k, 15)
+    x = synth.random_bf16(rng, (m, k))
+    y = ops.gemm(_dev_u8(raw, dev), "q8", _dev_bf16(x, dev), n // 32, k // 256,
+                 policy=ops.Policy(gemm_ksplit=parts)).cpu().numpy()
+    _check_rows(y, qo.gemv(raw, "q8", x, n // 32, k // 256, acc=np.float64))
 
 
 @pytest.mark.parametrize("kind", ["q4", "q8"])

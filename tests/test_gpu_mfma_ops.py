@@ -205,6 +205,48 @@ def test_mfma_gate_up_swiglu(dev, mfma, batch, norm):
     assert_bf16_close(bits(hout), do.swiglu_from_raw(raw_np[:, :inter], raw_np[:, inter:]))
 
 
+@pytest.mark.parametrize("parts", [1, 3])
+def test_mfma_rowblock_split_fused(dev, parts):
+    """The fused epilogues on row-block workgroups (two per group: 32 [gate, up] groups and
+    12 [q, k, v] heads at 5 rows), whole and with K in 3 parts: gate/up accumulators and q/k/v
+    (before RoPE) at the GEMV bar, SwiGLU and the rotated q to the oracle's rounding."""
+    rng = np.random.default_rng(95 + parts)
+    hid, inter, batch = 2560, 1024, 5
+    kt = hid // 256
+    pol = ops.Policy(gemm_ksplit=parts)
+    d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
+    x = synth.random_bf16(rng, (batch, hid))
+    wg = synth.q4_tiles(rng, inter, hid).reshape(-1, 5120)
+    wu = synth.q4_tiles(rng, inter, hid).reshape(-1, 5120)
+    raw = torch.empty((batch, 2 * inter), dtype=torch.float32, device=dev)
+    hout = ops.gate_up_swiglu(d(wg), d(wu), inter // 32, kt, bf16_dev(x, dev), raw_out=raw,
+                              policy=pol)
+    raw_np = raw.cpu().numpy()
+    ref = np.concatenate([qo.gemv(wg, "q4", x, inter // 32, kt, acc=np.float64),
+                          qo.gemv(wu, "q4", x, inter // 32, kt, acc=np.float64)],
+                         axis=1).reshape(batch, -1)
+    rows_close(raw_np, ref, REL, COS)
+    assert_bf16_close(bits(hout), do.swiglu_from_raw(raw_np[:, :inter], raw_np[:, inter:]))
+    hq, hkv, lmax = 8, 2, 128
+    wq = synth.q4_tiles(rng, hq * 64, hid).reshape(-1, 5120)
+    wk = synth.q4_tiles(rng, hkv * 64, hid).reshape(-1, 5120)
+    wv = synth.q4_tiles(rng, hkv * 64, hid).reshape(-1, 5120)
+    pos = rng.integers(0, lmax, batch).astype(np.int32)
+    kc = torch.zeros((batch, hkv, lmax, 64), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    rq = torch.empty((batch, (hq + 2 * hkv) * 64), dtype=torch.float32, device=dev)
+    q = ops.qkv_rope(d(wq), d(wk), d(wv), hq, hkv, kt, bf16_dev(x, dev),
+                     torch.from_numpy(pos).to(dev), ops.rope_table(lmax, 64, 10000.0), kc, vc,
+                     raw_out=rq, policy=pol)
+    rq_np = rq.cpu().numpy()
+    ref = np.concatenate([qo.gemv(w_, "q4", x, n, kt, acc=np.float64).reshape(batch, -1)
+                          for w_, n in ((wq, hq * 2), (wk, hkv * 2), (wv, hkv * 2))], axis=1)
+    rows_close(rq_np, ref, REL, COS)
+    qr, _, _ = do.qkv_rope_from_raw(rq_np[:, :hq * 64], rq_np[:, hq * 64:(hq + hkv) * 64],
+                                    rq_np[:, (hq + hkv) * 64:], pos, do.rope_table(lmax, 64, 10000.0))
+    assert_bf16_close(bits(q).reshape(batch, hq, 64), qr)
+
+
 def test_mfma_and_valu_agree(dev):
     """The two kernel families on the same batch-3 inputs: both within the oracle's bar. (Their
     bf16 outputs are not compared with each other: where g is near zero, a 1e-6 absolute
