@@ -199,8 +199,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
     wait_vm();
     __syncthreads();
     if (tid == 0) {
-      const unsigned prev = atomicAdd(&a.counters[bk], 1u);
-      *s_last = (prev == (unsigned)(a.n_split - 1)) ? 1 : 0;
+      *s_last = ticket(&a.counters[bk], a.n_split) ? 1 : 0;
     }
     __syncthreads();
     if (!*s_last) return;
@@ -233,8 +232,6 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, float (*s_fin)[kP
         }
       }
     }
-    if (tid == 0)  // ready for the next call
-      __hip_atomic_store(&a.counters[bk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
   }
 

@@ -116,6 +116,14 @@ __device__ __forceinline__ float load_sys(const float* p) {
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Arrival ticket of one of `parts` workgroups on a counter that starts at 0: true for the
+// last to arrive. The increment wraps (atomicInc: old >= parts - 1 stores 0), so the last
+// arrival leaves the counter at 0 for the next launch with no store of its own; a separate
+// system-scope reset at the end of the merge cost 0.2-0.26 us per launch.
+__device__ __forceinline__ bool ticket(unsigned* counter, int parts) {
+  return atomicInc(counter, (unsigned)(parts - 1)) == (unsigned)(parts - 1);
+}
+
 // Attention split record: per (sequence, kv head, split, query head of the group) the fp32
 // acc[64] of the split's positions, its running max m (scale*log2e units) at [64], its sum l
 // at [65], two pad words; records of one (sequence, kv head) consecutive by split.

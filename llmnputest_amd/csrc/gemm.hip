@@ -296,7 +296,7 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
                *(const uint4*)outp((4 * e) / NW, (4 * e) % NW));
     wait_vm();
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&a.counters[cnt], 1u) == (unsigned)(a.ksplit - 1) ? 1 : 0;
+    if (tid == 0) s_last = ticket(&a.counters[cnt], a.ksplit) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
     for (int e = tid; e < (int)nrec / 4; e += NT) {
@@ -310,8 +310,6 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       }
       *(float4*)outp((4 * e) / NW, (4 * e) % NW) = v;
     }
-    if (tid == 0)   // ready for the next launch
-      __hip_atomic_store(&a.counters[cnt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
   }
 

@@ -553,7 +553,7 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
     }
     wait_vm();
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&a.counters[group], 1u) == (unsigned)(ks - 1) ? 1 : 0;
+    if (tid == 0) s_last = ticket(&a.counters[group], ks) ? 1 : 0;
     __syncthreads();
     if (!s_last) return false;
     const uint32_t rec0 = (uint32_t)(group * ks * nrec) * 4u;
@@ -577,8 +577,6 @@ __device__ __forceinline__ bool gemv_body(const GemvArgs& a, const int blk) {
       sgrp[b][r + 2] = acc4.z;
       sgrp[b][r + 3] = acc4.w;
     }
-    if (tid == 0)  // ready for the next launch
-      __hip_atomic_store(&a.counters[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
   }
 
