@@ -326,9 +326,10 @@ int q4nx_argmax(const float *logits, int n, int batch, int64_t stride, int32_t *
 int q4nx_decode_advance(const uint64_t *keys, int n_slots, int32_t *tokens, int32_t *pos,
                         int32_t *lens, int32_t *history, int32_t *step, int history_len,
                         int batch, void *stream);
-/* q4nx_decode_advance, then q4nx_embed of the new tokens into h / ssq_out in the same launch
- * (batch 1..64): a greedy loop's next step starts from h with no embedding launch. No
- * reference counterpart (the reference has no token loop, README.md:295-311). */
+/* q4nx_decode_advance, then q4nx_embed of the new tokens into h / ssq_out (batch 1..64): a
+ * greedy loop's next step starts from h with no embedding launch of its own. One launch at
+ * batch 1; from batch 2 one workgroup per row, then a one-wave launch for the history and the
+ * step counter. No reference counterpart (the reference has no token loop, README.md:295-311). */
 int q4nx_decode_advance_embed(const uint64_t *keys, int n_slots, int32_t *tokens, int32_t *pos,
                               int32_t *lens, int32_t *history, int32_t *step, int history_len,
                               int batch, int kind, const void *table, int vocab, int hidden,

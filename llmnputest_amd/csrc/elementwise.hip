@@ -208,6 +208,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 // ------------------------------------------------------------------ decode bookkeeping
 // keys: [batch][n_slots] order-preserving argmax keys (one per lm_head tile-row). With s_tok,
 // token b is also left in s_tok[b] (batch <= kAdvanceEmbedMaxBatch) for the whole workgroup.
+// Without step (a workgroup of one row of several), the history and the step counter are
+// left to decode_step_kernel.
 constexpr int kAdvanceEmbedMaxBatch = 64;
 
 // max(k, k of the lane DPP control CTRL names), 64-bit (the two halves move together)
@@ -257,7 +259,7 @@ __device__ __forceinline__ void decode_advance_body(
   const int n_waves = (int)(blockDim.x >> 6);
   const int wpr = batch >= n_waves ? 1 : n_waves / batch;
   const int groups = n_waves / wpr;
-  const int s = step[0];
+  const int s = step != nullptr ? step[0] : 0;
   for (int b0 = 0; b0 < batch; b0 += groups) {
     const int b = b0 + wave / wpr, sub = wave % wpr;
     const bool active = wave < groups * wpr && b < batch;
@@ -286,12 +288,13 @@ __device__ __forceinline__ void decode_advance_body(
         if (s_tok != nullptr) s_tok[b] = tok;
         pos[b] = p_old + 1;
         lens[b] = p_old + 2;
-        if (history != nullptr && s < history_len) history[(int64_t)s * batch + b] = tok;
+        if (step != nullptr && history != nullptr && s < history_len)
+          history[(int64_t)s * batch + b] = tok;
       }
     }
     __syncthreads();
   }
-  if (tid == 0) step[0] = s + 1;
+  if (tid == 0 && step != nullptr) step[0] = s + 1;
 }
 
 __global__ __launch_bounds__(1024) void decode_advance_kernel(
@@ -302,18 +305,26 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
                       nullptr);
 }
 
-// The same, then the embedding rows of the new tokens (as embed_kernel): the next step's
-// input is ready when the launch ends, with no launch of its own.
+// history[step][b] = tokens[b] while step < history_len, then step += 1: the end of a greedy
+// step whose rows were advanced by one workgroup each. One wave: every lane loads the
+// counter before lane 0 stores it.
+__global__ __launch_bounds__(64) void decode_step_kernel(const int32_t* __restrict__ tokens,
+                                                         int32_t* __restrict__ history,
+                                                         int32_t* __restrict__ step,
+                                                         int history_len, int batch) {
+  const int s = step[0];
+  if (history != nullptr && s < history_len)
+    for (int b = (int)threadIdx.x; b < batch; b += 64) history[(int64_t)s * batch + b] = tokens[b];
+  if (threadIdx.x == 0) step[0] = s + 1;
+}
+
+// The embedding rows of s_tok[0..batch) into h / ssq_out (as embed_kernel), by all 1024
+// threads of the workgroup.
 template <int KIND>
-__global__ __launch_bounds__(1024) void decode_advance_embed_kernel(
-    const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
-    int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
-    int32_t* __restrict__ step, int history_len, int batch, const uint8_t* __restrict__ table,
-    int vocab, int hidden, float* __restrict__ h, float* __restrict__ ssq_out) {
-  __shared__ int s_tok[kAdvanceEmbedMaxBatch];
-  decode_advance_body(keys, n_slots, tokens, pos, lens, history, step, history_len, batch,
-                      s_tok);
-  __syncthreads();
+__device__ __forceinline__ void embed_rows(const int* s_tok, int batch,
+                                           const uint8_t* __restrict__ table, int vocab,
+                                           int hidden, float* __restrict__ h,
+                                           float* __restrict__ ssq_out) {
   // Four 1024-entry chunks of the [batch][hidden] rows at a time, across row boundaries:
   // every load of the chunks is issued before the first value is stored, so a group of
   // chunks costs one memory round trip (eight rows of 2560: five, against one per row and
@@ -345,6 +356,38 @@ __global__ __launch_bounds__(1024) void decode_advance_embed_kernel(
       }
     }
   }
+}
+
+// The advance, then the embedding rows of the new tokens: the next step's input is ready
+// when the launch ends, with no launch of its own. One workgroup for all rows.
+template <int KIND>
+__global__ __launch_bounds__(1024) void decode_advance_embed_kernel(
+    const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
+    int32_t* __restrict__ pos, int32_t* __restrict__ lens, int32_t* __restrict__ history,
+    int32_t* __restrict__ step, int history_len, int batch, const uint8_t* __restrict__ table,
+    int vocab, int hidden, float* __restrict__ h, float* __restrict__ ssq_out) {
+  __shared__ int s_tok[kAdvanceEmbedMaxBatch];
+  decode_advance_body(keys, n_slots, tokens, pos, lens, history, step, history_len, batch,
+                      s_tok);
+  __syncthreads();
+  embed_rows<KIND>(s_tok, batch, table, vocab, hidden, h, ssq_out);
+}
+
+// The same with one workgroup per row (blockIdx.x): the row's token, position, length and
+// embedding row; decode_step_kernel then writes the history and advances the step. Eight
+// rows of a 6272-key head: 18.3 us from one workgroup, as many rows in parallel here.
+template <int KIND>
+__global__ __launch_bounds__(1024) void decode_rows_embed_kernel(
+    const unsigned long long* __restrict__ keys, int n_slots, int32_t* __restrict__ tokens,
+    int32_t* __restrict__ pos, int32_t* __restrict__ lens, const uint8_t* __restrict__ table,
+    int vocab, int hidden, float* __restrict__ h, float* __restrict__ ssq_out) {
+  __shared__ int s_tok[1];
+  const int b = blockIdx.x;
+  decode_advance_body(keys + (int64_t)b * n_slots, n_slots, tokens + b, pos + b, lens + b,
+                      nullptr, nullptr, 0, 1, s_tok);
+  __syncthreads();
+  embed_rows<KIND>(s_tok, 1, table, vocab, hidden, h + (int64_t)b * hidden,
+                   ssq_out != nullptr ? ssq_out + (int64_t)b * (hidden / 16) : nullptr);
 }
 
 }  // namespace q4nx
@@ -466,6 +509,20 @@ int q4nx_decode_advance_embed(const uint64_t* keys, int n_slots, int32_t* tokens
   const auto* k = (const unsigned long long*)keys;
   const uint8_t* w = (const uint8_t*)table;
   hipStream_t s = (hipStream_t)stream;
+  if (batch > 1) {   // a workgroup per row, then the history and the step counter
+    if (kind == Q4NX_KIND_BF16)
+      hipLaunchKernelGGL(decode_rows_embed_kernel<Q4NX_KIND_BF16>, dim3(batch), dim3(1024), 0,
+                         s, k, n_slots, tokens, pos, lens, w, vocab, hidden, h, ssq_out);
+    else if (kind == Q4NX_KIND_Q8)
+      hipLaunchKernelGGL(decode_rows_embed_kernel<Q4NX_KIND_Q8>, dim3(batch), dim3(1024), 0, s,
+                         k, n_slots, tokens, pos, lens, w, vocab, hidden, h, ssq_out);
+    else
+      hipLaunchKernelGGL(decode_rows_embed_kernel<Q4NX_KIND_Q4>, dim3(batch), dim3(1024), 0, s,
+                         k, n_slots, tokens, pos, lens, w, vocab, hidden, h, ssq_out);
+    hipLaunchKernelGGL(decode_step_kernel, dim3(1), dim3(64), 0, s, tokens, history, step,
+                       history_len, batch);
+    return check_launch(what);
+  }
   if (kind == Q4NX_KIND_BF16)
     hipLaunchKernelGGL(decode_advance_embed_kernel<Q4NX_KIND_BF16>, dim3(1), dim3(1024), 0, s, k,
                        n_slots, tokens, pos, lens, history, step, history_len, batch, w, vocab,

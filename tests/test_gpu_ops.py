@@ -444,7 +444,7 @@ def test_decode_advance_against_numpy(dev, batch):
     assert int(step.cpu()) == 3
 
 
-@pytest.mark.parametrize("kind,batch", [("q8", 1), ("q4", 3), ("bf16", 2)])
+@pytest.mark.parametrize("kind,batch", [("q8", 1), ("q4", 3), ("bf16", 2), ("q8", 8), ("q4", 64)])
 def test_decode_advance_embed_equals_advance_then_embed(dev, kind, batch):
     """The fused greedy-loop launch (argmax keys -> token, positions, history, then the token's
     embedding row and its sums of squares) writes exactly what decode_advance followed by
