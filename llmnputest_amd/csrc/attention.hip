@@ -451,8 +451,9 @@ __device__ __forceinline__ void attn_mfma_round(MfmaLane& st, const u32x4_t (&kr
   }
 }
 
-// NW waves of 32 positions per round (4, or 8 for launches whose splits are longer than a
-// 4-wave round: one round of 256 positions instead of two of 128).
+// NW waves of 32 positions per round (4; 8 for launches whose splits are longer than a
+// 4-wave round: one round of 256 positions instead of two of 128; 12 for splits of 513-768
+// positions: two rounds of 384 instead of three of 256).
 template <int G, bool NT, int NW = kAttnWaves>
 __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
   static_assert(G * 32 <= 256 && G <= 16, "one thread per (head, split) in the merge");
@@ -502,6 +503,12 @@ __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
   for (int u = 0; u < 4; ++u) st.o[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int end = min(stop, max(0, a.lens[b]));
   const int nr = end > start ? (end - start + R - 1) / R : 0;
+  if constexpr (NW > 8) {
+    // launched only for splits of at most two rounds (launch_attn), both in flight from the
+    // start: two buffers, 88 VGPRs where the three-buffer loop takes 170
+    if (nr > 0) attn_mfma_round(st, kA, vA, start + wo, end, g, a.scale_l2);
+    if (nr > 1) attn_mfma_round(st, kB, vB, start + R + wo, end, g, a.scale_l2);
+  } else
   for (int r = 0; r < nr; r += 3) {
     const int p0 = start + r * R + wo;   // this wave's first position of round r
     if (r + 2 < nr) attn_mfma_load<NT>(kbase, vbase, p0 + 2 * R, stop, j, g, kC, vC);
@@ -614,7 +621,12 @@ static void launch_attn(const AttnArgs& a, bool mfma, dim3 grid, hipStream_t s) 
   // kernel, bit for bit; batch 8 at context 2048 with 8 splits, 512 workgroups: 3379 tok/s on
   // 4 waves against 3169 on 8)
   const bool wide = attn_wide(a.chunk, (long long)grid.x);
-  if (mfma && nt && wide)
+  // a split of 513-768 positions: two rounds of 12 waves instead of three of 8 (batch 8 at
+  // context 2112, 3 splits of 704: decode 3912 -> 3943 tok/s; 16 waves, two rounds of 512,
+  // read 3855)
+  if (mfma && !nt && wide && a.chunk > 2 * 2 * kAttnRound && a.chunk <= 2 * 3 * kAttnRound)
+    hipLaunchKernelGGL((gqa_mfma_kernel<G, false, 12>), grid, dim3(768), 0, s, a);
+  else if (mfma && nt && wide)
     hipLaunchKernelGGL((gqa_mfma_kernel<G, true, 8>), grid, dim3(512), 0, s, a);
   else if (mfma && nt) hipLaunchKernelGGL((gqa_mfma_kernel<G, true>), grid, dim3(256), 0, s, a);
   else if (mfma && wide)

@@ -263,7 +263,7 @@ def test_gate_up_swiglu(dev, vpath, batch, norm, ksplit):
 
 @pytest.mark.parametrize("batch,L,ragged", [
     (1, 1, False), (1, 32, False), (1, 100, False), (1, 512, False), (1, 4096, False),
-    (8, 512, True), (8, 4096, False), (1, 32768, False),
+    (8, 512, True), (8, 2112, True), (8, 4096, False), (1, 32768, False),
 ])
 def test_gqa_decode(dev, apath, batch, L, ragged):
     rng = np.random.default_rng(15 + L)
@@ -338,7 +338,7 @@ def test_gqa_decode_group_sizes(dev, apath, hq, hkv, L):
     assert np.array_equal(of1, of2)
 
 
-@pytest.mark.parametrize("n_split", [1, 2, 7, 33])
+@pytest.mark.parametrize("n_split", [1, 2, 3, 7, 33])
 def test_gqa_decode_splits(dev, apath, n_split):
     rng = np.random.default_rng(17)
     L = 2100
@@ -486,6 +486,7 @@ def test_decode_advance_embed_equals_advance_then_embed(dev, kind, batch):
 
 @pytest.mark.parametrize("hq,hkv,L,lmax,n_split,n_out", [
     (40, 8, 2112, 2176, 9, 2560),    # the 3B decode shape at the policy's split count (8 waves)
+    (40, 8, 2112, 2176, 3, 2560),    # splits of 728 positions: two rounds of 12 waves
     (40, 8, 2112, 2176, 17, 2560),   # the same with 17 splits (4 waves)
     (40, 8, 2112, 2176, 18, 2560),   # the most splits the merge holds
     (40, 8, 300, 320, 1, 512),       # one split still publishes a record
