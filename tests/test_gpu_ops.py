@@ -356,6 +356,27 @@ def test_gqa_decode_splits(dev, apath, n_split):
     assert not ws.buf[:ops.WS_COUNTER_BYTES].cpu().numpy().any()
 
 
+def test_gqa_decode_split_edges_b8(dev, apath):
+    """Batch 8 at a 2176-position cache (the decode step's attention: 3 splits of 728
+    positions, two rounds each) with lengths at the edges of splits and rounds: an empty
+    sequence (all zeros), one position, the last position of a round and of a split and the
+    first past them, and a full cache."""
+    rng = np.random.default_rng(23)
+    B, hq, hkv, L = 8, 40, 8, 2176
+    q = synth.random_bf16(rng, (B, hq, 64))
+    k = synth.random_bf16(rng, (B, hkv, L, 64))
+    v = synth.random_bf16(rng, (B, hkv, L, 64))
+    lens = np.array([0, 1, 384, 385, 728, 729, 1500, 2176], np.int32)
+    out, of = ops.gqa_decode(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
+                             torch.from_numpy(lens).to(dev), 0.125, want_f32=True)
+    got = of.cpu().numpy()
+    assert not got[0].any()
+    ref = do.gqa_attention(qo.bf16_to_f32(q[1:]), qo.bf16_to_f32(k[1:]), qo.bf16_to_f32(v[1:]),
+                           lens[1:], 0.125)
+    assert_close(got[1:], ref)
+    assert_bf16_close(bits(out)[1:], ref)
+
+
 def test_gqa_decode_garbage_past_length(dev, apath):
     """Cache rows at and past a sequence's length take no part in the result whatever they
     hold: K = +Inf and V = NaN bit patterns there leave the output equal to the oracle's on
