@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/q4nx_hip.h"
 
 namespace q4nx {
@@ -193,10 +195,20 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8 lanes
 constexpr int kDppRor4 = 0x124;       // rotate by 4 inside each row of 16 lanes
 constexpr int kDppRor8 = 0x128;       // rotate by 8 inside each row of 16 lanes
+constexpr int kDppRowBcast = 0x150;   // + n: lane n of each row of 16 lanes to the whole row
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
+// f(std::integral_constant<int, I>) for I = B .. E-1, each with I a constant expression.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // All-reduce over aligned groups of 16 or 32 lanes; every lane of the group ends with the
 // bit-identical result (each step combines the same two values in either order).
 __device__ __forceinline__ float group16_max(float v) {

@@ -223,7 +223,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   uint2 nv[TPW];          // bf16 norm_w[k .. k+3]
   float4 sq[NORM ? NSS : 1];
   float4 racc[XREC ? XNS : 1];
-  float2 rml[XREC ? XNS : 1];
+  float2 rml[XREC ? (XNS + 15) / 16 : 1];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     const int k = min(kt0 + t, k_t - 1) * kTileK + k0;
@@ -243,7 +243,14 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
       for (int i = 0; i < XNS; ++i) {
         const char* ri = (const char*)xin + (size_t)((uint32_t)i * rs);   // uniform base
         racc[i] = *(const float4*)(ri + oa);
-        rml[i] = *(const float2*)(ri + ob);
+      }
+      // (m, l) of one split per lane: the 16 lanes of a head (a DPP row) hold splits
+      // lane % 16 (+ 16), and the merge broadcasts them along the row, so the wave loads
+      // 8 bytes per lane instead of 8 per lane and split (a third of the record bytes)
+#pragma unroll
+      for (int u = 0; u < (XNS + 15) / 16; ++u) {
+        const uint32_t s = (uint32_t)min((lane & 15) + 16 * u, XNS - 1);
+        rml[u] = *(const float2*)((const char*)xin + (s * rs + ob));
       }
     } else if constexpr (NORM) {
       hv[t] = *(const float4*)((const float*)xin + k);
@@ -304,21 +311,32 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   // ---- 2. activations: as given, RMSNorm of h, or merged attention records; bf16 bits
   uint2 xr[TPW];
   if constexpr (XREC) {   // the split merge of attention's own finish, in split order
+    // M over the head's splits (a max: any order gives the same value), then split s's
+    // weight exp2(m_s - M) from the lane that holds it, broadcast with l_s along the row
+    constexpr int XMU = (XNS + 15) / 16;
+    float mj[XMU], fj[XMU];
     float M = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < XNS; ++i) M = fmaxf(M, rml[i].x);
-    float L = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int i = 0; i < XNS; ++i) {
-        const float f = __builtin_amdgcn_exp2f(rml[i].x - M);
-        L = fmaf(rml[i].y, f, L);
-        A0 = fmaf(racc[i].x, f, A0);
-        A1 = fmaf(racc[i].y, f, A1);
-        A2 = fmaf(racc[i].z, f, A2);
-        A3 = fmaf(racc[i].w, f, A3);
-      }
+    for (int u = 0; u < XMU; ++u) {
+      mj[u] = (lane & 15) + 16 * u < XNS ? rml[u].x : -INFINITY;
+      M = fmaxf(M, mj[u]);
     }
+    M = group16_max(M);
+    // an empty head (every m = -inf) weighs its zero records by exp2(-inf) = 0
+    const float Mb = M == -INFINITY ? 0.f : M;
+#pragma unroll
+    for (int u = 0; u < XMU; ++u) fj[u] = __builtin_amdgcn_exp2f(mj[u] - Mb);
+    float L = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
+    static_for<0, XNS>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const float f = dpp<kDppRowBcast + (i & 15)>(fj[i / 16]);
+      const float l = dpp<kDppRowBcast + (i & 15)>(rml[i / 16].y);
+      L = fmaf(l, f, L);
+      A0 = fmaf(racc[i].x, f, A0);
+      A1 = fmaf(racc[i].y, f, A1);
+      A2 = fmaf(racc[i].z, f, A2);
+      A3 = fmaf(racc[i].w, f, A3);
+    });
     const float o0 = L > 0.f ? attn_div(A0, L) : 0.f, o1 = L > 0.f ? attn_div(A1, L) : 0.f;
     const float o2 = L > 0.f ? attn_div(A2, L) : 0.f, o3 = L > 0.f ? attn_div(A3, L) : 0.f;
     xr[0] = make_uint2(pack_bf16x2_op(o0, o1), pack_bf16x2_op(o2, o3));
