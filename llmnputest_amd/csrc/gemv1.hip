@@ -132,6 +132,13 @@ template <int OP, int G, int TPW, int NSS, int XNS, int HB, int KIND>
 __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   constexpr bool NORM = NSS > 0;
   constexpr bool XREC = XNS > 0;
+  // The two members of a normalised group ([q, k, v] heads' tile-row pairs, gate and up)
+  // read the same activations: the member-0 wave of each K-chunk loads and normalises them
+  // and hands the fp16 operands, their group sums and scale to the member-1 wave through
+  // LDS, so half the waves load neither h nor the norm weights nor the sums of squares (at
+  // two workgroups per CU a quarter of the bytes each CU takes in)
+  constexpr bool SHARE = NORM && G == 2;
+  __shared__ uint32_t xsh[SHARE ? 8 : 1][SHARE ? 3 * TPW + 1 : 1][64];
   static_assert(HB == 16 || (HB == 8 && OP == G1_QKV), "half row blocks: q/k/v only");
   static_assert(KIND == 4 || (KIND == 8 && OP == G1_PLAIN && !XREC && HB == 16),
                 "q8 tiles: plain GEMV only");
@@ -161,6 +168,7 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int WM = (k_t + TPW - 1) / TPW;   // waves per member (the launch gives G * WM)
   const int member = (G == 2 && wave >= WM) ? 1 : 0, chunk = wave - member * WM;
+  const bool own_x = !SHARE || member == 0;   // this wave loads its activations
   const int bi = blockIdx.x;
   // HB = 16: two workgroups per group (its row blocks); HB = 8: four (the halves of each
   // row block). A group's workgroups are 8 apart, so the dispatcher puts them on one XCD.
@@ -253,13 +261,17 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
         rml[u] = *(const float2*)((const char*)xin + (s * rs + ob));
       }
     } else if constexpr (NORM) {
-      hv[t] = *(const float4*)((const float*)xin + k);
-      nv[t] = *(const uint2*)(norm_w + k);
+      if (own_x) {
+        hv[t] = *(const float4*)((const float*)xin + k);
+        nv[t] = *(const uint2*)(norm_w + k);
+      }
     } else {
       xv[t] = *(const uint2*)((const uint16_t*)xin + k);
     }
   }
-  if constexpr (NORM) ssq_load<NSS>(ssq_in, lane, K / kSsqRows, sq);
+  if constexpr (NORM) {
+    if (own_x) ssq_load<NSS>(ssq_in, lane, K / kSsqRows, sq);
+  }
   // the epilogue's own inputs (thread r < 16 owns output row r of each member): the residual
   // (plain), the sequence position (q/k/v)
   const int er = tid & 15;
@@ -341,16 +353,18 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
     const float o2 = L > 0.f ? attn_div(A2, L) : 0.f, o3 = L > 0.f ? attn_div(A3, L) : 0.f;
     xr[0] = make_uint2(pack_bf16x2_op(o0, o1), pack_bf16x2_op(o2, o3));
   } else if constexpr (NORM) {
-    const float inv = rms_inv(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / kSsqRows)), K, a.eps);
+    if (own_x) {
+      const float inv = rms_inv(wave_sum(ssq_lane_sum<NSS>(sq, lane, K / kSsqRows)), K, a.eps);
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const float n0 = (hv[t].x * inv) * bf16lo(nv[t].x), n1 = (hv[t].y * inv) * bf16hi(nv[t].x);
-      const float n2 = (hv[t].z * inv) * bf16lo(nv[t].y), n3 = (hv[t].w * inv) * bf16hi(nv[t].y);
-      xr[t] = make_uint2(pack_bf16x2_op(n0, n1), pack_bf16x2_op(n2, n3));
-      // the stored row keeps NaN payloads as every bf16 output does
-      if (a.xn_out != nullptr && group == 0 && rb == 0 && member == 0 && kt0 + t < a.k_t)
-        *(uint2*)(a.xn_out + (kt0 + t) * kTileK + k0) =
-            make_uint2(pack_bf16x2(n0, n1), pack_bf16x2(n2, n3));
+      for (int t = 0; t < TPW; ++t) {
+        const float n0 = (hv[t].x * inv) * bf16lo(nv[t].x), n1 = (hv[t].y * inv) * bf16hi(nv[t].x);
+        const float n2 = (hv[t].z * inv) * bf16lo(nv[t].y), n3 = (hv[t].w * inv) * bf16hi(nv[t].y);
+        xr[t] = make_uint2(pack_bf16x2_op(n0, n1), pack_bf16x2_op(n2, n3));
+        // the stored row keeps NaN payloads as every bf16 output does
+        if (a.xn_out != nullptr && group == 0 && rb == 0 && member == 0 && kt0 + t < a.k_t)
+          *(uint2*)(a.xn_out + (kt0 + t) * kTileK + k0) =
+              make_uint2(pack_bf16x2(n0, n1), pack_bf16x2(n2, n3));
+      }
     }
   } else {
 #pragma unroll
@@ -370,42 +384,65 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
   // |x| is taken on the bf16 bits: its exponent field E bounds it by 2^(E - 126), and
   // se = 141 - E brings it under 2^15, inside fp16's range. (A wave's clamped duplicate of
   // the last K-tile repeats values the wave already holds, so it never changes the max.)
-  uint32_t am = 0;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const uint32_t u = xr[t].x, v = xr[t].y;
-    am = max(am, max(max(__builtin_amdgcn_ubfe(u, 0, 15), __builtin_amdgcn_ubfe(u, 16, 15)),
-                     max(__builtin_amdgcn_ubfe(v, 0, 15), __builtin_amdgcn_ubfe(v, 16, 15))));
-  }
-  am = max(am, dpp_u<kDppXor1>(am));
-  am = max(am, dpp_u<kDppXor2>(am));
-  am = max(am, dpp_u<kDppHalfMirror>(am));
-  const int se = min(141 - (int)(am >> 7), 120);   // zero / subnormal groups: 2^120
-  const float xs = __uint_as_float((uint32_t)(se + 127) << 23);
+  int se = 0;
   uint32_t xp[TPW][2];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    half2_t h;
-    h.x = (_Float16)(bf16lo(xr[t].x) * xs);
-    h.y = (_Float16)(bf16hi(xr[t].x) * xs);
-    xp[t][0] = h2_bits(h);
-    h.x = (_Float16)(bf16lo(xr[t].y) * xs);
-    h.y = (_Float16)(bf16hi(xr[t].y) * xs);
-    xp[t][1] = h2_bits(h);
-  }
-
-  // sum of the K-group's x (the minimum's factor) per tile, with the activation scale undone
-  const int ur = 20 - se, ux = -se;
   float Xs[TPW];
+  if (own_x) {
+    uint32_t am = 0;
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    float X = dot2_0(xp[t][0], 0x3C003C00u);
-    X = dot2(xp[t][1], 0x3C003C00u, X);
-    X += dpp<kDppHalfMirror>(X);
-    X += dpp<kDppXor2>(X);
-    X += dpp<kDppXor1>(X);
-    Xs[t] = __builtin_amdgcn_ldexpf(X, ux);
+    for (int t = 0; t < TPW; ++t) {
+      const uint32_t u = xr[t].x, v = xr[t].y;
+      am = max(am, max(max(__builtin_amdgcn_ubfe(u, 0, 15), __builtin_amdgcn_ubfe(u, 16, 15)),
+                       max(__builtin_amdgcn_ubfe(v, 0, 15), __builtin_amdgcn_ubfe(v, 16, 15))));
+    }
+    am = max(am, dpp_u<kDppXor1>(am));
+    am = max(am, dpp_u<kDppXor2>(am));
+    am = max(am, dpp_u<kDppHalfMirror>(am));
+    se = min(141 - (int)(am >> 7), 120);   // zero / subnormal groups: 2^120
+    const float xs = __uint_as_float((uint32_t)(se + 127) << 23);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      half2_t h;
+      h.x = (_Float16)(bf16lo(xr[t].x) * xs);
+      h.y = (_Float16)(bf16hi(xr[t].x) * xs);
+      xp[t][0] = h2_bits(h);
+      h.x = (_Float16)(bf16lo(xr[t].y) * xs);
+      h.y = (_Float16)(bf16hi(xr[t].y) * xs);
+      xp[t][1] = h2_bits(h);
+    }
+    // sum of the K-group's x (the minimum's factor) per tile, with the activation scale undone
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      float X = dot2_0(xp[t][0], 0x3C003C00u);
+      X = dot2(xp[t][1], 0x3C003C00u, X);
+      X += dpp<kDppHalfMirror>(X);
+      X += dpp<kDppXor2>(X);
+      X += dpp<kDppXor1>(X);
+      Xs[t] = __builtin_amdgcn_ldexpf(X, -se);
+    }
   }
+  if constexpr (SHARE) {   // member 0's chunk hands its converted activations to member 1's
+    if (member == 0) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        xsh[chunk][3 * t][lane] = xp[t][0];
+        xsh[chunk][3 * t + 1][lane] = xp[t][1];
+        xsh[chunk][3 * t + 2][lane] = __float_as_uint(Xs[t]);
+      }
+      xsh[chunk][3 * TPW][lane] = (uint32_t)se;
+    }
+    __syncthreads();
+    if (member == 1) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        xp[t][0] = xsh[chunk][3 * t][lane];
+        xp[t][1] = xsh[chunk][3 * t + 1][lane];
+        Xs[t] = __uint_as_float(xsh[chunk][3 * t + 2][lane]);
+      }
+      se = (int)xsh[chunk][3 * TPW][lane];
+    }
+  }
+  const int ur = 20 - se;
   uint32_t sl[4];   // v_perm selectors of the lane's byte slots
 #pragma unroll
   for (int j = 0; j < 4; ++j) sl[j] = sel_pair(j ^ gsw);
