@@ -489,12 +489,14 @@ __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
     attn_mfma_load<NT>(kbase, vbase, start + R + wo, stop, j, g, kB, vB);
   MfmaLane st;
   {
-    const uint16_t* qrow = a.q + ((size_t)b * a.hq + kvh * G + (j < G ? j : 0)) * 64;
-    const u32x4_t z = {0u, 0u, 0u, 0u};
+    // the group's G heads through a buffer resource; a padded head's lanes (j >= G) read
+    // outside it: zero rows, with no memory access
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + ((size_t)b * a.hq + kvh * G) * 64, G * 128);
+    const uint32_t qo = j < G ? (uint32_t)(j * 128 + 16 * g) : 0x80000000u;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const u32x4_t v = *(const u32x4_t*)(qrow + 32 * c + 8 * g);
-      st.q[c] = j < G ? v : z;   // padded heads: zero rows
+      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(qo + 64 * c), 0, 0);
+      st.q[c] = u32x4_t{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
     }
   }
   st.m = -INFINITY;
