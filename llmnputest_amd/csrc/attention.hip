@@ -363,13 +363,35 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 }
 
 // K rows (tile t, dims half c) and the 8-byte V pieces of one wave's 32 positions from p0;
-// positions at or past `stop` read row 0 instead (masked later). NT: streaming (non-temporal)
-// loads, for launches whose K/V is too large to stay in the caches.
+// positions at or past `stop` read zeros (cached loads: outside a buffer resource over the
+// rows before stop, no memory access; batched decode +0.4 %) or row 0 (NT), masked later.
+// NT: streaming (non-temporal) loads, for launches whose K/V is too large to stay in the
+// caches.
 template <bool NT>
 __device__ __forceinline__ void attn_mfma_load(const uint16_t* kbase, const uint16_t* vbase,
                                                int p0, int stop, int j, int g,
                                                u32x4_t (&kr)[4], uint2 (&vr)[8]) {
   typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+  if constexpr (!NT) {
+    const __amdgpu_buffer_rsrc_t kr_ = make_rsrc(kbase, (uint32_t)stop * 128u);
+    const __amdgpu_buffer_rsrc_t vr_ = make_rsrc(vbase, (uint32_t)stop * 128u);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t o = (uint32_t)(p0 + 16 * t + j) * 128u + 16u * g;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(kr_, (int)(o + 64u * c), 0, 0);
+        kr[2 * t + c] = u32x4_t{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t o = (uint32_t)(p0 + 16 * (e >> 2) + 4 * g + (e & 3)) * 128u + 8u * j;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(vr_, (int)o, 0, 0);
+      vr[e] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int pos = p0 + 16 * t + j;
