@@ -134,18 +134,33 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
     if constexpr (RB) {
       constexpr int MC = GemmFmt<KIND>::kCodes, BC = GemmFmt<KIND>::kBlockCodes;
       ld_off[i] = o < MC ? o : MC + rb * BC + min(o - MC, BC - 16);
+      // q4: each 64-byte group of d (and of m) holds row block 0's 32 bytes, then block 1's
+      if (KIND == 4 && o < MC && ((l >> 1) & 1) != rb) ld_off[i] = -1;
     } else {
       ld_off[i] = o - ((KIND == 8 && i == NLD - 1 && l >= 32) ? 512 : 0);
     }
   }
 
+  // RB q4: the weights through buffer resources over the tile-rows, so the other row
+  // block's metadata (ld_off -1) reads out of range: zeros, no memory access
+  __amdgpu_buffer_rsrc_t wrs[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) wrs[r] = make_rsrc(wr[r], (uint32_t)(a.k_t * TB));
+  auto wload = [&](int r, size_t off, int i) -> u32x4_t {
+    if constexpr (RB && KIND == 4) {
+      const uint32_t o = ld_off[i] < 0 ? 0x80000000u : (uint32_t)(off + ld_off[i]);
+      const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs[r], (int)o, 0, 0);
+      return u32x4_t{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    } else {
+      return *(const u32x4_t*)(wr[r] + off + ld_off[i]);
+    }
+  };
   u32x4_t pf[RT][NLD];
   if (n_it > 0) {
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int i = 0; i < NLD; ++i)
-        pf[r][i] = *(const u32x4_t*)(wr[r] + (size_t)(kbeg + wk) * TB + ld_off[i]);
+      for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, (size_t)(kbeg + wk) * TB, i);
   }
 
   const uint16_t* xrow[MT];
@@ -188,7 +203,7 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) pf[r][i] = *(const u32x4_t*)(wr[r] + off + ld_off[i]);
+        for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, off, i);
     }
     asm volatile("" ::: "memory");
 
