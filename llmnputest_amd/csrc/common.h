@@ -252,8 +252,15 @@ __device__ __forceinline__ float wave_max(float v) {
 constexpr int kSsqRows = 16;   // entries per partial sum of squares
 template <int NQ>
 __device__ __forceinline__ void ssq_load(const float* row, int lane, int n, float4 (&q)[NQ]) {
+  // through a buffer resource over the row's n floats: lanes past its end read zeros with no
+  // memory access (and ssq_lane_sum leaves them out)
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(row, (uint32_t)n * 4u);
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) q[j] = *(const float4*)(row + min(4 * (lane + 64 * j), n - 4));
+  for (int j = 0; j < NQ; ++j) {
+    const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(r, 16 * (lane + 64 * j), 0, 0);
+    q[j] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z),
+                       __int_as_float(v.w));
+  }
 }
 template <int NQ>
 __device__ __forceinline__ float ssq_lane_sum(const float4 (&q)[NQ], int lane, int n) {
