@@ -601,6 +601,12 @@ static int auto_split(int batch, int hkv, int max_len, bool mfma) {
   const int by_len = (max_len + kAttnRound - 1) / kAttnRound;   // rounds per (b, kv head)
   const int bh = batch * hkv;
   if (mfma) {
+    // Up to two 8-wave rounds per (sequence, kv head) the whole length stays in one split:
+    // the split merge's hand-off costs more than the longer workgroup (swept over batch 1-8,
+    // L = 128-768, against every split count: L = 256 4.5 against 5.9 us, batch 8 at
+    // L = 512 6.84 against 7.13 us); at batch 1 and L = 512 four splits are still ahead
+    // (5.96 against 6.03 us), as they are everywhere past 512 positions.
+    if (by_len <= 3 || (by_len == 4 && bh >= 16)) return 1;
     // A split's rounds pipeline through its three K/V buffers, and each split adds a record
     // to the merge: a split per round while the whole launch is short, then two rounds per
     // split up to 16 splits, 16 splits up to 128 rounds, then a split per 8 rounds up to 32;
