@@ -670,6 +670,10 @@ int mfma_launch(int kind, int op, GemmArgs& a, int n_units, void* ws, size_t ws_
     pf_launch(kind, a, (uint8_t*)ws + pf_off, st);
     return check_launch(what);
   }
+  // one m-tile reads x through a buffer resource with 32-bit byte offsets
+  Q4NX_REQUIRE(p.mt != 1 || (int64_t)a.m_rows * a.x_stride * 2 < ((int64_t)1 << 31),
+               Q4NX_ERR_SHAPE, "%s: %d rows of x at a stride of %lld span 2 GiB or more", what,
+               a.m_rows, (long long)a.x_stride);
   a.ksplit = p.ksplit;
   a.kpp = p.kpp;
   if (p.ksplit > 1) {
