@@ -742,6 +742,9 @@ static int attn_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   Q4NX_REQUIRE(max_len >= 1 && kv_h_stride >= (int64_t)max_len * 64 && kv_h_stride % 8 == 0 &&
                    kv_b_stride >= (int64_t)n_kv_heads * kv_h_stride && kv_b_stride % 8 == 0,
                Q4NX_ERR_SHAPE, "%s: cache strides do not hold [Hkv][max_len][64]", what);
+  // a (sequence, kv head)'s rows are read with 32-bit byte offsets
+  Q4NX_REQUIRE(max_len < (1 << 24), Q4NX_ERR_SHAPE, "%s: max_len=%d beyond 2^24 positions", what,
+               max_len);
   AttnArgs a{};
   a.q = q;
   a.k = k_cache;
