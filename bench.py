@@ -701,9 +701,9 @@ def main() -> int:
             "cpu_baseline": dec_cpu,
         }
         if dec_cpu is not None and dec.get("cpu") is not None:
-            # the float64 checker's own rate on the same workload, kept apart: it is the
-            # oracle, not a CPU decoder
-            dec_cpu["float64_checker"] = dec["cpu"]
+            # the float64 oracle's own rate on the same workload, kept apart: it checks
+            # results and is not a CPU decoder
+            dec_cpu["float64_oracle"] = dec["cpu"]
     if dec8 is not None:
         line["decode_batched"] = {
             "workload": f"the same decode with {dec8['batch']} sequences per step (weights read "

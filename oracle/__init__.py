@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. Only `tests/`, `__graft_entry__.smoke()` and the
 `cpu_baseline` leg of `bench.py` may import anything under `oracle/`, and only as
-the checker or as the timed CPU baseline, never as the product path.
+the reference results or as the timed CPU baseline, never as the product path.
 
 Modules:
   q4nx_oracle    tile format, dequantisation and GEMV (tools/q4nx.py, lm_head.py,
