@@ -408,6 +408,8 @@ class GraniteDecoder:
         b = first.numel()
         if int(start.max()) + n_new > self.max_len:
             raise ValueError("max_len too small for this many new tokens")
+        if int(start.min()) < 0 or start.numel() != b:
+            raise ValueError("start positions must be >= 0, one per sequence")
         if b != self.max_batch:
             raise ValueError("generate() runs all max_batch sequences; size the decoder to them")
         if self.graph is None or self.graph_batch != b:

@@ -298,6 +298,24 @@ def test_two_decoders_keep_their_policies(dev):
     assert rel < REL and cos >= COS
 
 
+def test_decoder_rejects_positions_outside_the_cache(dev):
+    """step() and generate() refuse positions outside [0, max_len) on the host, before any
+    launch, and the decoder still steps correctly afterwards."""
+    cfg = GraniteConfig(n_layers=1)
+    w = GraniteWeights.synthetic(cfg, seed=61, device=dev)
+    dec = GraniteDecoder(w, max_batch=1, max_len=64, device=dev)
+    dec.seed_cache(32, seed=62)
+    ok = dec.step([5], [32]).clone()
+    for bad in ([-1], [64]):
+        with pytest.raises(ValueError):
+            dec.step([5], bad)
+    with pytest.raises(ValueError):
+        dec.generate([5], [-1], 2)
+    with pytest.raises(ValueError):
+        dec.generate([5], [63], 2)      # the second token would land at position 64
+    assert torch.equal(dec.step([5], [32]), ok)
+
+
 # ------------------------------------------------------------------ a real-layout file
 
 def test_decode_from_q4nx_file(dev, tmp_path):
