@@ -155,12 +155,54 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       return *(const u32x4_t*)(wr[r] + off + ld_off[i]);
     }
   };
+  // The epilogue's own inputs are requested ahead of the weight stream: the residual of each
+  // (row, output) this thread finishes (plain), the sequence positions and, once the weight
+  // loads are out, their cos/sin (q/k/v). Loaded in the epilogue they put one (two, the table
+  // read depending on the position) memory round trips after the last MFMA.
+  constexpr int EIT_P = (MB * NW + NT - 1) / NT;   // plain epilogue iterations per thread
+  constexpr int EIT_Q = (MB * TW + NT - 1) / NT;   // q/k/v epilogue iterations per thread
+  constexpr bool PF_RES = OP == GOP_PLAIN && EIT_P <= 2;
+  constexpr bool PF_POS = OP == GOP_QKV && EIT_Q <= 2;
+  float ep_res[PF_RES ? EIT_P : 1] = {};
+  int ep_pos[PF_POS ? EIT_Q : 1];
+  float ep_cs[PF_POS ? EIT_Q : 1] = {}, ep_sn[PF_POS ? EIT_Q : 1] = {};
+  if constexpr (PF_RES) {
+    if (a.residual != nullptr) {
+      const int64_t gn0 = (int64_t)(group * RT * 2 + rb) * 16;
+#pragma unroll
+      for (int i = 0; i < EIT_P; ++i) {
+        const int e = i * NT + tid, gm = mblk * MB + e / NW;
+        if (e < MB * NW && gm < a.m_rows) ep_res[i] = a.residual[gm * a.y_stride + gn0 + e % NW];
+      }
+    }
+  }
+  if constexpr (PF_POS) {
+#pragma unroll
+    for (int i = 0; i < EIT_Q; ++i) {
+      const int e = i * NT + tid, gm = mblk * MB + e / TW;
+      ep_pos[i] = e < MB * TW && gm < a.m_rows ? a.pos[gm] : -1;
+    }
+  }
+  asm volatile("" ::: "memory");
   u32x4_t pf[RT][NLD];
   if (n_it > 0) {
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, (size_t)(kbeg + wk) * TB, i);
+  }
+  asm volatile("" ::: "memory");
+  if constexpr (PF_POS) {
+    if (seg != 2) {
+#pragma unroll
+      for (int i = 0; i < EIT_Q; ++i) {
+        const int p = ep_pos[i], d = rb * 16 + (i * NT + tid) % TW;
+        if (p >= 0 && p < a.max_pos) {
+          ep_cs[i] = a.rope_tab[(int64_t)p * 64 + d];
+          ep_sn[i] = a.rope_tab[(int64_t)p * 64 + 32 + d];
+        }
+      }
+    }
   }
 
   const uint16_t* xrow[MT];
@@ -362,7 +404,8 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       float v = 0.f;
       if (live) {
         v = *outp(m, n);
-        if (a.residual != nullptr) v += a.residual[gm * a.y_stride + gn];
+        if constexpr (PF_RES) v += ep_res[e0 / NT];
+        else if (a.residual != nullptr) v += a.residual[gm * a.y_stride + gn];
         if (a.y != nullptr) a.y[gm * a.y_stride + gn] = v;
         if (a.argmax_keys != nullptr) atomicMax(&skey[m * NB + n / 16], argmax_key(v, (uint32_t)gn));
       }
@@ -410,15 +453,16 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       }
       const float x0 = bf16_to_f32(f32_to_bf16(r0));
       const float x1 = bf16_to_f32(f32_to_bf16(r1));
-      const int p = a.pos[gm];
+      const int it = (e - tid) / NT;
+      const int p = PF_POS ? ep_pos[PF_POS ? it : 0] : a.pos[gm];
       if (p < 0 || p >= a.max_pos) continue;
       if (seg == 2) {
         uint16_t* dst = a.v_cache + gm * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
         dst[d] = f32_to_bf16(x0);
         dst[32 + d] = f32_to_bf16(x1);
       } else {
-        const float cs = a.rope_tab[(int64_t)p * 64 + d];
-        const float sn = a.rope_tab[(int64_t)p * 64 + 32 + d];
+        const float cs = PF_POS ? ep_cs[PF_POS ? it : 0] : a.rope_tab[(int64_t)p * 64 + d];
+        const float sn = PF_POS ? ep_sn[PF_POS ? it : 0] : a.rope_tab[(int64_t)p * 64 + 32 + d];
         const float y0 = fmaf(x0, cs, -(x1 * sn));
         const float y1 = fmaf(x1, cs, x0 * sn);
         uint16_t* dst = seg == 0
