@@ -501,14 +501,11 @@ __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
   const uint16_t* vbase = a.v + head_off;
   const int wo = wave * 32;
 
-  // the first two rounds' K/V, q and the length all in flight together; three buffers, so
-  // that two rounds are in flight while one is computed (one wave per SIMD at long
-  // contexts: nothing else hides a round's latency)
-  u32x4_t kA[4], kB[4], kC[4];
-  uint2 vA[8], vB[8], vC[8];
-  attn_mfma_load<NT>(kbase, vbase, start + wo, stop, j, g, kA, vA);
-  if (stop - start > R)   // a second round exists (known before the length is)
-    attn_mfma_load<NT>(kbase, vbase, start + R + wo, stop, j, g, kB, vB);
+  // the length, q and the first two rounds' K/V all in flight together, in that order: the
+  // in-order load counter then lets round 1 start when its own K/V are in, not after round
+  // 2's; three buffers, so that two rounds are in flight while one is computed (one wave per
+  // SIMD at long contexts: nothing else hides a round's latency)
+  const int len_b = a.lens[b];
   MfmaLane st;
   {
     // the group's G heads through a buffer resource; a padded head's lanes (j >= G) read
@@ -521,11 +518,17 @@ __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
       st.q[c] = u32x4_t{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
     }
   }
+  asm volatile("" ::: "memory");
+  u32x4_t kA[4], kB[4], kC[4];
+  uint2 vA[8], vB[8], vC[8];
+  attn_mfma_load<NT>(kbase, vbase, start + wo, stop, j, g, kA, vA);
+  if (stop - start > R)   // a second round exists (known before the length is)
+    attn_mfma_load<NT>(kbase, vbase, start + R + wo, stop, j, g, kB, vB);
   st.m = -INFINITY;
   st.l = 0.f;
 #pragma unroll
   for (int u = 0; u < 4; ++u) st.o[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int end = min(stop, max(0, a.lens[b]));
+  const int end = min(stop, max(0, len_b));
   const int nr = end > start ? (end - start + R - 1) / R : 0;
   if constexpr (NW > 8) {
     // launched only for splits of at most two rounds (launch_attn), both in flight from the
