@@ -282,7 +282,11 @@ __global__ __launch_bounds__(1024) void gemv1_kernel(Gemv1Args a) {
                                             : (const float*)w0;
     ep_res = *rp;
   }
-  if constexpr (OP == G1_QKV) ep_pos = *posp;
+  // The position is one word for the whole workgroup: read through the scalar path. As a
+  // vector load the compiler made it scalar with a readfirstlane placed before the barrier
+  // below, whose wait (the in-order vector load counter) then held the weight stream back
+  // until every activation load had arrived.
+  if constexpr (OP == G1_QKV) ep_pos = *(const __attribute__((address_space(4))) int32_t*)posp;
   // The vector L1 returns a wave's loads in issue order, so a small activation load queued
   // behind other waves' weight misses waits for them. Every wave of the workgroup issues its
   // activation loads before any issues a weight load (an execution barrier only: nothing
