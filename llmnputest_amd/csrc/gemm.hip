@@ -165,6 +165,7 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
   constexpr bool PF_POS = OP == GOP_QKV && EIT_Q <= 2;
   float ep_res[PF_RES ? EIT_P : 1] = {};
   int ep_pos[PF_POS ? EIT_Q : 1];
+  bool ep_live[PF_POS ? EIT_Q : 1];
   float ep_cs[PF_POS ? EIT_Q : 1] = {}, ep_sn[PF_POS ? EIT_Q : 1] = {};
   if constexpr (PF_RES) {
     if (a.residual != nullptr) {
@@ -180,23 +181,29 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < EIT_Q; ++i) {
       const int e = i * NT + tid, gm = mblk * MB + e / TW;
-      ep_pos[i] = e < MB * TW && gm < a.m_rows ? a.pos[gm] : -1;
+      // every lane loads (a clamped row): no branch around the load and nothing computed
+      // from it here, so the wait for it below counts exactly the weight loads after it
+      ep_pos[i] = a.pos[min(gm, a.m_rows - 1)];
+      ep_live[i] = e < MB * TW && gm < a.m_rows;
     }
   }
   asm volatile("" ::: "memory");
+  // the first tile's weights; for q/k/v also in a wave with no tile (a clamped tile, never
+  // used), so that no branch makes the compiler's count for the cos/sin loads below fall
+  // back to waiting for every load
   u32x4_t pf[RT][NLD];
-  if (n_it > 0) {
+  if (PF_POS || n_it > 0) {
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, (size_t)(kbeg + wk) * TB, i);
+      for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, (size_t)(PF_POS ? min(kbeg + wk, a.k_t - 1) : kbeg + wk) * TB, i);
   }
   asm volatile("" ::: "memory");
   if constexpr (PF_POS) {
     if (seg != 2) {
 #pragma unroll
       for (int i = 0; i < EIT_Q; ++i) {
-        const int p = ep_pos[i], d = rb * 16 + (i * NT + tid) % TW;
+        const int p = ep_live[i] ? ep_pos[i] : -1, d = rb * 16 + (i * NT + tid) % TW;
         if (p >= 0 && p < a.max_pos) {
           ep_cs[i] = a.rope_tab[(int64_t)p * 64 + d];
           ep_sn[i] = a.rope_tab[(int64_t)p * 64 + 32 + d];
@@ -454,7 +461,7 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       const float x0 = bf16_to_f32(f32_to_bf16(r0));
       const float x1 = bf16_to_f32(f32_to_bf16(r1));
       const int it = (e - tid) / NT;
-      const int p = PF_POS ? ep_pos[PF_POS ? it : 0] : a.pos[gm];
+      const int p = PF_POS ? ep_pos[PF_POS ? it : 0] : a.pos[gm];   // gm < m_rows here
       if (p < 0 || p >= a.max_pos) continue;
       if (seg == 2) {
         uint16_t* dst = a.v_cache + gm * a.kv_b_stride + hg * a.kv_h_stride + (int64_t)p * 64;
