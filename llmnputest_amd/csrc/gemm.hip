@@ -188,16 +188,48 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
     }
   }
   asm volatile("" ::: "memory");
-  // the first tile's weights; for q/k/v also in a wave with no tile (a clamped tile, never
-  // used), so that no branch makes the compiler's count for the cos/sin loads below fall
-  // back to waiting for every load
-  u32x4_t pf[RT][NLD];
-  if (PF_POS || n_it > 0) {
+  const uint16_t* xrow[MT];
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, (size_t)(PF_POS ? min(kbeg + wk, a.k_t - 1) : kbeg + wk) * TB, i);
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(m0 + 16 * mt + c, a.m_rows - 1);
+    xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
   }
+  // One m-tile (at most 16 rows): the operand rows past the batch load through a buffer
+  // resource over the batch's rows at an offset outside it, which returns zeros without a
+  // memory access, instead of re-reading the last row (batch-8 decode 3909 -> 3943 tok/s;
+  // a branch around those lanes' loads measured slower). Their outputs are never stored.
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((int64_t)a.m_rows * a.x_stride * 2));
+  const uint32_t xoff = m0 + c < a.m_rows ? (uint32_t)(((int64_t)(m0 + c) * a.x_stride + 8 * s) * 2)
+                                          : 0x80000000u;
+  u32x4_t xa[8][MT];
+  auto xload = [&](int kt) {
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (MT == 1) {
+          const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(
+              xrs, (int)(xoff + (uint32_t)(kt * 512 + kb * 64)), 0, 0);
+          xa[kb][mt] = u32x4_t{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+        } else {
+          xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
+        }
+      }
+  };
+  // the first tile's weights, also in a wave with no tile (a clamped tile, never used): no
+  // branch around the first loads, so the compiler's counts for the waits below stay exact
+  // (after a branch they fall back to waiting for every load)
+  u32x4_t pf[RT][NLD];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) pf[r][i] = wload(r, (size_t)min(kbeg + wk, a.k_t - 1) * TB, i);
+  asm volatile("" ::: "memory");
+  // One m-tile: the first tile's activations right behind its weights, so that they are in
+  // flight while the wave waits for the weights (issued after the tile's LDS store, their
+  // latency followed the weights' in every one-tile wave, which is every wave of a decode
+  // batch's launches; issued ahead of the weights they delayed the weight stream)
+  if (MT == 1) xload(kbeg + wk);   // unused in a wave with no tile (zeros past the rows)
   asm volatile("" ::: "memory");
   if constexpr (PF_POS) {
     if (seg != 2) {
@@ -212,19 +244,6 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
     }
   }
 
-  const uint16_t* xrow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = min(m0 + 16 * mt + c, a.m_rows - 1);
-    xrow[mt] = a.x + (int64_t)m * a.x_stride + 8 * s;
-  }
-  // One m-tile (at most 16 rows): the operand rows past the batch load through a buffer
-  // resource over the batch's rows at an offset outside it, which returns zeros without a
-  // memory access, instead of re-reading the last row (batch-8 decode 3909 -> 3943 tok/s;
-  // a branch around those lanes' loads measured slower). Their outputs are never stored.
-  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((int64_t)a.m_rows * a.x_stride * 2));
-  const uint32_t xoff = m0 + c < a.m_rows ? (uint32_t)(((int64_t)(m0 + c) * a.x_stride + 8 * s) * 2)
-                                          : 0x80000000u;
   for (int it = 0; it < n_it; ++it) {
     const int kt = kbeg + wk + it * WK;
 #pragma unroll
@@ -233,19 +252,7 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
       for (int i = 0; i < NLD; ++i) *(u32x4_t*)(slot + r * SLOT + 16 * (64 * i + l)) = pf[r][i];
     // activations of this tile first, then the next tile's weights: the in-order load
     // counter then lets the arithmetic start before the next tile arrives
-    u32x4_t xa[8][MT];
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if constexpr (MT == 1) {
-          const v4i_t v = __builtin_amdgcn_raw_buffer_load_b128(
-              xrs, (int)(xoff + (uint32_t)(kt * 512 + kb * 64)), 0, 0);
-          xa[kb][mt] = u32x4_t{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
-        } else {
-          xa[kb][mt] = *(const u32x4_t*)(xrow[mt] + kt * 256 + kb * 32);
-        }
-      }
+    if (MT != 1 || it > 0) xload(kt);
     asm volatile("" ::: "memory");
     if (it + 1 < n_it) {   // wave-uniform: a one-iteration wave issues no second tile
       const size_t off = (size_t)(kt + WK) * TB;
