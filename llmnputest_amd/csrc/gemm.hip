@@ -229,7 +229,8 @@ __global__ __launch_bounds__(64 * NWV) void gemm_kernel(GemmArgs a) {
   // flight while the wave waits for the weights (issued after the tile's LDS store, their
   // latency followed the weights' in every one-tile wave, which is every wave of a decode
   // batch's launches; issued ahead of the weights they delayed the weight stream)
-  if (MT == 1) xload(kbeg + wk);   // unused in a wave with no tile (zeros past the rows)
+  // (a wave with no tile loads bytes it never uses: inside the rows' buffer, or zeros past it)
+  if (MT == 1) xload(kbeg + wk);
   asm volatile("" ::: "memory");
   if constexpr (PF_POS) {
     if (seg != 2) {
