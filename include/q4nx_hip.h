@@ -196,7 +196,9 @@ int q4nx_swiglu(const void *g, const void *u, int in_f32, uint16_t *y, float *y_
 /* ---------------------------------------------------------------- fused groups
  * [q, k, v, RoPE] in one launch: q|k|v GEMVs over the same input, the q/k accumulators
  * narrowed to bf16 and rotated, v narrowed; q goes to q_out [batch][n_q*64], k and v
- * are written into the caches at positions[b]. Replaces the fused design
+ * are written into the caches at positions[b]; a row whose position lies outside
+ * [0, max_pos) writes neither its q nor the caches (raw_out still receives its GEMV outputs).
+ * Replaces the fused design
  * designs/granite_gemv/granite_qkv.py:50-128 with its epilogue granite_qkv_rope.h:74-78.
  * Input: bf16 x [batch][x_stride], or, when norm_w != NULL, the fp32 residual h
  * [batch][x_stride] normalised in the prologue (RMSNorm with norm_w, eps).

@@ -193,6 +193,50 @@ def test_qkv_rope(dev, vpath, batch, norm, ksplit):
         assert not kcn[b][:, mask].any() and not vcn[b][:, mask].any()   # nothing else written
 
 
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_qkv_rope_positions_outside_cache(dev, kpath, batch):
+    """A row whose position lies outside [0, max_pos) writes neither its q nor the caches (its
+    raw GEMV outputs are still written); every other row is bit for bit what the same launch
+    writes with all positions valid. Positions -1 and max_pos, on every kernel family."""
+    rng = np.random.default_rng(29)
+    hq, hkv, hid, lmax = 40, 8, 2560, 64
+    kt = hid // 256
+    d = lambda a: torch.from_numpy(a.reshape(-1)).to(dev)
+    wq = d(synth.q4_tiles(rng, hq * 64, hid))
+    wk = d(synth.q4_tiles(rng, hkv * 64, hid))
+    wv = d(synth.q4_tiles(rng, hkv * 64, hid))
+    x = bf16_dev(synth.random_bf16(rng, (batch, hid)), dev)
+    tab = ops.rope_table(lmax, 64, 10000.0)
+    good = rng.integers(0, lmax, batch).astype(np.int32)
+    bad = good.copy()
+    bad[0] = -1
+    if batch > 1:
+        bad[-1] = lmax
+    sentinel = 0x1234
+
+    def run(pos):
+        kc = torch.zeros((batch, hkv, lmax, 64), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        q = torch.full((batch, hq * 64), sentinel, dtype=torch.int16, device=dev).view(torch.bfloat16)
+        raw = torch.empty((batch, (hq + 2 * hkv) * 64), dtype=torch.float32, device=dev)
+        ops.qkv_rope(wq, wk, wv, hq, hkv, kt, x, torch.from_numpy(pos).to(dev), tab, kc, vc,
+                     q_out=q, raw_out=raw)
+        torch.cuda.synchronize()
+        return bits(q), bits(kc), bits(vc), raw.cpu().numpy()
+
+    q_g, k_g, v_g, raw_g = run(good)
+    q_b, k_b, v_b, raw_b = run(bad)
+    assert np.array_equal(raw_b, raw_g)
+    for b in range(batch):
+        if 0 <= bad[b] < lmax:
+            assert np.array_equal(q_b[b], q_g[b])
+            assert np.array_equal(k_b[b], k_g[b]) and np.array_equal(v_b[b], v_g[b])
+        else:
+            assert (q_b[b] == sentinel).all()
+            assert not k_b[b].any() and not v_b[b].any()
+            assert k_g[b].any()   # the valid launch did write this row
+
+
 @pytest.mark.parametrize("batch,ksplit", [(1, 0), (3, 0), (2, 1)], indirect=["ksplit"])
 def test_qkv_rope_ssq_in(dev, vpath, batch, ksplit):
     """The norm fed the producer's per-16 sums of squares gives the same normalised input
