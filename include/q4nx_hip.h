@@ -232,7 +232,8 @@ int q4nx_gate_up_swiglu(const uint8_t *wg, const uint8_t *wu, int n_tile_rows,
 
 /* ---------------------------------------------------------------- attention
  * GQA flash-decode: one query token per sequence, out[b][h] = softmax(scale * K q) V
- * over positions [0, lens[b]) of the caches, q head h reading kv head h / (Hq/Hkv).
+ * over positions [0, lens[b]) of the caches, q head h reading kv head h / (Hq/Hkv); a
+ * sequence with lens[b] <= 0 gets zeros, and lens[b] > max_len reads max_len positions.
  * Split-K over the KV length with an exact (m, l, acc) combine. Replaces
  * designs/granite_gemv/granite_attention.h:221-237 (granite_attn_block /
  * granite_attn_finish). head_dim must be 64. q: bf16 [B][Hq][64]; out: bf16 and/or fp32
