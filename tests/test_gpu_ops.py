@@ -421,6 +421,21 @@ def test_gqa_decode_split_edges_b8(dev, apath):
     assert_bf16_close(bits(out)[1:], ref)
 
 
+def test_gqa_decode_length_past_cache(dev, apath):
+    """A length beyond the cache reads the whole cache and no further: the same bits as the
+    length equal to max_len, at every split count."""
+    rng = np.random.default_rng(31)
+    L = 640
+    q = bf16_dev(synth.random_bf16(rng, (2, 40, 64)), dev)
+    k = bf16_dev(synth.random_bf16(rng, (2, 8, L, 64)), dev)
+    v = bf16_dev(synth.random_bf16(rng, (2, 8, L, 64)), dev)
+    for n_split in (0, 1, 3):
+        outs = [ops.gqa_decode(q, k, v, torch.tensor(lens, dtype=torch.int32, device=dev), 0.125,
+                               n_split=n_split, want_f32=True)[1].cpu().numpy()
+                for lens in ([L, L], [L + 1, 1 << 20])]
+        assert np.array_equal(outs[0], outs[1])
+
+
 def test_gqa_decode_garbage_past_length(dev, apath):
     """Cache rows at and past a sequence's length take no part in the result whatever they
     hold: K = +Inf and V = NaN bit patterns there leave the output equal to the oracle's on
