@@ -113,6 +113,38 @@ def test_mfma_gemv_ex_norm_ssq_keys(dev, mfma, kind, batch):
     assert tok.cpu().numpy().tolist() == np.argmax(y, axis=1).tolist()
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_gemv_ex_random_shapes_all_epilogues(dev, kpath, case):
+    """Seeded random shapes with every epilogue of the plain GEMV at once (RMSNorm prologue
+    from the producer's sums of squares, a residual added in place, the outputs' sums of
+    squares and argmax keys) on each kernel family: tile-row counts that do not fill a grid,
+    short and long K, batches up to 16 on the matrix cores (8 on the VALU kernels)."""
+    rng = np.random.default_rng(3100 + 7 * case)
+    kind = "q8" if case % 3 == 2 else "q4"
+    n_t = int(rng.integers(1, 120))
+    k_t = int(rng.choice([1, 2, 3, 5, 10, 13]))
+    batch = int(rng.integers(1, 17 if kpath == "mfma" else 9))
+    n, k = 32 * n_t, 256 * k_t
+    t = synth.q4_tiles(rng, n, k) if kind == "q4" else synth.q8_tiles(rng, n, k)
+    raw = t.reshape(-1, t.shape[-1])
+    w = torch.from_numpy(raw.reshape(-1)).to(dev)
+    hd, ss_in, nwd, x64 = normed_input(rng, batch, k, dev)
+    res = rng.standard_normal((batch, n)).astype(np.float32)
+    y = torch.from_numpy(res.copy()).to(dev)
+    ss_out = torch.empty((batch, n // 16), dtype=torch.float32, device=dev)
+    keys = torch.zeros((batch, n // 16), dtype=torch.int64, device=dev)
+    ops.gemv_ex(w, kind, hd, n_t, k_t, norm_w=nwd, eps=1e-5, residual=y, out=y, ssq_in=ss_in,
+                ssq_out=ss_out, argmax_keys=keys)
+    got = y.cpu().numpy()
+    assert_close_norm(got, raw, kind, x64, n_t, k_t, res)
+    sref = ssq16(got)
+    assert np.abs(ss_out.cpu().numpy() - sref).max() <= 1e-6 * sref.max()
+    z = lambda: torch.zeros(batch, dtype=torch.int32, device=dev)
+    tok = z()
+    ops.decode_advance(keys, n // 16, tok, z(), z(), torch.zeros(1, dtype=torch.int32, device=dev))
+    assert tok.cpu().numpy().tolist() == np.argmax(got, axis=1).tolist()
+
+
 @pytest.mark.parametrize("batch", [1, 3, 11, 20])
 def test_mfma_gemv_plain_keys_only(dev, mfma, batch):
     """argmax keys without an output vector (the decode step's lm_head form)."""
