@@ -502,8 +502,8 @@ __global__ __launch_bounds__(NW * 64) void gqa_mfma_kernel(AttnArgs a) {
   const int wo = wave * 32;
 
   // the length, q and the first two rounds' K/V all in flight together, in that order: the
-  // in-order load counter then lets round 1 start when its own K/V are in, not after round
-  // 2's; three buffers, so that two rounds are in flight while one is computed (one wave per
+  // in-order load counter then lets the first K/V round start when its own bytes are in, not
+  // after the second's; three buffers, so that two rounds are in flight while one is computed (one wave per
   // SIMD at long contexts: nothing else hides a round's latency)
   const int len_b = a.lens[b];
   MfmaLane st;
